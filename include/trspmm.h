@@ -1,0 +1,200 @@
+/* trspmm.h -- C ABI of the MI355X (gfx950) hybrid fp16 SpMM / SDDMM library (libtrspmm.so).
+ *
+ * Plain pointers and sizes only; no exceptions cross this boundary.  Every function returns a
+ * trs_status; on failure trs_last_error() describes the problem (thread-local).
+ *
+ * Object model
+ *   trs_format  host-side output of the format builder (the reference's 29-array tuple + spill).
+ *   trs_plan    device-resident, immutable execution plan.  Plans may be shared between threads;
+ *               calls on the same plan may run concurrently on different streams as long as each
+ *               call gets its own output buffer and workspace.
+ * Device pointers (B, C, X, Y, out, workspace) are caller-owned HIP device memory; `stream` is a
+ * hipStream_t (NULL = the default stream).  fp16 data is passed as uint16_t bit patterns.
+ */
+#ifndef TRSPMM_H
+#define TRSPMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum trs_status {
+  TRS_OK = 0,
+  TRS_EINVAL = 1,     /* bad argument: shape, dtype-size, range (reference: TORCH_CHECK -> RuntimeError) */
+  TRS_ENOMEM = 2,     /* host or device allocation failed */
+  TRS_EDEVICE = 3,    /* HIP runtime error (no GPU, launch failure, ...) */
+  TRS_ENOTCANON = 4,  /* CSR rows not strictly increasing: a plan cannot be built from it */
+  TRS_ERANGE = 5      /* index outside [0, rows) / [0, cols), or size beyond int32 addressing */
+} trs_status;
+
+/* ---------------------------------------------------------------------------------------------
+ * Format builder.
+ * Replaces Libra5BlockOnline.block_sptc_2to4_online
+ * (TR-source/Block/block_online.cpp:545-549 signature, :844-870 return list).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct trs_build_params {
+  int32_t part_size_t;       /* partSize_t: TC sub-blocks per part (32) */
+  int32_t part_size_c;       /* partSize_c: residual nnz per long part (32) */
+  int32_t short_size;        /* shortSize: residual rows with <= this nnz form short parts (3) */
+  int32_t density;           /* TC column threshold: nnz of a column inside a window (8) */
+  int32_t window;            /* rows per window, 1..32 (16) */
+  int32_t wide;              /* accepted and range-checked (1..32) only, as in the reference (16) */
+  float tc_min_util;         /* minimum fill of a 16x8 TC chunk (0.0) */
+  float sptc_min_util;       /* accepted, unused -- as in the reference (0.5) */
+  int32_t sptc_threshold;    /* accepted, unused -- as in the reference (12) */
+  int32_t skip_tc;           /* -1: read env LIBRA_SKIP_TC like the reference; 0 / 1 explicit */
+  int32_t sptc_unit_min_nnz; /* -1: read env LIBRA_SPTC_UNIT_MIN_NNZ (default 2); >= 0 explicit */
+  int32_t num_threads;       /* host threads; 0 = OpenMP default */
+} trs_build_params;
+
+void trs_build_params_default(trs_build_params* p);
+
+typedef struct trs_format trs_format;
+
+/* rowptr[rows+1], col[nnz], val[nnz] (float32) on the host.  Output arrays are bit-exact with the
+ * reference builder for any input; the spill list (slots 29-31) holds the entries the reference
+ * drops, so that tuple + spill reproduces the input exactly. */
+int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val, int32_t rows,
+                     int64_t nnz, const trs_build_params* params, trs_format** out);
+
+/* Slot 0..28: reference tuple order (t_rowkNew_offset ... s_window_tile_offset);
+ * slot 29/30/31: spill rows (int32) / columns (int32) / values (float32).
+ * Element types per slot: int32 except 3, 11, 16, 19, 31 (float32), 6 (int64), 18 (uint8),
+ * 20 (int8).  The data pointer stays valid until trs_format_free. */
+int trs_format_slot(const trs_format* f, int32_t slot, const void** data, int64_t* numel);
+double trs_format_elapsed(const trs_format* f);  /* reference slot 29: build wall time, s */
+int32_t trs_format_window(const trs_format* f);
+int32_t trs_format_rows(const trs_format* f);
+int32_t trs_format_canonical(const trs_format* f); /* 1 if every row had increasing columns */
+void trs_format_free(trs_format* f);
+
+/* ---------------------------------------------------------------------------------------------
+ * Plans.  A plan lowers format arrays to the device layout the kernels read (dense 16x16 fp16
+ * MFMA tiles + an fp16 CSR residual with load-balanced row tasks), validates every index on the
+ * host, and uploads once.  m = output rows (mOri), n = rows of the dense operand (kOri).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct trs_plan trs_plan;
+
+typedef struct trs_plan_options {
+  int32_t mfma_tc;        /* 1: TC sub-blocks run on MFMA tiles; 0: lowered to the CSR residual */
+  int32_t mfma_sptc;      /* 1: 2:4 group tiles whose fill >= sptc_min_fill run on MFMA */
+  float sptc_min_fill;    /* fill threshold (nnz / 256 slots of a 16x16 tile) for mfma_sptc */
+  int32_t task_nnz;       /* residual nnz per lane-group task (0 = automatic) */
+} trs_plan_options;
+
+void trs_plan_options_default(trs_plan_options* o);
+
+/* Full-accuracy plan from the builder output: TC + 2:4 groups + residual + spill == input.
+ * Replaces the device half of Libra6SpMMOnline.forward_fp16_tcu_cuda_sptc_mma_parallel_online
+ * (TR-source/SpMM/mGCN_online.cpp:760-1138) for callers that keep the trs_format. */
+int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt,
+                    trs_plan** out);
+
+/* Plan from the host arrays the reference parallel operator receives
+ * (mGCN_online.cpp:760-800; t_value / c_value are fp16 bits, s_value float32, t_binary int64).
+ * The result is the SpMM of exactly what those arrays carry (no spill).  spill_* may be NULL
+ * (spill_count 0); when given, the plan also carries those entries. */
+typedef struct trs_parallel_arrays {
+  const int32_t* t_row_offset; int64_t n_t_row_offset;
+  const int32_t* t_block_offset; int64_t n_t_block_offset;
+  const int32_t* t_column; int64_t n_t_column;
+  const uint16_t* t_value; int64_t n_t_value;
+  const int32_t* t_window_row; int64_t n_t_window_row;
+  const int32_t* t_atomic; int64_t n_t_atomic;
+  const int64_t* t_binary; int64_t n_t_binary;
+  const int32_t* c_row_offsets; int64_t n_c_row_offsets;
+  const int32_t* c_row; int64_t n_c_row;
+  const int32_t* c_atomic; int64_t n_c_atomic;
+  const int32_t* c_column; int64_t n_c_column;
+  const uint16_t* c_value; int64_t n_c_value;
+  const int32_t* cs_row_offsets; int64_t n_cs_row_offsets;
+  const int32_t* cs_row; int64_t n_cs_row;
+  const int32_t* cs_atomic; int64_t n_cs_atomic;
+  const int32_t* cs_column; int64_t n_cs_column;
+  const uint16_t* cs_value; int64_t n_cs_value;
+  const int32_t* s_column; const float* s_value; const int8_t* s_pos; int64_t groups;
+  const int32_t* s_offsets; int64_t n_s_offsets;          /* windows + 1 */
+  const int32_t* s_tile_column; const int32_t* s_packed_a; const int32_t* s_packed_meta;
+  const int32_t* s_window_tile_offset; int64_t tiles; int64_t n_s_window_tile_offset;
+  int32_t use_packed_tiles;  /* 1: 2:4 share from packed tiles (as the reference parallel kernel);
+                                0: from s_column/s_value/s_pos */
+  const int32_t* spill_row; const int32_t* spill_col; const float* spill_val; int64_t spill_count;
+  int32_t parts_t, parts_c, partsize_c, parts_c_short, window, m, n;
+} trs_parallel_arrays;
+
+int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_options* opt, trs_plan** out);
+
+/* 2:4-group-only plans.
+ * Replaces forward_fp16_sptc_online (s_window rows, mGCN_online.cpp:202-400) when s_window != NULL,
+ * and forward_fp16_sptc_mma_online (window from s_offsets, mGCN_online.cpp:404-650) otherwise. */
+int trs_plan_create_sptc(const int32_t* s_column, const float* s_value, const int8_t* s_pos,
+                         int64_t groups, const int32_t* s_window, const int32_t* s_offsets,
+                         int64_t n_s_offsets, int32_t window, int32_t m, int32_t n,
+                         const trs_plan_options* opt, trs_plan** out);
+
+/* Replaces forward_fp16_sptc_mma_packed_online (mGCN_online.cpp:654-757). */
+int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_packed_a,
+                                const int32_t* s_packed_meta, const int32_t* s_window_tile_offset,
+                                int64_t tiles, int64_t n_s_window_tile_offset, int32_t window,
+                                int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out);
+
+/* Plain CSR plan (fp16 values): the pattern an SDDMM samples, or a pure-residual SpMM.
+ * No reference counterpart (the reference has no SDDMM). */
+int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_t* val,
+                        int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out);
+
+typedef struct trs_plan_stats {
+  int64_t m, n, nnz;                 /* nnz carried by the plan (all shares) */
+  int64_t mfma_tiles, mfma_nnz;      /* 16x16 tiles on MFMA and the nonzeros inside them */
+  int64_t csr_nnz;                   /* residual nonzeros */
+  int64_t tasks, split_rows, partial_slots;
+  int64_t device_bytes;              /* plan footprint in HBM */
+  int64_t mfma_windows;              /* 16-row windows owned by the MFMA window kernel */
+  int64_t window_csr_nnz;            /* residual nonzeros inside those windows */
+} trs_plan_stats;
+
+int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s);
+void trs_plan_free(trs_plan* p);
+
+/* ---------------------------------------------------------------------------------------------
+ * Execution.
+ * ------------------------------------------------------------------------------------------- */
+/* Bytes of device workspace trs_spmm_f16 needs for feature width K (0 when none). */
+int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K);
+
+/* C[m, K] (float32, row stride ldc) = A_plan (m x n) * B[n, K] (fp16, row stride ldb).
+ * Every element of C is written exactly once per call (no prior zeroing needed, no atomics).
+ * fp16 products, fp32 accumulation. */
+int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[e] = sum_k X[row_e, k] * Y[col_e, k] for every stored entry e of the plan, in the plan's CSR
+ * order (row-major, columns ascending).  X [m, K], Y [n, K] fp16; out float32 [nnz].
+ * Only plans from trs_plan_create_csr are accepted. */
+int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                  int32_t K, float* out, void* stream);
+
+/* Launch-by-launch timing helper for the reference operators' `epoches` semantics
+ * (mGCNkernel_online.cu:1604-1712): `warmup` untimed calls, then `iters` timed calls bracketed by
+ * HIP events on `stream`; *ms_avg = mean time per call.  C holds the result of the last call. */
+int trs_spmm_f16_timed(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C,
+                       int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream,
+                       int32_t warmup, int32_t iters, float* ms_avg);
+
+/* Per-kernel durations for profiling: `iters` calls, each of the (up to) three kernels of a call
+ * bracketed by HIP events on `stream`.  ms[0] = residual task kernel, ms[1] = MFMA window kernel,
+ * ms[2] = split-row fixup kernel; averages per call, 0 for a kernel the plan does not launch.
+ * No reference counterpart (the reference reports per-stream completion times instead,
+ * mGCNkernel_online.cu:1676-1687). */
+int trs_spmm_f16_kernel_ms(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C,
+                           int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream,
+                           int32_t iters, float* ms);
+
+const char* trs_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRSPMM_H */

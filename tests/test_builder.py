@@ -1,0 +1,156 @@
+"""Product format builder (libtrspmm.so, C ABI and the Libra5BlockOnline drop-in) against the
+reference fixtures and the literal oracle; spill equality; parameter / error behaviour."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_files, load_golden, same_array
+from oracle import builder as ob
+from trspmm import graphs
+import trspmm
+
+
+def product_build(rowptr, col, val, params, **kw):
+    f = trspmm.build_format(rowptr, col, val, part_t=params["part_t"], part_c=params["part_c"],
+                            short_size=params["short_size"], density=params["density"], window=params["window"],
+                            tc_min_util=params["tc_min_util"], **kw)
+    return f.arrays(), f.spill(), f
+
+
+@pytest.mark.parametrize("path", golden_files(), ids=lambda p: os.path.basename(p)[8:-4])
+def test_product_matches_reference_fixture(path, golden_env):
+    rowptr, col, val, params, env, outs = load_golden(path)
+    golden_env(env)
+    arrs, _, _ = product_build(rowptr, col, val, params)
+    bad = [ob.SLOTS[i][0] for i in range(29) if not same_array(arrs[i], outs[i])]
+    assert not bad, f"arrays differing from the reference: {bad}"
+
+
+@pytest.mark.parametrize("path", golden_files(), ids=lambda p: os.path.basename(p)[8:-4])
+def test_dropin_module_matches_reference_fixture(path, golden_env):
+    import Libra5BlockOnline as L5
+    rowptr, col, val, p, env, outs = load_golden(path)
+    golden_env(env)
+    res = L5.block_sptc_2to4_online(torch.from_numpy(rowptr), torch.from_numpy(col), torch.from_numpy(val),
+                                    p["part_t"], p["part_c"], p["short_size"], p["density"], p["window"], 16,
+                                    float(p["tc_min_util"]), 0.5, 12)
+    assert len(res) == 30
+    assert res[29].dim() == 0 and res[29].dtype == torch.float32 and float(res[29]) >= 0
+    for i in range(29):
+        assert same_array(res[i].numpy(), outs[i]), ob.SLOTS[i][0]
+
+
+CASES = [
+    ("rand_dense", lambda: graphs.random_csr(400, 300, 0.2, seed=1), {}),
+    ("rand_sparse", lambda: graphs.random_csr(700, 2000, 0.004, seed=2), {}),
+    ("rmat12", lambda: graphs.rmat(scale=12, edge_factor=8, seed=7), {}),
+    ("sbm256", lambda: graphs.sbm(communities=256, seed=8, val_seed=9), {}),
+    ("grid96", lambda: graphs.grid_hubs(side=96, hubs=3, hub_degree=3000, seed=1, val_seed=2), {}),
+    ("w4", lambda: graphs.random_csr(300, 200, 0.1, seed=3, window=4), dict(window=4, density=2)),
+    ("w24", lambda: graphs.random_csr(240, 100, 0.2, seed=4, window=24), dict(window=24, density=10)),
+    ("params", lambda: graphs.random_csr(333, 150, 0.3, seed=5), dict(part_t=3, part_c=7, short_size=1,
+                                                                      density=4, tc_min_util=0.3)),
+]
+DEFAULT = dict(part_t=32, part_c=32, short_size=3, density=8, window=16, tc_min_util=0.0)
+
+
+@pytest.mark.parametrize("name,gen,over", CASES, ids=[c[0] for c in CASES])
+def test_product_matches_oracle(name, gen, over, golden_env):
+    golden_env({})
+    g = gen()
+    p = dict(DEFAULT, **over)
+    arrs, spill, f = product_build(g.rowptr, g.col, g.val, p)
+    o_arrs, o_spill = ob.build(g.rowptr, g.col, g.val, **p)
+    for i in range(29):
+        assert same_array(arrs[i], o_arrs[i]), ob.SLOTS[i][0]
+    for a, b in zip(spill, o_spill):
+        assert same_array(a, b)
+    assert f.canonical
+
+
+def test_noncanonical_input_bit_exact_and_flagged(golden_env):
+    golden_env({})
+    rng = np.random.default_rng(3)
+    counts = rng.integers(0, 25, size=64)
+    rowptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    col = rng.integers(0, 30, size=rowptr[-1]).astype(np.int32)
+    val = rng.standard_normal(rowptr[-1]).astype(np.float32)
+    p = dict(DEFAULT, density=3)
+    arrs, spill, f = product_build(rowptr, col, val, p)
+    o_arrs, o_spill = ob.build(rowptr, col, val, **p)
+    for i in range(29):
+        assert same_array(arrs[i], o_arrs[i]), ob.SLOTS[i][0]
+    for a, b in zip(spill, o_spill):
+        assert same_array(a, b)
+    assert not f.canonical
+
+
+def test_thread_count_does_not_change_output(golden_env):
+    golden_env({})
+    g = graphs.rmat(scale=11, edge_factor=8, seed=9)
+    a1 = trspmm.build_format(g.rowptr, g.col, g.val, num_threads=1)
+    a8 = trspmm.build_format(g.rowptr, g.col, g.val, num_threads=8)
+    for i in range(32):
+        assert same_array(a1.slot(i), a8.slot(i))
+
+
+def test_env_controls_like_reference(golden_env):
+    g = graphs.sbm(communities=32, seed=1, val_seed=2)
+    golden_env({"LIBRA_SKIP_TC": "true"})
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    assert f.slot(3).size == 0            # no TC values
+    golden_env({"LIBRA_SKIP_TC": "yes"})  # only "1" / "true" / "TRUE" enable (block_online.cpp:118-122)
+    assert trspmm.build_format(g.rowptr, g.col, g.val).slot(3).size > 0
+    golden_env({"LIBRA_SPTC_UNIT_MIN_NNZ": "100"})
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    assert f.slot(21).size <= f.slot(17).size // 4  # unmatched units all fall to the residual
+
+
+def test_empty_and_degenerate_inputs(golden_env):
+    golden_env({})
+    f = trspmm.build_format(np.zeros(1, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+    a = f.arrays()
+    assert a[22].tolist() == [0] and a[28].tolist() == [0] and a[0].tolist() == [0]
+    f = trspmm.build_format(np.zeros(17, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+    assert f.arrays()[22].tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("kw,msg", [(dict(window=0), "window"), (dict(window=33), "window"), (dict(wide=0), "wide"),
+                                    (dict(wide=33), "wide")])
+def test_builder_parameter_errors(kw, msg):
+    g = graphs.random_csr(32, 32, 0.1, seed=0)
+    with pytest.raises(RuntimeError, match=msg):
+        trspmm.build_format(g.rowptr, g.col, g.val, **kw)
+
+
+def test_builder_csr_errors():
+    with pytest.raises(RuntimeError, match="rowptr"):
+        trspmm.build_format(np.array([1, 2], np.int32), np.array([0, 1], np.int32), np.ones(2, np.float32))
+    with pytest.raises(RuntimeError, match="negative column"):
+        trspmm.build_format(np.array([0, 1], np.int32), np.array([-3], np.int32), np.ones(1, np.float32))
+
+
+def test_dropin_argument_errors():
+    import Libra5BlockOnline as L5
+    r = torch.tensor([0, 1], dtype=torch.int32)
+    c = torch.tensor([0], dtype=torch.int32)
+    v = torch.tensor([1.0])
+    with pytest.raises(RuntimeError):
+        L5.block_sptc_2to4_online(r.long(), c, v, 32, 32, 3, 8, 16, 16, 0.0, 0.5, 12)
+    with pytest.raises(RuntimeError):
+        L5.block_sptc_2to4_online(r, c, v.double(), 32, 32, 3, 8, 16, 16, 0.0, 0.5, 12)
+    with pytest.raises(RuntimeError):
+        L5.block_sptc_2to4_online(r, c, v, 32, 32, 3, 8, 40, 16, 0.0, 0.5, 12)
+    with pytest.raises(TypeError):
+        L5.block_sptc_2to4_online(r, c, v, 32.5, 32, 3, 8, 16, 16, 0.0, 0.5, 12)
+    out = L5.block_sptc_2to4_online_with_spill(r, c, v, 32, 32, 3, 8, 16, 16, 0, 0.5, 12)
+    assert len(out) == 33
+
+
+def test_dropin_module_is_the_product():
+    import Libra5BlockOnline as L5
+    import Libra6SpMMOnline as L6
+    assert "tr-spmm_zzx_amd" in L5.__file__ and "tr-spmm_zzx_amd" in L6.__file__
+    assert hasattr(L5, "block_sptc_2to4_online_with_spill")

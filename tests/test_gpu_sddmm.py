@@ -1,0 +1,55 @@
+"""GPU parity of SDDMM (no reference counterpart; closed form out[e] = X[row_e] . Y[col_e])."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmm as osp
+from trspmm import graphs
+import trspmm
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("K", [1, 7, 32, 64, 128, 256, 600])
+def test_sddmm_matches_closed_form(K):
+    print("sddmm K", K, flush=True)
+    g = graphs.rmat(scale=12, edge_factor=16, seed=4)
+    plan = trspmm.Plan.from_csr(g.rowptr, g.col, g.val.astype(np.float16), g.m, g.n)
+    Xh = graphs.dense_operand(g.m, K, seed=4)
+    Yh = graphs.dense_operand(g.n, K, seed=5)
+    out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda())
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    got = out.cpu().numpy()
+    assert got.shape == R.shape
+    # per-entry dot of K fp16 products, fp32 accumulation
+    tol = 1e-5 * np.sqrt(K) * 4 + 1e-6
+    assert np.max(np.abs(got - R)) <= tol * max(1.0, np.max(np.abs(R))), np.max(np.abs(got - R))
+
+
+def test_sddmm_long_rows_and_empty_rows():
+    rng = np.random.default_rng(1)
+    m, n = 48, 50000
+    degs = np.array([30000 if r == 5 else (0 if r % 3 == 0 else 4) for r in range(m)])
+    cols = np.concatenate([np.sort(rng.choice(n, size=d, replace=False)) for d in degs]).astype(np.int32)
+    rowptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+    plan = trspmm.Plan.from_csr(rowptr, cols, np.ones(len(cols), np.float16), m, n)
+    Xh = graphs.dense_operand(m, 64, seed=1)
+    Yh = graphs.dense_operand(n, 64, seed=2)
+    out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda())
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(rowptr, cols, Xh, Yh)
+    assert np.max(np.abs(out.cpu().numpy() - R)) < 1e-3
+
+
+def test_sddmm_matches_torch_sampled_addmm():
+    g = graphs.random_csr(200, 300, 0.05, seed=3)
+    plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)
+    Xh = graphs.dense_operand(g.m, 48, seed=1)
+    Yh = graphs.dense_operand(g.n, 48, seed=2)
+    out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()).cpu().numpy()
+    nnz = int(g.rowptr[g.m])
+    A = torch.sparse_csr_tensor(torch.from_numpy(g.rowptr[: g.m + 1].astype(np.int64)),
+                                torch.from_numpy(g.col[:nnz].astype(np.int64)), torch.ones(nnz), size=(g.m, g.n))
+    ref = torch.sparse.sampled_addmm(A, torch.from_numpy(Xh).float(), torch.from_numpy(Yh).float().T, beta=0.0)
+    assert np.allclose(out, ref.values().numpy(), atol=1e-4)

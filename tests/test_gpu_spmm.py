@@ -1,0 +1,164 @@
+"""GPU parity: hybrid fp16 SpMM through libtrspmm.so against the float64 CSR oracle.
+
+Tolerance (fp16 inputs, fp32 accumulation): elementwise
+|C - R| <= 1e-2 |R| + 1e-3 max|R|, and max|C - R| / max|R| <= 1e-2 (oracle.spmm.spmm_error).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmm as osp
+from trspmm import graphs
+import trspmm
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.cuda.init()
+
+
+def dense_B(n, K, seed):
+    return graphs.dense_operand(n, K, seed)
+
+
+def check(C, R, what):
+    e = osp.spmm_error(C, R)
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, f"{what}: {e}"
+    return e
+
+
+def run_plan(plan, Bh, **kw):
+    B = torch.from_numpy(Bh).cuda()
+    C = plan.spmm(B, **kw)
+    torch.cuda.synchronize()
+    return C.cpu().numpy()
+
+
+GRAPHS = [
+    ("er4096", lambda: graphs.erdos_renyi_gcn()),
+    ("rmat14", lambda: graphs.rmat(scale=14, edge_factor=16, seed=42)),
+    ("sbm2k", lambda: graphs.sbm(communities=2048, seed=3, val_seed=3)),
+    ("gridhubs", lambda: graphs.grid_hubs(side=256, hubs=8, hub_degree=20000, seed=6, val_seed=6)),
+    ("rand", lambda: graphs.random_csr(1000, 3000, 0.01, seed=5)),
+]
+
+
+@pytest.mark.parametrize("name,gen", GRAPHS, ids=[g[0] for g in GRAPHS])
+@pytest.mark.parametrize("K", [64, 128])
+def test_hybrid_spmm_matches_csr(name, gen, K):
+    say("case", name, K)
+    g = gen()
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n)
+    Bh = dense_B(g.n, K, seed=K)
+    C = run_plan(plan, Bh)
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh.astype(np.float64), m=g.m)
+    e = check(C, R, name)
+    say(name, K, plan.stats(), e)
+
+
+@pytest.mark.parametrize("mfma_tc,mfma_sptc,fill", [(1, 1, 0.25), (0, 0, 1.0), (1, 1, 0.0), (1, 0, 1.0)])
+def test_mfma_and_residual_routes_agree(mfma_tc, mfma_sptc, fill):
+    say("routes", mfma_tc, mfma_sptc, fill)
+    g = graphs.sbm(communities=1024, seed=11, val_seed=12)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n, mfma_tc=bool(mfma_tc), mfma_sptc=bool(mfma_sptc), sptc_min_fill=fill)
+    st = plan.stats()
+    if mfma_tc:
+        assert st["mfma_tiles"] > 0 and st["mfma_nnz"] > 0
+    else:
+        assert st["mfma_tiles"] == 0
+    assert st["nnz"] == g.nnz
+    Bh = dense_B(g.n, 96, seed=5)
+    C = run_plan(plan, Bh)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), "routes")
+
+
+@pytest.mark.parametrize("K", [1, 3, 8, 16, 24, 40, 200, 256, 520, 1030])
+def test_feature_widths(K):
+    say("K", K)
+    g = graphs.sbm(communities=128, seed=1, val_seed=2)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n, sptc_min_fill=0.1)
+    Bh = dense_B(g.n, K, seed=K)
+    C = run_plan(plan, Bh)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"K={K}")
+
+
+def test_strided_operands_and_output():
+    g = graphs.random_csr(300, 500, 0.02, seed=9)
+    plan = trspmm.Plan.from_format(trspmm.build_format(g.rowptr, g.col, g.val), g.m, g.n)
+    Bfull = torch.from_numpy(dense_B(g.n, 96, seed=1)).cuda()
+    B = Bfull[:, 8:72]                       # ldb 96, K 64
+    out_full = torch.full((g.m, 80), 7.0, device="cuda")
+    out = out_full[:, 4:68]
+    plan.spmm(B, out=out)
+    torch.cuda.synchronize()
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, B.cpu().numpy(), m=g.m)
+    check(out.cpu().numpy(), R, "strided")
+    assert torch.all(out_full[:, :4] == 7.0) and torch.all(out_full[:, 68:] == 7.0)
+
+
+def test_long_rows_are_split_and_fixed_up():
+    say("long rows")
+    # a few rows with 20k-60k entries next to short rows: pieces + fixup, no atomics
+    rng = np.random.default_rng(4)
+    m, n = 64, 80000
+    degs = np.array([60000 if r % 16 == 3 else (20000 if r == 40 else int(rng.integers(0, 5))) for r in range(m)])
+    rows = np.repeat(np.arange(m), degs)
+    cols = np.concatenate([np.sort(rng.choice(n, size=d, replace=False)) for d in degs])
+    rowptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+    val = rng.uniform(0, 1, size=len(cols)).astype(np.float16).astype(np.float32)
+    plan = trspmm.Plan.from_format(trspmm.build_format(rowptr, cols.astype(np.int32), val), m, n)
+    st = plan.stats()
+    assert st["split_rows"] >= 4 and st["partial_slots"] > st["split_rows"]
+    Bh = dense_B(n, 128, seed=3)
+    C = run_plan(plan, Bh)
+    check(C, osp.csr_spmm(rowptr, cols, val, Bh, m=m), "long rows")
+    del rows
+
+
+def test_empty_rows_and_empty_matrix_are_zero():
+    rowptr = np.zeros(33, np.int32)
+    plan = trspmm.Plan.from_format(trspmm.build_format(rowptr, np.zeros(0, np.int32), np.zeros(0, np.float32)), 32, 10)
+    B = torch.ones(10, 64, dtype=torch.float16, device="cuda")
+    out = torch.full((32, 64), 3.0, device="cuda")
+    plan.spmm(B, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(out == 0)
+
+
+def test_rows_beyond_m_are_dropped_like_reference():
+    # mOri smaller than the padded row count: rows >= m are not written (mGCNkernel_online.cu `row < mOri`)
+    g = graphs.random_csr(40, 50, 0.2, seed=2)            # padded to 48 rows
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, 40, g.n)
+    Bh = dense_B(g.n, 32, seed=1)
+    C = run_plan(plan, Bh)
+    assert C.shape == (40, 32)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=40), "m<rows")
+
+
+def test_deterministic_bitwise():
+    g = graphs.rmat(scale=13, edge_factor=16, seed=1)
+    plan = trspmm.Plan.from_format(trspmm.build_format(g.rowptr, g.col, g.val), g.m, g.n)
+    B = torch.from_numpy(dense_B(g.n, 128, seed=2)).cuda()
+    c1 = plan.spmm(B).clone()
+    c2 = plan.spmm(B).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(c1, c2)
+
+
+def test_plan_from_plain_csr_is_sddmm_only():
+    g = graphs.random_csr(50, 50, 0.1, seed=1)
+    plan = trspmm.Plan.from_csr(g.rowptr[:51], g.col, g.val.astype(np.float16), g.m, g.n)
+    B = torch.zeros(g.n, 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="SDDMM"):
+        plan.spmm(B)

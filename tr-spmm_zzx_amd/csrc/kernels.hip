@@ -1,0 +1,408 @@
+// HIP kernels for gfx950 (CDNA4, wave64): hybrid fp16 SpMM and SDDMM.
+//
+// Three SpMM kernels, all writing every output element exactly once (no atomics, no zero-fill):
+//   k_spmm_tasks    residual CSR.  A "lane group" of LPG lanes owns one task: a run of whole rows
+//                   (the entries streamed flat, rows flushed as their end is crossed) or one piece
+//                   of a long row.  Each lane holds VEC=8 consecutive features, so one B row of
+//                   K fp16 is fetched by K/8 lanes with 16-byte loads; U nonzeros are in flight per
+//                   lane.  fp32 accumulation.  Replaces the reference residual kernels
+//                   (TR-source/SpMM/mGCNkernel.cu:976-1171, spmm_utils/compute.h:27-240), which
+//                   accumulate in fp16 and only handle K = 128.
+//   k_spmm_fixup    sums the pieces of split rows in a fixed order (deterministic).
+//   k_spmm_mfma_win one workgroup owns a 16-row window: dense 16x16 fp16 tiles (TC blocks and
+//                   well-filled 2:4 group tiles) go through v_mfma_f32_16x16x16_f16 with the 16
+//                   gathered B rows staged in LDS, then the window's residual rows are added in LDS
+//                   and the 16 x KC tile is stored once.  Replaces the reference TC and packed
+//                   mma.sp kernels (mGCNkernel_online.cu:54-241, 812-933) and the add kernel
+//                   (:1314-1324).
+// SDDMM: k_sddmm_tasks, one lane group per task, per-entry dot products reduced across the group.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace trs {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+template <int VEC>
+struct BFrag;
+template <>
+struct BFrag<8> {
+  half8_t v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const half8_t*>(p); }
+  __device__ __forceinline__ void zero() { v = half8_t{0, 0, 0, 0, 0, 0, 0, 0}; }
+  __device__ __forceinline__ void fma(float (&acc)[8], float a) const {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_fmaf(a, (float)v[i], acc[i]);
+  }
+  __device__ __forceinline__ float dot(const BFrag& o) const {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s = __builtin_fmaf((float)v[i], (float)o.v[i], s);
+    return s;
+  }
+};
+template <>
+struct BFrag<1> {
+  _Float16 v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = __builtin_bit_cast(_Float16, *p); }
+  __device__ __forceinline__ void zero() { v = (_Float16)0; }
+  __device__ __forceinline__ void fma(float (&acc)[1], float a) const { acc[0] = __builtin_fmaf(a, (float)v, acc[0]); }
+  __device__ __forceinline__ float dot(const BFrag& o) const { return (float)v * (float)o.v; }
+};
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(float* dst, const float (&acc)[VEC]) {
+  if constexpr (VEC == 8) {
+    reinterpret_cast<float4_t*>(dst)[0] = float4_t{acc[0], acc[1], acc[2], acc[3]};
+    reinterpret_cast<float4_t*>(dst)[1] = float4_t{acc[4], acc[5], acc[6], acc[7]};
+  } else {
+    dst[0] = acc[0];
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+}
+
+// Accumulate entries [p0, p1) of one row into acc (U loads in flight).
+template <int VEC, int U>
+__device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
+                                               const uint16_t* __restrict__ B, int64_t ldb, int f, bool active,
+                                               int p0, int p1, float (&acc)[VEC]) {
+  for (int p = p0; p < p1; p += U) {
+    int cc[U];
+    float vv[U];
+    BFrag<VEC> bb[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const bool in = p + i < p1;
+      cc[i] = in ? col[p + i] : 0;
+      vv[i] = in ? h2f(val[p + i]) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (active && p + i < p1) bb[i].load(B + (int64_t)cc[i] * ldb + f);
+      else bb[i].zero();
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) bb[i].fma(acc, vv[i]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+template <int VEC, int LPG, int U>
+__global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
+                                                    int K, float* __restrict__ C, int64_t ldc,
+                                                    float* __restrict__ partial) {
+  constexpr int GPW = 64 / LPG;
+  const int lane = threadIdx.x & 63;
+  const int task_id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
+  if (task_id >= P.ntasks) return;
+  const int f = blockIdx.y * (LPG * VEC) + (lane % LPG) * VEC;
+  const bool active = f < K;
+  const Task t = P.tasks[task_id];
+  const int32_t* __restrict__ col = P.col;
+  const uint16_t* __restrict__ val = P.val;
+  float acc[VEC];
+  zero_acc(acc);
+
+  if (t.row_end < 0) {   // piece of a split row -> partial slot
+    accumulate_row<VEC, U>(col, val, B, ldb, f, active, t.nz_begin, t.nz_end, acc);
+    if (active) store_vec<VEC>(partial + (int64_t)(~t.row_end) * K + f, acc);
+    return;
+  }
+  // whole rows [row_begin, row_end): stream entries, flush a row when its end is crossed
+  int r = t.row_begin;
+  int rend = P.rowptr[r + 1];
+  for (int p = t.nz_begin; p < t.nz_end; p += U) {
+    int cc[U];
+    float vv[U];
+    BFrag<VEC> bb[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const bool in = p + i < t.nz_end;
+      cc[i] = in ? col[p + i] : 0;
+      vv[i] = in ? h2f(val[p + i]) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (active && p + i < t.nz_end) bb[i].load(B + (int64_t)cc[i] * ldb + f);
+      else bb[i].zero();
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      if (p + i < t.nz_end) {
+        while (p + i >= rend) {
+          if (active) store_vec<VEC>(C + (int64_t)r * ldc + f, acc);
+          zero_acc(acc);
+          ++r;
+          rend = P.rowptr[r + 1];
+        }
+        bb[i].fma(acc, vv[i]);
+      }
+    }
+  }
+  for (; r < t.row_end; ++r) {
+    if (active) store_vec<VEC>(C + (int64_t)r * ldc + f, acc);
+    zero_acc(acc);
+  }
+}
+
+template <int VEC, int LPG>
+__global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
+                                                    const float* __restrict__ partial) {
+  constexpr int GPW = 64 / LPG;
+  const int lane = threadIdx.x & 63;
+  const int id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
+  if (id >= P.nfixups) return;
+  const int f = blockIdx.y * (LPG * VEC) + (lane % LPG) * VEC;
+  if (f >= K) return;
+  const Fixup x = P.fixups[id];
+  float acc[VEC];
+  zero_acc(acc);
+  for (int s = 0; s < x.slots; ++s) {
+    const float* src = partial + (int64_t)(x.slot_begin + s) * K + f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[i] += src[i];
+  }
+  store_vec<VEC>(C + (int64_t)x.row * ldc + f, acc);
+}
+
+// ------------------------------------------------------------------------------------------------
+// MFMA window kernel.  KC = features per workgroup (multiple of 16, <= 256); NT = MFMA n-tiles
+// (16 features each) per wave = KC / 64 rounded up.
+// MFMA 16x16x16 f16 operand layout (lane l, j = 0..3):
+//   A: A[l % 16][4 * (l / 16) + j]      B: B[4 * (l / 16) + j][l % 16]
+//   D: D[4 * (l / 16) + j][l % 16]
+// Here A = the 16x16 tile (window row x tile column), B = gathered B rows (tile column x feature).
+template <int VEC, int NT>
+__global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
+                                                       int K, float* __restrict__ C, int64_t ldc, int KC) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int KCP = KC + 4;   // fp32 output tile row stride
+  const int KCB = KC + 8;   // fp16 staged-B row stride (keeps 16-byte alignment)
+  float* otile = reinterpret_cast<float*>(smem);
+  _Float16* bst = reinterpret_cast<_Float16*>(otile + 16 * KCP);
+
+  const MfmaWindow w = P.mwin[blockIdx.x];
+  const int fbase = blockIdx.y * KC;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int ntn = KC / 16;
+
+  float4_t acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int t = w.tile_begin; t < w.tile_end; ++t) {
+    __syncthreads();
+    // stage the 16 gathered B rows (features [fbase, fbase + KC)) into LDS
+    const int per_row = KC / VEC;
+    for (int idx = threadIdx.x; idx < 16 * per_row; idx += 256) {
+      const int k = idx / per_row;
+      const int ff = (idx % per_row) * VEC;
+      const int c = P.tile_cols[t * 16 + k];
+      BFrag<VEC> b;
+      if (c >= 0 && fbase + ff < K) b.load(B + (int64_t)c * ldb + fbase + ff);
+      else b.zero();
+      if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
+      else bst[k * KCB + ff] = b.v;
+    }
+    __syncthreads();
+    const half4_t a = *reinterpret_cast<const half4_t*>(
+        reinterpret_cast<const _Float16*>(P.tile_a) + (int64_t)t * 256 + (lane & 15) * 16 + 4 * (lane >> 4));
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int nt = wave + 4 * j;
+      if (nt < ntn) {
+        half4_t b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = bst[(4 * (lane >> 4) + i) * KCB + nt * 16 + (lane & 15)];
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[j], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int nt = wave + 4 * j;
+    if (nt < ntn) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) otile[(4 * (lane >> 4) + i) * KCP + nt * 16 + (lane & 15)] = acc[j][i];
+    }
+  }
+  __syncthreads();
+
+  // residual rows of this window, added on top of the MFMA share
+  const int gs = KC / VEC;         // threads per row group
+  const int groups = 256 / gs;
+  const int g = threadIdx.x / gs;
+  const int ff = (threadIdx.x % gs) * VEC;
+  const int f = fbase + ff;
+  for (int rl = g; rl < 16; rl += groups) {
+    const int row = w.row0 + rl;
+    if (row >= P.m) break;
+    float racc[VEC];
+    zero_acc(racc);
+    accumulate_row<VEC, 8>(P.col, P.val, B, ldb, f, f < K, P.rowptr[row], P.rowptr[row + 1], racc);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) otile[rl * KCP + ff + i] += racc[i];
+  }
+  __syncthreads();
+
+  // store the 16 x KC tile once
+  const int per_row4 = KC / 4;
+  for (int idx = threadIdx.x; idx < 16 * per_row4; idx += 256) {
+    const int rl = idx / per_row4;
+    const int c4 = (idx % per_row4) * 4;
+    const int row = w.row0 + rl;
+    if (row >= P.m) continue;
+    const float* src = otile + rl * KCP + c4;
+    float* dst = C + (int64_t)row * ldc + fbase + c4;
+    if constexpr (VEC == 8) {
+      if (fbase + c4 < K) *reinterpret_cast<float4_t*>(dst) = float4_t{src[0], src[1], src[2], src[3]};
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (fbase + c4 + i < K) dst[i] = src[i];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+template <int VEC, int LPG, int U>
+__global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
+                                                     const uint16_t* __restrict__ Y, int64_t ldy, int K,
+                                                     float* __restrict__ out) {
+  constexpr int GPW = 64 / LPG;
+  constexpr int FPP = LPG * VEC;   // features per pass
+  const int lane = threadIdx.x & 63;
+  const int task_id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
+  const bool valid = task_id < P.ntasks;
+  const Task t = P.tasks[valid ? task_id : 0];
+  const int li = lane % LPG;
+  // rows of a task: whole rows [row_begin, row_end) or one piece of a row
+  const int rb = t.row_begin;
+  const int re = t.row_end < 0 ? t.row_begin + 1 : t.row_end;
+  int p_lo = t.nz_begin;
+  for (int r = rb; r < re; ++r) {
+    const int p_hi = t.row_end < 0 ? t.nz_end : min(t.nz_end, P.rowptr[r + 1]);
+    for (int p = p_lo; p < p_hi; p += U) {
+      float s[U];
+#pragma unroll
+      for (int i = 0; i < U; ++i) s[i] = 0.f;
+      for (int f0 = 0; f0 < K; f0 += FPP) {
+        const int f = f0 + li * VEC;
+        const bool act = valid && f < K;
+        BFrag<VEC> x;
+        if (act) x.load(X + (int64_t)r * ldx + f);
+        else x.zero();
+        int cc[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) cc[i] = (p + i < p_hi) ? P.col[p + i] : 0;
+        BFrag<VEC> y[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+          if (act && p + i < p_hi) y[i].load(Y + (int64_t)cc[i] * ldy + f);
+          else y[i].zero();
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) s[i] += x.dot(y[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+#pragma unroll
+        for (int o = LPG / 2; o > 0; o >>= 1) s[i] += __shfl_xor(s[i], o, 64);
+      }
+      if (valid && li == 0) {
+#pragma unroll
+        for (int i = 0; i < U; ++i)
+          if (p + i < p_hi) out[p + i] = s[i];
+      }
+    }
+    p_lo = p_hi;
+  }
+}
+
+int lanes_for(int K, int vec) {
+  const int need = (K + vec - 1) / vec;
+  int l = 1;
+  while (l < need && l < 64) l <<= 1;
+  return l;
+}
+
+template <int VEC>
+hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
+                           float* partial, hipStream_t s, hipEvent_t* ev) {
+  if (ev) (void)hipEventRecord(ev[0], s);
+  const int lpg = lanes_for(K, VEC);
+  const int fpp = lpg * VEC;
+  const int passes = (K + fpp - 1) / fpp;
+  if (p.ntasks > 0) {
+    const int gpb = 4 * (64 / lpg);
+    dim3 grid((p.ntasks + gpb - 1) / gpb, passes);
+#define TRS_TASKS(L) case L: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break;
+    switch (lpg) { TRS_TASKS(1) TRS_TASKS(2) TRS_TASKS(4) TRS_TASKS(8) TRS_TASKS(16) TRS_TASKS(32) TRS_TASKS(64) }
+#undef TRS_TASKS
+  }
+  if (ev) (void)hipEventRecord(ev[1], s);
+  if (p.nmwin > 0) {
+    const int kc16 = ((K + 15) / 16) * 16;
+    const int KC = kc16 < 256 ? kc16 : 256;
+    dim3 grid(p.nmwin, (K + KC - 1) / KC);
+    const size_t shm = (size_t)16 * (KC + 4) * 4 + (size_t)16 * (KC + 8) * 2;
+    if (KC <= 64) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 1>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
+    else if (KC <= 128) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 2>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
+    else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 4>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
+  }
+  if (ev) (void)hipEventRecord(ev[2], s);
+  if (p.nfixups > 0) {
+    const int gpb = 4 * (64 / lpg);
+    dim3 grid((p.nfixups + gpb - 1) / gpb, passes);
+#define TRS_FIX(L) case L: hipLaunchKernelGGL((k_spmm_fixup<VEC, L>), grid, dim3(256), 0, s, p, K, C, ldc, partial); break;
+    switch (lpg) { TRS_FIX(1) TRS_FIX(2) TRS_FIX(4) TRS_FIX(8) TRS_FIX(16) TRS_FIX(32) TRS_FIX(64) }
+#undef TRS_FIX
+  }
+  if (ev) (void)hipEventRecord(ev[3], s);
+  return hipGetLastError();
+}
+
+template <int VEC>
+hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                            int K, float* out, hipStream_t s) {
+  if (p.ntasks <= 0) return hipSuccess;
+  const int lpg = lanes_for(K, VEC);
+  const int gpb = 4 * (64 / lpg);
+  dim3 grid((p.ntasks + gpb - 1) / gpb);
+#define TRS_SD(L) case L: hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break;
+  switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
+#undef TRS_SD
+  return hipGetLastError();
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
+                       float* partial, hipStream_t stream, hipEvent_t* ev) {
+  const bool v8 = K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
+                  (partial == nullptr || aligned16(partial));
+  return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, stream, ev)
+            : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, stream, ev);
+}
+
+hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                        int K, float* out, hipStream_t stream) {
+  const bool v8 = K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
+  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream)
+            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream);
+}
+
+}  // namespace trs

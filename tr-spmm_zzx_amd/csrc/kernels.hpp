@@ -1,0 +1,44 @@
+// Device kernels of the hybrid SpMM / SDDMM path (gfx950) and their launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace trs {
+
+// Residual task: rows [row_begin, row_end) with their entries [nz_begin, nz_end), or, when
+// row_end < 0, a piece [nz_begin, nz_end) of row `row_begin` whose sum goes to partial slot
+// ~row_end (a split row, finished by the fixup kernel).
+struct Task { int32_t row_begin, row_end, nz_begin, nz_end; };
+
+// A split row: C[row] = sum of partial slots [slot_begin, slot_begin + slots) in order.
+struct Fixup { int32_t row, slot_begin, slots, pad; };
+
+// A window handled by the MFMA window kernel: 16 output rows starting at row0 (rows >= m are
+// dropped), dense 16x16 fp16 tiles [tile_begin, tile_end), plus that window's residual rows.
+struct MfmaWindow { int32_t row0, tile_begin, tile_end, pad; };
+
+struct DevicePlan {
+  int32_t m = 0, n = 0;
+  int64_t nnz_csr = 0;
+  const int32_t* rowptr = nullptr;   // [m + 1] residual CSR (fp16 values)
+  const int32_t* col = nullptr;
+  const uint16_t* val = nullptr;
+  const Task* tasks = nullptr;
+  int32_t ntasks = 0;
+  const Fixup* fixups = nullptr;
+  int32_t nfixups = 0;
+  int32_t partial_slots = 0;
+  const MfmaWindow* mwin = nullptr;
+  int32_t nmwin = 0;
+  const int32_t* tile_cols = nullptr;  // [tiles][16]
+  const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16
+  int32_t ntiles = 0;
+};
+
+// ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
+hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
+                       float* partial, hipStream_t stream, hipEvent_t* ev = nullptr);
+hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                        int K, float* out, hipStream_t stream);
+
+}  // namespace trs

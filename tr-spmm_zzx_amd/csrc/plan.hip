@@ -1,0 +1,741 @@
+// Plans: lower format arrays to the device layout the kernels read, validate, upload once.
+//
+// Meaning of the arrays (the semantics every lowering below follows):
+//   TC sub-block s of part p (TR-source/SpMM/mGCNkernel_online.cu:54-241): rows t_window_row[p] +
+//     0..15, columns t_column[8s .. 8s+7] (-1 = empty); bit (r*8 + k) of t_binary[2s] (rows 0-7)
+//     or t_binary[2s+1] (rows 8-15) marks a stored value; values sit at t_blockNew_offset[s] in
+//     ascending bit order, the rows 8-15 after the rows 0-7.
+//   2:4 group g (mGCNkernel_online.cu:248-337): rows window_of(g) * window + lr, up to two values
+//     s_value[g][lr][q] at columns s_column[g][s_pos[g][lr][q]] (pos -1 = empty).
+//   packed tile t (block_online.cpp:796-841, mGCNkernel_online.cu:812-933): rows w*window + rg and
+//     + rg + 8; chunk c holds two fp16 values (s_packed_a) at 2-bit positions (s_packed_meta) of
+//     columns s_tile_column[t][4c .. 4c+3].
+//   residual part i (mGCNkernel.cu:976-1171): row c_row[i], entries c_row_offsets[i] .. [i+1].
+// Output rows >= m are dropped, as the reference kernels guard `row < mOri`.  Column indices must
+// lie in [0, n): the reference reads out of bounds there, this library rejects the plan instead.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "format.hpp"
+#include "kernels.hpp"
+
+namespace {
+thread_local std::string g_error;
+}
+
+namespace trs {
+void set_error(const std::string& msg) { g_error = msg; }
+}  // namespace trs
+
+struct trs_plan {
+  trs::DevicePlan dp;
+  void* dmem = nullptr;
+  size_t dbytes = 0;
+  int device = 0;
+  bool csr_only = false;
+  trs_plan_stats stats{};
+  ~trs_plan() {
+    if (dmem) (void)hipFree(dmem);
+  }
+};
+
+namespace {
+
+struct Status {
+  int code = TRS_OK;
+  std::string msg;
+  bool ok() const { return code == TRS_OK; }
+};
+
+Status fail(int code, const std::string& m) { return Status{code, m}; }
+
+// Host-side staging of one plan.
+struct Lowering {
+  int32_t m = 0, n = 0;
+  std::vector<int32_t> row, col;
+  std::vector<float> val;
+  // MFMA tiles: row0, 16 columns, dense 16x16 values
+  struct Tile { int32_t row0; int32_t cols[16]; float a[256]; int nnz; };
+  std::vector<Tile> tiles;
+  Status st;
+
+  bool check_col(int64_t c) {
+    if (c < 0 || c >= n) {
+      if (st.ok()) st = fail(TRS_ERANGE, "column index " + std::to_string(c) + " outside [0, " + std::to_string(n) + ")");
+      return false;
+    }
+    return true;
+  }
+  void add(int64_t r, int64_t c, float v) {
+    if (r < 0 || r >= m) return;   // reference kernels drop rows >= mOri
+    if (!check_col(c)) return;
+    row.push_back((int32_t)r);
+    col.push_back((int32_t)c);
+    val.push_back(v);
+  }
+  // Tile entry; -1 columns never carry values.
+  void tile_add(Tile& t, int r, int k, float v) {
+    t.a[r * 16 + k] += v;
+    t.nnz++;
+  }
+};
+
+
+float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// TC sub-blocks -> MFMA tiles (pairs of sub-blocks of one part, 16 columns) or entries.
+void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_t* t_blockoff,
+              const int32_t* t_col, const float* vals_f32, const uint16_t* vals_f16, int64_t nvals,
+              const int32_t* t_winrow, const int64_t* t_bin, bool to_mfma) {
+  for (int64_t p = 0; p < nparts && L.st.ok(); ++p) {
+    const int32_t s0 = t_rowoff[p], s1 = t_rowoff[p + 1];
+    const int32_t row0 = t_winrow[p];
+    const bool mfma = to_mfma && row0 % 16 == 0 && row0 >= 0;
+    for (int32_t s = s0; s < s1 && L.st.ok(); s += (mfma ? 2 : 1)) {
+      Lowering::Tile T;
+      if (mfma) {
+        T.row0 = row0;
+        std::fill(T.cols, T.cols + 16, -1);
+        std::fill(T.a, T.a + 256, 0.f);
+        T.nnz = 0;
+      }
+      const int nsub = mfma ? std::min(2, s1 - s) : 1;
+      for (int h = 0; h < nsub; ++h) {
+        const int32_t sb = s + h;
+        const uint64_t lo = (uint64_t)t_bin[2 * (int64_t)sb], hi = (uint64_t)t_bin[2 * (int64_t)sb + 1];
+        int64_t vi = t_blockoff[sb];
+        const int pop = __builtin_popcountll(lo) + __builtin_popcountll(hi);
+        if (vi < 0 || vi + pop > nvals) {
+          L.st = fail(TRS_EINVAL, "t_blockNew_offset / t_binary describe values beyond t_value");
+          return;
+        }
+        for (int k = 0; k < 8 && mfma; ++k) {
+          const int32_t c = t_col[(int64_t)sb * 8 + k];
+          if (c >= 0 && !L.check_col(c)) return;
+          T.cols[h * 8 + k] = c;
+        }
+        for (int half = 0; half < 2; ++half) {
+          uint64_t bits = half ? hi : lo;
+          while (bits) {
+            const int b = __builtin_ctzll(bits);
+            bits &= bits - 1;
+            const int r = half * 8 + b / 8, k = b % 8;
+            const int32_t c = t_col[(int64_t)sb * 8 + k];
+            const float v = vals_f32 ? vals_f32[vi] : f16_to_f32(vals_f16[vi]);
+            ++vi;
+            if (c < 0) continue;   // value at an empty column: the reference reads B[-1]; skip
+            if (mfma) {
+              if (row0 + r < L.m) L.tile_add(T, r, h * 8 + k, v);
+            } else {
+              L.add((int64_t)row0 + r, c, v);
+            }
+          }
+        }
+      }
+      if (mfma) L.tiles.push_back(T);
+    }
+  }
+}
+
+void lower_residual(Lowering& L, const int32_t* off, const int32_t* rows, int64_t nparts, const int32_t* cols,
+                    const float* vf32, const uint16_t* vf16, int64_t ncols) {
+  for (int64_t i = 0; i < nparts && L.st.ok(); ++i) {
+    if (off[i] < 0 || off[i + 1] < off[i] || off[i + 1] > ncols) {
+      L.st = fail(TRS_EINVAL, "residual offsets out of range");
+      return;
+    }
+    for (int32_t e = off[i]; e < off[i + 1]; ++e) L.add(rows[i], cols[e], vf32 ? vf32[e] : f16_to_f32(vf16[e]));
+  }
+}
+
+// 2:4 groups (s_column / s_value / s_pos) grouped in tiles of 4 per window as the reference packs them.
+void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
+                  const int32_t* s_win, const int32_t* s_off, int64_t nwin, int window, bool to_mfma,
+                  float min_fill) {
+  auto group_row0 = [&](int64_t g, int64_t w) { return (int64_t)(s_win ? s_win[g] : w) * window; };
+  auto emit_group = [&](int64_t g, int64_t row0) {
+    for (int lr = 0; lr < window; ++lr)
+      for (int q = 0; q < 2; ++q) {
+        const int p = s_pos[(g * window + lr) * 2 + q];
+        if (p < 0) continue;
+        if (p > 3) { if (L.st.ok()) L.st = fail(TRS_EINVAL, "s_pos entry outside 0..3"); return; }
+        const int32_t c = s_col[g * 4 + p];
+        if (c < 0) continue;   // value at a padded column slot (scalar kernel skips it)
+        L.add(row0 + lr, c, s_val[(g * window + lr) * 2 + q]);
+      }
+  };
+  if (!s_off || !to_mfma || window != 16) {
+    if (s_off) {
+      for (int64_t w = 0; w < nwin && L.st.ok(); ++w)
+        for (int64_t g = s_off[w]; g < s_off[w + 1]; ++g) emit_group(g, group_row0(g, w));
+    } else {
+      for (int64_t g = 0; g < groups && L.st.ok(); ++g) emit_group(g, group_row0(g, 0));
+    }
+    return;
+  }
+  for (int64_t w = 0; w < nwin && L.st.ok(); ++w) {
+    for (int64_t base = s_off[w]; base < s_off[w + 1] && L.st.ok(); base += 4) {
+      const int64_t end = std::min<int64_t>(base + 4, s_off[w + 1]);
+      int kept = 0;
+      for (int64_t g = base; g < end; ++g)
+        for (int i = 0; i < window * 2; ++i) kept += s_pos[g * window * 2 + i] >= 0;
+      const int64_t row0 = group_row0(base, w);
+      if (kept < min_fill * 256.f || row0 % 16 != 0) {
+        for (int64_t g = base; g < end; ++g) emit_group(g, group_row0(g, w));
+        continue;
+      }
+      Lowering::Tile T;
+      T.row0 = (int32_t)row0;
+      std::fill(T.cols, T.cols + 16, -1);
+      std::fill(T.a, T.a + 256, 0.f);
+      T.nnz = 0;
+      for (int64_t g = base; g < end; ++g) {
+        const int gi = (int)(g - base);
+        for (int p = 0; p < 4; ++p) {
+          const int32_t c = s_col[g * 4 + p];
+          if (c >= 0 && !L.check_col(c)) return;
+          T.cols[gi * 4 + p] = c;
+        }
+        for (int lr = 0; lr < window; ++lr)
+          for (int q = 0; q < 2; ++q) {
+            const int p = s_pos[(g * window + lr) * 2 + q];
+            if (p < 0) continue;
+            if (p > 3) { L.st = fail(TRS_EINVAL, "s_pos entry outside 0..3"); return; }
+            if (s_col[g * 4 + p] < 0) continue;
+            if (row0 + lr < L.m) L.tile_add(T, lr, gi * 4 + p, s_val[(g * window + lr) * 2 + q]);
+          }
+      }
+      L.tiles.push_back(T);
+    }
+  }
+}
+
+// Packed 2:4 tiles (s_tile_column / s_packed_a / s_packed_meta) -> entries or MFMA tiles.
+void lower_packed(Lowering& L, const int32_t* tcol, const int32_t* pa, const int32_t* pm, int64_t tiles,
+                  const int32_t* wto, int64_t nwin, int window, bool to_mfma, float min_fill) {
+  for (int64_t w = 0; w < nwin && L.st.ok(); ++w) {
+    if (wto[w] < 0 || wto[w + 1] < wto[w] || wto[w + 1] > tiles) {
+      L.st = fail(TRS_EINVAL, "s_window_tile_offset out of range");
+      return;
+    }
+    for (int64_t t = wto[w]; t < wto[w + 1] && L.st.ok(); ++t) {
+      struct E { int r, k; float v; };
+      std::vector<E> es;
+      for (int rg = 0; rg < 8; ++rg) {
+        const uint32_t meta = (uint32_t)pm[t * 8 + rg];
+        for (int hsel = 0; hsel < 2; ++hsel) {
+          const int lr = rg + 8 * hsel;
+          if (lr >= window) continue;
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t word = (uint32_t)pa[((t * 8 + rg) * 4 + c) * 2 + hsel];
+            const uint32_t m4 = (meta >> (16 * hsel + 4 * c)) & 15u;
+            const int p0 = m4 & 3, p1 = (m4 >> 2) & 3;
+            const float v0 = f16_to_f32((uint16_t)(word & 0xffffu));
+            const float v1 = f16_to_f32((uint16_t)(word >> 16));
+            if (v0 != 0.f) es.push_back({lr, c * 4 + p0, v0});
+            if (v1 != 0.f) es.push_back({lr, c * 4 + p1, v1});
+          }
+        }
+      }
+      const int64_t row0 = w * (int64_t)window;
+      const bool mfma = to_mfma && window == 16 && row0 % 16 == 0 && (float)es.size() >= min_fill * 256.f;
+      Lowering::Tile T;
+      if (mfma) {
+        T.row0 = (int32_t)row0;
+        T.nnz = 0;
+        std::fill(T.a, T.a + 256, 0.f);
+        for (int k = 0; k < 16; ++k) {
+          const int32_t c = tcol[t * 16 + k];
+          if (c >= 0 && !L.check_col(c)) return;
+          T.cols[k] = c;
+        }
+      }
+      for (const E& e : es) {
+        const int32_t c = tcol[t * 16 + e.k];
+        if (c < 0) continue;
+        if (mfma) {
+          if (row0 + e.r < L.m) L.tile_add(T, e.r, e.k, e.v);
+        } else {
+          L.add(row0 + e.r, c, e.v);
+        }
+      }
+      if (mfma) L.tiles.push_back(T);
+    }
+  }
+}
+
+template <class T>
+size_t push_bytes(std::vector<unsigned char>& blob, const std::vector<T>& v) {
+  size_t off = (blob.size() + 255) & ~size_t(255);
+  blob.resize(off + v.size() * sizeof(T));
+  if (!v.empty()) std::memcpy(blob.data() + off, v.data(), v.size() * sizeof(T));
+  return off;
+}
+
+// Residual CSR + tasks + MFMA windows -> device plan.
+Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool keep_order, trs_plan** out) {
+  if (!L.st.ok()) return L.st;
+  const int32_t m = L.m;
+  const int64_t nent = (int64_t)L.row.size();
+  if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
+
+  // MFMA windows: 16-row blocks owning at least one tile.
+  std::vector<int32_t> block_tiles_begin, block_of_tile;
+  std::sort(L.tiles.begin(), L.tiles.end(), [](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; });
+  const int32_t nblocks = (m + 15) / 16;
+  std::vector<uint8_t> owned(nblocks, 0);
+  for (const auto& t : L.tiles) owned[t.row0 / 16] = 1;
+
+  // residual CSR sorted by (row, column); stable so equal keys keep insertion order
+  std::vector<int64_t> cnt(m + 1, 0);
+  for (int64_t i = 0; i < nent; ++i) cnt[L.row[i] + 1]++;
+  for (int32_t r = 0; r < m; ++r) cnt[r + 1] += cnt[r];
+  std::vector<int32_t> rowptr(m + 1);
+  for (int32_t r = 0; r <= m; ++r) rowptr[r] = (int32_t)cnt[r];
+  std::vector<int32_t> col(nent);
+  std::vector<uint16_t> val(nent);
+  {
+    std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
+    std::vector<int64_t> perm(nent);
+    for (int64_t i = 0; i < nent; ++i) perm[pos[L.row[i]]++] = i;
+    for (int32_t r = 0; r < m; ++r) {
+      auto b = perm.begin() + rowptr[r], e = perm.begin() + rowptr[r + 1];
+      if (!keep_order) std::stable_sort(b, e, [&](int64_t x, int64_t y) { return L.col[x] < L.col[y]; });
+    }
+    for (int64_t i = 0; i < nent; ++i) {
+      col[i] = L.col[perm[i]];
+      val[i] = trs::half_bits(L.val[perm[i]]);
+    }
+  }
+
+  // Hand a tile-owning block back to the residual path when one of its rows is very long
+  // (the window kernel walks each residual row with one lane group).
+  const int row_cap = 4096;
+  std::vector<Lowering::Tile> kept_tiles;
+  std::vector<trs::MfmaWindow> mwin;
+  {
+    std::vector<uint8_t> demote(nblocks, 0);
+    for (int32_t b = 0; b < nblocks; ++b) {
+      if (!owned[b]) continue;
+      for (int32_t r = b * 16; r < std::min(m, b * 16 + 16); ++r)
+        if (rowptr[r + 1] - rowptr[r] > row_cap) demote[b] = 1;
+    }
+    bool any_demote = false;
+    for (int32_t b = 0; b < nblocks; ++b) any_demote |= demote[b] != 0;
+    if (any_demote) {
+      // re-lower demoted tiles as entries and rebuild the residual CSR
+      Lowering L2;
+      L2.m = L.m; L2.n = L.n;
+      L2.row = L.row; L2.col = L.col; L2.val = L.val;
+      for (const auto& t : L.tiles) {
+        if (!demote[t.row0 / 16]) { L2.tiles.push_back(t); continue; }
+        for (int r = 0; r < 16; ++r)
+          for (int k = 0; k < 16; ++k)
+            if (t.cols[k] >= 0 && t.a[r * 16 + k] != 0.f) L2.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
+      }
+      return finalize(L2, opt, csr_only, keep_order, out);
+    }
+  }
+  for (size_t i = 0; i < L.tiles.size();) {
+    size_t j = i;
+    while (j < L.tiles.size() && L.tiles[j].row0 == L.tiles[i].row0) ++j;
+    mwin.push_back({L.tiles[i].row0, (int32_t)i, (int32_t)j, 0});
+    i = j;
+  }
+  std::vector<int32_t> tile_cols(L.tiles.size() * 16);
+  std::vector<uint16_t> tile_a(L.tiles.size() * 256);
+  int64_t mfma_nnz = 0;
+  for (size_t t = 0; t < L.tiles.size(); ++t) {
+    int32_t first_valid = 0;
+    for (int k = 0; k < 16; ++k) tile_cols[t * 16 + k] = L.tiles[t].cols[k];
+    (void)first_valid;
+    for (int i = 0; i < 256; ++i) tile_a[t * 256 + i] = trs::half_bits(L.tiles[t].a[i]);
+    mfma_nnz += L.tiles[t].nnz;
+  }
+
+  // residual tasks over rows not owned by an MFMA window
+  const int S = opt.task_nnz > 0 ? opt.task_nnz : 64;
+  const int piece_max = std::max(S, 256);
+  const int rows_cap = 64;
+  std::vector<trs::Task> pieces, packed;
+  std::vector<trs::Fixup> fix;
+  int32_t slots = 0;
+  int64_t split_rows = 0;
+  int32_t r = 0;
+  while (r < m) {
+    if (owned[r / 16]) { r = std::min(m, (r / 16 + 1) * 16); continue; }
+    const int32_t deg = rowptr[r + 1] - rowptr[r];
+    if (deg > piece_max && !csr_only) {
+      const int np = (deg + piece_max - 1) / piece_max;
+      const int32_t base = slots;
+      for (int q = 0; q < np; ++q) {
+        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
+        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
+        pieces.push_back({r, ~slots, b, e});
+        ++slots;
+      }
+      fix.push_back({r, base, np, 0});
+      ++split_rows;
+      ++r;
+      continue;
+    }
+    if (deg > piece_max && csr_only) {   // SDDMM: pieces write their own outputs, no fixup
+      const int np = (deg + piece_max - 1) / piece_max;
+      for (int q = 0; q < np; ++q) {
+        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
+        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
+        pieces.push_back({r, -1, b, e});
+      }
+      ++r;
+      continue;
+    }
+    // pack whole rows while the entry count stays within S (a single long row forms its own task)
+    int32_t r1 = r + 1;
+    int32_t tot = deg;
+    while (r1 < m && r1 - r < rows_cap && !owned[r1 / 16]) {
+      const int32_t d = rowptr[r1 + 1] - rowptr[r1];
+      if (d > piece_max || tot + d > S) break;
+      tot += d;
+      ++r1;
+    }
+    packed.push_back({r, r1, rowptr[r], rowptr[r1]});
+    r = r1;
+  }
+  std::vector<trs::Task> tasks;
+  tasks.reserve(pieces.size() + packed.size());
+  tasks.insert(tasks.end(), pieces.begin(), pieces.end());
+  tasks.insert(tasks.end(), packed.begin(), packed.end());
+  if (tasks.size() > (size_t)INT32_MAX / 64) return fail(TRS_ERANGE, "too many tasks");
+
+  // one device allocation
+  std::vector<unsigned char> blob;
+  const size_t o_rowptr = push_bytes(blob, rowptr);
+  const size_t o_col = push_bytes(blob, col);
+  const size_t o_val = push_bytes(blob, val);
+  const size_t o_tasks = push_bytes(blob, tasks);
+  const size_t o_fix = push_bytes(blob, fix);
+  const size_t o_mwin = push_bytes(blob, mwin);
+  const size_t o_tcol = push_bytes(blob, tile_cols);
+  const size_t o_ta = push_bytes(blob, tile_a);
+  blob.resize(std::max<size_t>(blob.size(), 256));
+
+  trs_plan* P = new trs_plan();
+  if (hipGetDevice(&P->device) != hipSuccess) {
+    delete P;
+    return fail(TRS_EDEVICE, "no HIP device available");
+  }
+  if (hipMalloc(&P->dmem, blob.size()) != hipSuccess) {
+    P->dmem = nullptr;
+    delete P;
+    (void)hipGetLastError();
+    return fail(TRS_ENOMEM, "hipMalloc of " + std::to_string(blob.size()) + " plan bytes failed");
+  }
+  P->dbytes = blob.size();
+  if (hipMemcpy(P->dmem, blob.data(), blob.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    delete P;
+    return fail(TRS_EDEVICE, "plan upload failed");
+  }
+  unsigned char* base = static_cast<unsigned char*>(P->dmem);
+  trs::DevicePlan& d = P->dp;
+  d.m = m;
+  d.n = L.n;
+  d.nnz_csr = nent;
+  d.rowptr = reinterpret_cast<const int32_t*>(base + o_rowptr);
+  d.col = reinterpret_cast<const int32_t*>(base + o_col);
+  d.val = reinterpret_cast<const uint16_t*>(base + o_val);
+  d.tasks = reinterpret_cast<const trs::Task*>(base + o_tasks);
+  d.ntasks = (int32_t)tasks.size();
+  d.fixups = reinterpret_cast<const trs::Fixup*>(base + o_fix);
+  d.nfixups = (int32_t)fix.size();
+  d.partial_slots = slots;
+  d.mwin = reinterpret_cast<const trs::MfmaWindow*>(base + o_mwin);
+  d.nmwin = (int32_t)mwin.size();
+  d.tile_cols = reinterpret_cast<const int32_t*>(base + o_tcol);
+  d.tile_a = reinterpret_cast<const uint16_t*>(base + o_ta);
+  d.ntiles = (int32_t)L.tiles.size();
+  P->csr_only = csr_only;
+  trs_plan_stats& s = P->stats;
+  s.m = m;
+  s.n = L.n;
+  s.csr_nnz = nent;
+  s.mfma_tiles = (int64_t)L.tiles.size();
+  s.mfma_nnz = mfma_nnz;
+  s.nnz = nent + mfma_nnz;
+  s.tasks = (int64_t)tasks.size();
+  s.split_rows = split_rows;
+  s.partial_slots = slots;
+  s.device_bytes = (int64_t)blob.size();
+  s.mfma_windows = (int64_t)mwin.size();
+  int64_t wnnz = 0;
+  for (const auto& w : mwin)
+    for (int32_t r = w.row0; r < std::min(m, w.row0 + 16); ++r) wnnz += rowptr[r + 1] - rowptr[r];
+  s.window_csr_nnz = wnnz;
+  *out = P;
+  return Status{};
+}
+
+int report(const Status& s) {
+  if (!s.ok()) trs::set_error(s.msg);
+  return s.code;
+}
+
+trs_plan_options resolve(const trs_plan_options* o) {
+  trs_plan_options r;
+  trs_plan_options_default(&r);
+  if (o) r = *o;
+  return r;
+}
+
+bool bad_dims(int32_t m, int32_t n) { return m < 0 || n < 0; }
+
+}  // namespace
+
+extern "C" {
+
+void trs_plan_options_default(trs_plan_options* o) {
+  if (!o) return;
+  o->mfma_tc = 1;
+  o->mfma_sptc = 1;
+  o->sptc_min_fill = 0.25f;
+  o->task_nnz = 0;
+}
+
+const char* trs_last_error(void) { return g_error.c_str(); }
+
+int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
+  if (!f || !out) return report(fail(TRS_EINVAL, "trs_plan_create: NULL argument"));
+  *out = nullptr;
+  if (bad_dims(m, n)) return report(fail(TRS_EINVAL, "trs_plan_create: negative m or n"));
+  if (!f->canonical)
+    return report(fail(TRS_ENOTCANON, "trs_plan_create: input rows were not strictly increasing; the format "
+                                      "arrays cannot describe duplicate or unsorted entries"));
+  const trs_plan_options o = resolve(opt);
+  Lowering L;
+  L.m = m;
+  L.n = n;
+  const size_t approx = f->t_val.size() + f->c_val.size() + f->cs_val.size() + f->s_val.size() / 2 + f->spill_val.size();
+  L.row.reserve(approx); L.col.reserve(approx); L.val.reserve(approx);
+  lower_tc(L, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
+           f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
+  lower_residual(L, f->c_off.data(), f->c_row.data(), (int64_t)f->c_row.size(), f->c_col.data(), f->c_val.data(),
+                 nullptr, (int64_t)f->c_col.size());
+  lower_residual(L, f->cs_off.data(), f->cs_row.data(), (int64_t)f->cs_row.size(), f->cs_col.data(),
+                 f->cs_val.data(), nullptr, (int64_t)f->cs_col.size());
+  lower_groups(L, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
+               f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
+  for (size_t i = 0; i < f->spill_row.size() && L.st.ok(); ++i) L.add(f->spill_row[i], f->spill_col[i], f->spill_val[i]);
+  return report(finalize(L, o, false, false, out));
+}
+
+int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_options* opt, trs_plan** out) {
+  if (!a || !out) return report(fail(TRS_EINVAL, "trs_plan_create_parallel: NULL argument"));
+  *out = nullptr;
+  if (bad_dims(a->m, a->n)) return report(fail(TRS_EINVAL, "negative m or n"));
+  const trs_plan_options o = resolve(opt);
+  // structural checks (mGCN_online.cpp:858-932)
+  if (a->n_t_row_offset < 1 || a->n_t_row_offset - 1 > a->n_t_window_row || a->n_t_binary < 2 * (a->n_t_block_offset - 1))
+    return report(fail(TRS_EINVAL, "TC arrays have inconsistent sizes"));
+  const int64_t nparts = a->n_t_row_offset - 1;
+  for (int64_t p = 0; p < nparts; ++p) {
+    const int32_t s0 = a->t_row_offset[p], s1 = a->t_row_offset[p + 1];
+    if (s0 < 0 || s1 < s0 || s1 >= a->n_t_block_offset || (int64_t)s1 * 8 > a->n_t_column)
+      return report(fail(TRS_EINVAL, "t_row_offset out of range"));
+  }
+  if (a->n_c_row_offsets < a->n_c_row + 1 || a->n_cs_row_offsets < a->n_cs_row + 1)
+    return report(fail(TRS_EINVAL, "residual offsets shorter than part lists"));
+  Lowering L;
+  L.m = a->m;
+  L.n = a->n;
+  lower_tc(L, a->t_row_offset, nparts, a->t_block_offset, a->t_column, nullptr, a->t_value, a->n_t_value,
+           a->t_window_row, a->t_binary, o.mfma_tc != 0);
+  lower_residual(L, a->c_row_offsets, a->c_row, a->n_c_row, a->c_column, nullptr, a->c_value, a->n_c_column);
+  lower_residual(L, a->cs_row_offsets, a->cs_row, a->n_cs_row, a->cs_column, nullptr, a->cs_value, a->n_cs_column);
+  if (a->use_packed_tiles) {
+    lower_packed(L, a->s_tile_column, a->s_packed_a, a->s_packed_meta, a->tiles, a->s_window_tile_offset,
+                 a->n_s_window_tile_offset - 1, a->window, o.mfma_sptc != 0, o.sptc_min_fill);
+  } else {
+    lower_groups(L, a->s_column, a->s_value, a->s_pos, a->groups, nullptr, a->s_offsets, a->n_s_offsets - 1,
+                 a->window, o.mfma_sptc != 0, o.sptc_min_fill);
+  }
+  for (int64_t i = 0; i < a->spill_count && L.st.ok(); ++i) L.add(a->spill_row[i], a->spill_col[i], a->spill_val[i]);
+  return report(finalize(L, o, false, false, out));
+}
+
+int trs_plan_create_sptc(const int32_t* s_column, const float* s_value, const int8_t* s_pos, int64_t groups,
+                         const int32_t* s_window, const int32_t* s_offsets, int64_t n_s_offsets, int32_t window,
+                         int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
+  if (!out) return report(fail(TRS_EINVAL, "trs_plan_create_sptc: NULL out"));
+  *out = nullptr;
+  if (bad_dims(m, n) || window <= 0 || groups < 0 || (groups > 0 && (!s_column || !s_value || !s_pos)))
+    return report(fail(TRS_EINVAL, "trs_plan_create_sptc: bad arguments"));
+  if (!s_window && (!s_offsets || n_s_offsets < 1 || s_offsets[0] != 0 || s_offsets[n_s_offsets - 1] != groups))
+    return report(fail(TRS_EINVAL, "s_offsets must start with 0 and end with the group count"));
+  if (s_offsets && !s_window)
+    for (int64_t w = 0; w + 1 < n_s_offsets; ++w)
+      if (s_offsets[w + 1] < s_offsets[w]) return report(fail(TRS_EINVAL, "s_offsets must be non-decreasing"));
+  const trs_plan_options o = resolve(opt);
+  Lowering L;
+  L.m = m;
+  L.n = n;
+  lower_groups(L, s_column, s_value, s_pos, groups, s_window, s_window ? nullptr : s_offsets,
+               s_window ? 0 : n_s_offsets - 1, window, o.mfma_sptc != 0 && !s_window, o.sptc_min_fill);
+  return report(finalize(L, o, false, false, out));
+}
+
+int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_packed_a, const int32_t* s_packed_meta,
+                                const int32_t* s_window_tile_offset, int64_t tiles, int64_t n_wto, int32_t window,
+                                int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
+  if (!out) return report(fail(TRS_EINVAL, "trs_plan_create_sptc_packed: NULL out"));
+  *out = nullptr;
+  if (bad_dims(m, n) || window <= 0 || window > 16 || n_wto < 2 || !s_window_tile_offset)
+    return report(fail(TRS_EINVAL, "trs_plan_create_sptc_packed: bad arguments"));
+  const trs_plan_options o = resolve(opt);
+  Lowering L;
+  L.m = m;
+  L.n = n;
+  lower_packed(L, s_tile_column, s_packed_a, s_packed_meta, tiles, s_window_tile_offset, n_wto - 1, window,
+               o.mfma_sptc != 0, o.sptc_min_fill);
+  return report(finalize(L, o, false, false, out));
+}
+
+int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_t* val, int32_t m, int32_t n,
+                        const trs_plan_options* opt, trs_plan** out) {
+  if (!out) return report(fail(TRS_EINVAL, "trs_plan_create_csr: NULL out"));
+  *out = nullptr;
+  if (bad_dims(m, n) || !rowptr) return report(fail(TRS_EINVAL, "trs_plan_create_csr: bad arguments"));
+  if (rowptr[0] != 0) return report(fail(TRS_EINVAL, "rowptr must start at 0"));
+  for (int32_t r = 0; r < m; ++r)
+    if (rowptr[r + 1] < rowptr[r]) return report(fail(TRS_EINVAL, "rowptr must be non-decreasing"));
+  const int64_t nnz = rowptr[m];
+  if (nnz > 0 && (!col || !val)) return report(fail(TRS_EINVAL, "trs_plan_create_csr: NULL col/val"));
+  const trs_plan_options o = resolve(opt);
+  Lowering L;
+  L.m = m;
+  L.n = n;
+  L.row.resize(nnz); L.col.resize(nnz); L.val.resize(nnz);
+  for (int32_t r = 0; r < m; ++r)
+    for (int32_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
+      if (col[e] < 0 || col[e] >= n) return report(fail(TRS_ERANGE, "column index outside [0, n)"));
+      L.row[e] = r; L.col[e] = col[e]; L.val[e] = f16_to_f32(val[e]);
+    }
+  return report(finalize(L, o, true, true, out));
+}
+
+int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s) {
+  if (!p || !s) return report(fail(TRS_EINVAL, "trs_plan_stats_get: NULL argument"));
+  *s = p->stats;
+  return TRS_OK;
+}
+
+void trs_plan_free(trs_plan* p) { delete p; }
+
+int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K) {
+  if (!p || K <= 0) return 0;
+  return (int64_t)p->dp.partial_slots * K * (int64_t)sizeof(float);
+}
+
+static int check_call(const trs_plan* p, int32_t K) {
+  if (!p) return report(fail(TRS_EINVAL, "NULL plan"));
+  if (K < 0) return report(fail(TRS_EINVAL, "K must be non-negative"));
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+    return report(fail(TRS_EDEVICE, "the current HIP device is not the device the plan was created on"));
+  return TRS_OK;
+}
+
+static int spmm_impl(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc, void* ws,
+                     int64_t ws_bytes, void* stream, hipEvent_t* ev) {
+  int rc = check_call(p, K);
+  if (rc) return rc;
+  if (p->csr_only) return report(fail(TRS_EINVAL, "trs_spmm_f16: plan was created for SDDMM (trs_plan_create_csr)"));
+  if (K == 0 || p->dp.m == 0) return TRS_OK;
+  if (!C || (p->dp.n > 0 && !B) || ldb < K || ldc < K)
+    return report(fail(TRS_EINVAL, "trs_spmm_f16: NULL operand or leading dimension < K"));
+  const int64_t need = trs_spmm_workspace_bytes(p, K);
+  if (ws_bytes < need || (need > 0 && !ws))
+    return report(fail(TRS_EINVAL, "trs_spmm_f16: workspace smaller than trs_spmm_workspace_bytes"));
+  const hipError_t e =
+      trs::launch_spmm(p->dp, B, ldb, K, C, ldc, static_cast<float*>(ws), static_cast<hipStream_t>(stream), ev);
+  if (e != hipSuccess) return report(fail(TRS_EDEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e)));
+  return TRS_OK;
+}
+
+int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc, void* ws,
+                 int64_t ws_bytes, void* stream) {
+  return spmm_impl(p, B, ldb, K, C, ldc, ws, ws_bytes, stream, nullptr);
+}
+
+int trs_spmm_f16_kernel_ms(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
+                           void* ws, int64_t ws_bytes, void* stream, int32_t iters, float* ms) {
+  if (!ms || iters <= 0) return report(fail(TRS_EINVAL, "trs_spmm_f16_kernel_ms: needs ms[3] and iters > 0"));
+  ms[0] = ms[1] = ms[2] = 0.f;
+  hipEvent_t ev[4];
+  for (auto& e : ev)
+    if (hipEventCreate(&e) != hipSuccess) return report(fail(TRS_EDEVICE, "hipEventCreate failed"));
+  int rc = TRS_OK;
+  for (int i = 0; i < iters && rc == TRS_OK; ++i) {
+    rc = spmm_impl(p, B, ldb, K, C, ldc, ws, ws_bytes, stream, ev);
+    if (rc) break;
+    (void)hipEventSynchronize(ev[3]);
+    for (int k = 0; k < 3; ++k) {
+      float t = 0.f;
+      (void)hipEventElapsedTime(&t, ev[k], ev[k + 1]);
+      ms[k] += t / (float)iters;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  return rc;
+}
+
+int trs_spmm_f16_timed(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc, void* ws,
+                       int64_t ws_bytes, void* stream, int32_t warmup, int32_t iters, float* ms_avg) {
+  if (ms_avg) *ms_avg = 0.f;
+  if (iters <= 0) return report(fail(TRS_EINVAL, "iters must be positive"));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int i = 0; i < warmup; ++i) {
+    int rc = trs_spmm_f16(p, B, ldb, K, C, ldc, ws, ws_bytes, stream);
+    if (rc) return rc;
+  }
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+    return report(fail(TRS_EDEVICE, "hipEventCreate failed"));
+  (void)hipEventRecord(e0, s);
+  int rc = TRS_OK;
+  for (int i = 0; i < iters && rc == TRS_OK; ++i) rc = trs_spmm_f16(p, B, ldb, K, C, ldc, ws, ws_bytes, stream);
+  (void)hipEventRecord(e1, s);
+  (void)hipEventSynchronize(e1);
+  float ms = 0.f;
+  (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (rc) return rc;
+  if (ms_avg) *ms_avg = ms / (float)iters;
+  return TRS_OK;
+}
+
+int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int32_t K,
+                  float* out, void* stream) {
+  int rc = check_call(p, K);
+  if (rc) return rc;
+  if (!p->csr_only) return report(fail(TRS_EINVAL, "trs_sddmm_f16: needs a plan from trs_plan_create_csr"));
+  if (p->dp.nnz_csr == 0) return TRS_OK;
+  if (!out || !X || !Y || (K > 0 && (ldx < K || ldy < K)))
+    return report(fail(TRS_EINVAL, "trs_sddmm_f16: NULL operand or leading dimension < K"));
+  if (K == 0) {
+    if (hipMemsetAsync(out, 0, p->dp.nnz_csr * sizeof(float), static_cast<hipStream_t>(stream)) != hipSuccess)
+      return report(fail(TRS_EDEVICE, "hipMemsetAsync failed"));
+    return TRS_OK;
+  }
+  const hipError_t e = trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return report(fail(TRS_EDEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e)));
+  return TRS_OK;
+}
+
+}  // extern "C"

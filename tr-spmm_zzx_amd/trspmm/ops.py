@@ -1,0 +1,213 @@
+"""Device-level Python API over the C ABI: Format (builder output), Plan, spmm, sddmm.
+
+Tensors handed to ``Plan.spmm`` / ``Plan.sddmm`` must already live on the GPU (fp16 operands,
+float32 outputs); work is enqueued on the current torch stream.  Everything runs through
+libtrspmm.so; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _native as nat
+
+# reference return-list names and element types (TR-source/Block/block_online.cpp:844-870)
+SLOT_NAMES = [
+    "t_rowkNew_offset", "t_blockNew_offset", "t_columnNew", "t_valueNew", "t_window_rowNew", "t_atomicNew",
+    "t_binaryNew", "c_rowNew_offset", "c_rowNew", "c_atomicNew", "c_columnNew", "c_valueNew",
+    "c_rowNew_offset_residue", "c_rowNew_residue", "c_atomicNew_residue", "c_columnNew_residue",
+    "c_valueNew_residue", "s_columns", "s_masks", "s_values", "s_pos", "s_window", "s_offsets", "s_tile_window",
+    "s_tile_group", "s_tile_columns", "s_packed_a", "s_packed_meta", "s_window_tile_offset",
+    "spill_row", "spill_col", "spill_val",
+]
+SLOT_DTYPES = [np.int32, np.int32, np.int32, np.float32, np.int32, np.int32, np.int64,
+               np.int32, np.int32, np.int32, np.int32, np.float32,
+               np.int32, np.int32, np.int32, np.int32, np.float32,
+               np.int32, np.uint8, np.float32, np.int8, np.int32, np.int32, np.int32, np.int32, np.int32,
+               np.int32, np.int32, np.int32, np.int32, np.int32, np.float32]
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data if a.size else 0
+
+
+class Format:
+    """Output of the format builder (owns a C ``trs_format``)."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            nat.lib().trs_format_free(h)
+            self._h = ctypes.c_void_p(0)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def slot(self, i: int) -> np.ndarray:
+        data = ctypes.c_void_p()
+        n = ctypes.c_int64()
+        nat.check(nat.lib().trs_format_slot(self._h, i, ctypes.byref(data), ctypes.byref(n)), "trs_format_slot")
+        a = np.empty(n.value, dtype=SLOT_DTYPES[i])
+        if n.value:
+            ctypes.memmove(a.ctypes.data, data.value, n.value * a.itemsize)
+        return a
+
+    @property
+    def window(self) -> int:
+        return int(nat.lib().trs_format_window(self._h))
+
+    @property
+    def elapsed(self) -> float:
+        return float(nat.lib().trs_format_elapsed(self._h))
+
+    @property
+    def canonical(self) -> bool:
+        return bool(nat.lib().trs_format_canonical(self._h))
+
+    def arrays(self) -> list:
+        """The 29 reference arrays with the reference's shapes."""
+        a = [self.slot(i) for i in range(29)]
+        w = self.window
+        g, t = a[21].shape[0], a[23].shape[0]
+        a[17] = a[17].reshape(g, 4)
+        a[18] = a[18].reshape(g, w)
+        a[19] = a[19].reshape(g, w, 2)
+        a[20] = a[20].reshape(g, w, 2)
+        a[25] = a[25].reshape(t, 16)
+        a[26] = a[26].reshape(t, 8, 4, 2)
+        a[27] = a[27].reshape(t, 8)
+        return a
+
+    def spill(self) -> tuple:
+        return self.slot(29), self.slot(30), self.slot(31)
+
+
+def build_format(rowptr, col, val, part_t: int = 32, part_c: int = 32, short_size: int = 3, density: int = 8,
+                 window: int = 16, wide: int = 16, tc_min_util: float = 0.0, sptc_min_util: float = 0.5,
+                 sptc_threshold: int = 12, skip_tc: Optional[bool] = None, unit_min_nnz: Optional[int] = None,
+                 num_threads: int = 0) -> Format:
+    """Run the builder (block_online.cpp:545-871 semantics).  ``skip_tc`` / ``unit_min_nnz`` of
+    None read LIBRA_SKIP_TC / LIBRA_SPTC_UNIT_MIN_NNZ from the environment like the reference."""
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    col = np.ascontiguousarray(col, dtype=np.int32)
+    val = np.ascontiguousarray(val, dtype=np.float32)
+    p = nat.BuildParams()
+    nat.lib().trs_build_params_default(ctypes.byref(p))
+    p.part_size_t, p.part_size_c, p.short_size, p.density = part_t, part_c, short_size, density
+    p.window, p.wide, p.tc_min_util, p.sptc_min_util = window, wide, tc_min_util, sptc_min_util
+    p.sptc_threshold = sptc_threshold
+    p.skip_tc = -1 if skip_tc is None else int(bool(skip_tc))
+    p.sptc_unit_min_nnz = -1 if unit_min_nnz is None else int(unit_min_nnz)
+    p.num_threads = num_threads
+    h = ctypes.c_void_p()
+    nat.check(nat.lib().trs_build_online(_ptr(rowptr), _ptr(col), _ptr(val), rowptr.shape[0] - 1, col.shape[0],
+                                         ctypes.byref(p), ctypes.byref(h)), "trs_build_online")
+    return Format(h.value)
+
+
+def _options(mfma_tc: bool, mfma_sptc: bool, sptc_min_fill: float, task_nnz: int) -> nat.PlanOptions:
+    o = nat.PlanOptions()
+    nat.lib().trs_plan_options_default(ctypes.byref(o))
+    o.mfma_tc, o.mfma_sptc, o.sptc_min_fill, o.task_nnz = int(mfma_tc), int(mfma_sptc), sptc_min_fill, task_nnz
+    return o
+
+
+def _stream_ptr(stream) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class Plan:
+    """Device-resident execution plan (owns a C ``trs_plan``)."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            nat.lib().trs_plan_free(h)
+            self._h = ctypes.c_void_p(0)
+
+    @classmethod
+    def from_format(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
+                    sptc_min_fill: float = 0.25, task_nnz: int = 0) -> "Plan":
+        o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz)
+        h = ctypes.c_void_p()
+        nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
+        return cls(h.value)
+
+    @classmethod
+    def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0) -> "Plan":
+        rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+        col = np.ascontiguousarray(col, dtype=np.int32)
+        val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
+        o = _options(False, False, 1.0, task_nnz)
+        h = ctypes.c_void_p()
+        nat.check(nat.lib().trs_plan_create_csr(_ptr(rowptr), _ptr(col), _ptr(val), m, n, ctypes.byref(o),
+                                                ctypes.byref(h)), "trs_plan_create_csr")
+        return cls(h.value)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def stats(self) -> dict:
+        s = nat.PlanStats()
+        nat.check(nat.lib().trs_plan_stats_get(self._h, ctypes.byref(s)), "trs_plan_stats_get")
+        return {k: int(getattr(s, k)) for k, _ in nat.PlanStats._fields_}
+
+    def workspace_bytes(self, K: int) -> int:
+        return int(nat.lib().trs_spmm_workspace_bytes(self._h, K))
+
+    def spmm(self, B: torch.Tensor, out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+             stream=None) -> torch.Tensor:
+        """C = A B for B [n, K] fp16 on the GPU; returns float32 [m, K]."""
+        st = self.stats()
+        if not (B.is_cuda and B.dtype == torch.float16 and B.dim() == 2 and B.shape[0] == st["n"]):
+            raise ValueError(f"B must be a CUDA fp16 tensor of shape [{st['n']}, K]")
+        if B.stride(1) != 1:
+            B = B.contiguous()
+        K = B.shape[1]
+        if out is None:
+            out = torch.empty((st["m"], K), dtype=torch.float32, device=B.device)
+        if not (out.is_cuda and out.dtype == torch.float32 and tuple(out.shape) == (st["m"], K) and out.stride(1) == 1):
+            raise ValueError("out must be a CUDA float32 tensor [m, K] with unit column stride")
+        need = self.workspace_bytes(K)
+        if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+            workspace = torch.empty(need, dtype=torch.uint8, device=B.device)
+        ws_ptr = workspace.data_ptr() if need else 0
+        nat.check(nat.lib().trs_spmm_f16(self._h, B.data_ptr(), B.stride(0), K, out.data_ptr(), out.stride(0),
+                                         ws_ptr, need, _stream_ptr(stream)), "trs_spmm_f16")
+        return out
+
+    def sddmm(self, X: torch.Tensor, Y: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """out[e] = X[row_e] . Y[col_e] for every stored entry (CSR order); float32 [nnz]."""
+        st = self.stats()
+        for name, t, rows in (("X", X, st["m"]), ("Y", Y, st["n"])):
+            if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 2 and t.shape[0] == rows):
+                raise ValueError(f"{name} must be a CUDA fp16 tensor with {rows} rows")
+        if X.shape[1] != Y.shape[1]:
+            raise ValueError("X and Y need the same feature width")
+        X = X if X.stride(1) == 1 else X.contiguous()
+        Y = Y if Y.stride(1) == 1 else Y.contiguous()
+        if out is None:
+            out = torch.empty(st["csr_nnz"], dtype=torch.float32, device=X.device)
+        nat.check(nat.lib().trs_sddmm_f16(self._h, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), X.shape[1],
+                                          out.data_ptr(), _stream_ptr(stream)), "trs_sddmm_f16")
+        return out
+
+
+def spmm(plan: Plan, B: torch.Tensor, **kw) -> torch.Tensor:
+    return plan.spmm(B, **kw)
+
+
+def sddmm(plan: Plan, X: torch.Tensor, Y: torch.Tensor, **kw) -> torch.Tensor:
+    return plan.sddmm(X, Y, **kw)
