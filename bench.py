@@ -93,6 +93,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}): this build has no multi-GPU path; "
@@ -122,6 +124,14 @@ def main():
     need = plan.workspace_bytes(K)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
 
+    if args.calibrate_copy_mib:
+        n_el = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n_el, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         plan.spmm(B, out=C, workspace=ws)
     torch.cuda.synchronize()

@@ -56,14 +56,28 @@ struct BFrag<1> {
   __device__ __forceinline__ float dot(const BFrag& o) const { return (float)v * (float)o.v; }
 };
 
-template <int VEC>
+// NT: non-temporal (streaming) store, so written output does not evict gathered B rows from L2.
+template <int VEC, bool NT = false>
 __device__ __forceinline__ void store_vec(float* dst, const float (&acc)[VEC]) {
   if constexpr (VEC == 8) {
-    reinterpret_cast<float4_t*>(dst)[0] = float4_t{acc[0], acc[1], acc[2], acc[3]};
-    reinterpret_cast<float4_t*>(dst)[1] = float4_t{acc[4], acc[5], acc[6], acc[7]};
+    const float4_t lo{acc[0], acc[1], acc[2], acc[3]}, hi{acc[4], acc[5], acc[6], acc[7]};
+    if constexpr (NT) {
+      __builtin_nontemporal_store(lo, reinterpret_cast<float4_t*>(dst));
+      __builtin_nontemporal_store(hi, reinterpret_cast<float4_t*>(dst) + 1);
+    } else {
+      reinterpret_cast<float4_t*>(dst)[0] = lo;
+      reinterpret_cast<float4_t*>(dst)[1] = hi;
+    }
   } else {
-    dst[0] = acc[0];
+    if constexpr (NT) __builtin_nontemporal_store(acc[0], dst);
+    else dst[0] = acc[0];
   }
+}
+
+template <bool NT, class T>
+__device__ __forceinline__ T load_stream(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
 }
 
 template <int VEC>
@@ -73,7 +87,7 @@ __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
 }
 
 // Accumulate entries [p0, p1) of one row into acc (U loads in flight).
-template <int VEC, int U>
+template <int VEC, int U, bool NT = false>
 __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
                                                const uint16_t* __restrict__ B, int64_t ldb, int f, bool active,
                                                int p0, int p1, float (&acc)[VEC]) {
@@ -84,8 +98,8 @@ __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, 
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const bool in = p + i < p1;
-      cc[i] = in ? col[p + i] : 0;
-      vv[i] = in ? h2f(val[p + i]) : 0.f;
+      cc[i] = in ? load_stream<NT>(col + p + i) : 0;
+      vv[i] = in ? h2f(load_stream<NT>(val + p + i)) : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -98,30 +112,48 @@ __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, 
 }
 
 // ------------------------------------------------------------------------------------------------
-template <int VEC, int LPG, int U>
+// Streaming-hint bits of DevicePlan::streaming: non-temporal A-stream loads / C stores.
+constexpr int kNtLoads = 1;
+constexpr int kNtStores = 2;
+
+template <int VEC, int LPG, int U, int NT>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                     int K, float* __restrict__ C, int64_t ldc,
                                                     float* __restrict__ partial) {
   constexpr int GPW = 64 / LPG;
+  constexpr bool NTL = (NT & kNtLoads) != 0;
+  constexpr bool NTS = (NT & kNtStores) != 0;
+  // row pointers of each lane group's task, preloaded once so a row flush never waits on a
+  // dependent global load (tasks carry at most kTaskRows rows)
+  __shared__ int s_rp[4][GPW][kTaskRows + 1];
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int task_id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
-  if (task_id >= P.ntasks) return;
-  const int f = blockIdx.y * (LPG * VEC) + (lane % LPG) * VEC;
+  const int grp = lane / LPG;
+  const int li = lane % LPG;
+  const int task_id = (blockIdx.x * 4 + wave) * GPW + grp;
+  const bool valid = task_id < P.ntasks;
+  const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
+  int* rp = s_rp[wave][grp];
+  if (valid && t.row_end >= 0)
+    for (int j = li; j <= t.row_end - t.row_begin; j += LPG) rp[j] = P.rowptr[t.row_begin + j];
+  __syncthreads();
+  if (!valid) return;
+
+  const int f = blockIdx.y * (LPG * VEC) + li * VEC;
   const bool active = f < K;
-  const Task t = P.tasks[task_id];
   const int32_t* __restrict__ col = P.col;
   const uint16_t* __restrict__ val = P.val;
   float acc[VEC];
   zero_acc(acc);
 
-  if (t.row_end < 0) {   // piece of a split row -> partial slot
-    accumulate_row<VEC, U>(col, val, B, ldb, f, active, t.nz_begin, t.nz_end, acc);
+  if (t.row_end < 0) {   // piece of a split row -> partial slot (re-read by the fixup: keep cached)
+    accumulate_row<VEC, U, NTL>(col, val, B, ldb, f, active, t.nz_begin, t.nz_end, acc);
     if (active) store_vec<VEC>(partial + (int64_t)(~t.row_end) * K + f, acc);
     return;
   }
   // whole rows [row_begin, row_end): stream entries, flush a row when its end is crossed
-  int r = t.row_begin;
-  int rend = P.rowptr[r + 1];
+  int r = 0;                       // row index relative to row_begin
+  int rend = rp[1];
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U];
     float vv[U];
@@ -129,8 +161,8 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const bool in = p + i < t.nz_end;
-      cc[i] = in ? col[p + i] : 0;
-      vv[i] = in ? h2f(val[p + i]) : 0.f;
+      cc[i] = in ? load_stream<NTL>(col + p + i) : 0;
+      vv[i] = in ? h2f(load_stream<NTL>(val + p + i)) : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -141,25 +173,27 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
     for (int i = 0; i < U; ++i) {
       if (p + i < t.nz_end) {
         while (p + i >= rend) {
-          if (active) store_vec<VEC>(C + (int64_t)r * ldc + f, acc);
+          if (active) store_vec<VEC, NTS>(C + (int64_t)(t.row_begin + r) * ldc + f, acc);
           zero_acc(acc);
           ++r;
-          rend = P.rowptr[r + 1];
+          rend = rp[r + 1];
         }
         bb[i].fma(acc, vv[i]);
       }
     }
   }
-  for (; r < t.row_end; ++r) {
-    if (active) store_vec<VEC>(C + (int64_t)r * ldc + f, acc);
+  for (; t.row_begin + r < t.row_end; ++r) {
+    if (active) store_vec<VEC, NTS>(C + (int64_t)(t.row_begin + r) * ldc + f, acc);
     zero_acc(acc);
   }
 }
 
+// C[row] = sum of a split row's partial slots, in slot order (deterministic), 4 slots in flight.
 template <int VEC, int LPG>
 __global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
                                                     const float* __restrict__ partial) {
   constexpr int GPW = 64 / LPG;
+  constexpr int SU = 4;
   const int lane = threadIdx.x & 63;
   const int id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
   if (id >= P.nfixups) return;
@@ -168,12 +202,60 @@ __global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* 
   const Fixup x = P.fixups[id];
   float acc[VEC];
   zero_acc(acc);
-  for (int s = 0; s < x.slots; ++s) {
-    const float* src = partial + (int64_t)(x.slot_begin + s) * K + f;
+  for (int s = 0; s < x.slots; s += SU) {
+    float v[SU][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) acc[i] += src[i];
+    for (int u = 0; u < SU; ++u) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[u][i] = 0.f;
+      if (s + u < x.slots) {
+        const float* src = partial + (int64_t)(x.slot_begin + s + u) * K + f;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[u][i] = src[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < SU; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] += v[u][i];
   }
   store_vec<VEC>(C + (int64_t)x.row * ldc + f, acc);
+}
+
+// Split rows with many slots: one workgroup per row.  Lane group g sums slots g, g + G, ... (in
+// order), then the G group sums are combined by a fixed binary tree in LDS (deterministic).
+template <int VEC, int LPG>
+__global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
+                                                         const float* __restrict__ partial) {
+  constexpr int G = 256 / LPG;
+  __shared__ float red[G][LPG * VEC];
+  const int g = threadIdx.x / LPG;
+  const int li = threadIdx.x % LPG;
+  const int f = blockIdx.y * (LPG * VEC) + li * VEC;
+  const Fixup x = P.wfixups[blockIdx.x];
+  float acc[VEC];
+  zero_acc(acc);
+  if (f < K) {
+    for (int s = g; s < x.slots; s += G) {
+      const float* src = partial + (int64_t)(x.slot_begin + s) * K + f;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] += src[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) red[g][li * VEC + i] = acc[i];
+  __syncthreads();
+  for (int h = G / 2; h > 0; h >>= 1) {
+    if (g < h)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) red[g][li * VEC + i] += red[g + h][li * VEC + i];
+    __syncthreads();
+  }
+  if (g == 0 && f < K) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) acc[i] = red[0][li * VEC + i];
+    store_vec<VEC>(C + (int64_t)x.row * ldc + f, acc);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -242,11 +324,11 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
 
   // residual rows of this window, added on top of the MFMA share
   const int gs = KC / VEC;         // threads per row group
-  const int groups = 256 / gs;
+  const int groups = 256 / gs;     // threads past groups * gs sit this phase out
   const int g = threadIdx.x / gs;
   const int ff = (threadIdx.x % gs) * VEC;
   const int f = fbase + ff;
-  for (int rl = g; rl < 16; rl += groups) {
+  for (int rl = g; g < groups && rl < 16; rl += groups) {
     const int row = w.row0 + rl;
     if (row >= P.m) break;
     float racc[VEC];
@@ -341,13 +423,24 @@ template <int VEC>
 hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                            float* partial, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
-  const int lpg = lanes_for(K, VEC);
+  int lpg = lanes_for(K, VEC);
+  // a plan may ask for fewer lanes per group: several feature passes, each gathering a narrower
+  // slice of B (smaller working set per pass)
+  while (p.feature_lanes > 0 && lpg > p.feature_lanes && lpg > 1) lpg >>= 1;
   const int fpp = lpg * VEC;
   const int passes = (K + fpp - 1) / fpp;
   if (p.ntasks > 0) {
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb, passes);
-#define TRS_TASKS(L) case L: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break;
+#define TRS_TASKS(L)                                                                                      \
+  case L:                                                                                                 \
+    switch (p.streaming & 3) {                                                                            \
+      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 0>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 1>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 2>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 3>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+    }                                                                                                     \
+    break;
     switch (lpg) { TRS_TASKS(1) TRS_TASKS(2) TRS_TASKS(4) TRS_TASKS(8) TRS_TASKS(16) TRS_TASKS(32) TRS_TASKS(64) }
 #undef TRS_TASKS
   }
@@ -368,6 +461,12 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 #define TRS_FIX(L) case L: hipLaunchKernelGGL((k_spmm_fixup<VEC, L>), grid, dim3(256), 0, s, p, K, C, ldc, partial); break;
     switch (lpg) { TRS_FIX(1) TRS_FIX(2) TRS_FIX(4) TRS_FIX(8) TRS_FIX(16) TRS_FIX(32) TRS_FIX(64) }
 #undef TRS_FIX
+  }
+  if (p.nwfixups > 0) {
+    dim3 grid(p.nwfixups, passes);
+#define TRS_WFIX(L) case L: hipLaunchKernelGGL((k_spmm_fixup_wide<VEC, L>), grid, dim3(256), 0, s, p, K, C, ldc, partial); break;
+    switch (lpg) { TRS_WFIX(1) TRS_WFIX(2) TRS_WFIX(4) TRS_WFIX(8) TRS_WFIX(16) TRS_WFIX(32) TRS_WFIX(64) }
+#undef TRS_WFIX
   }
   if (ev) (void)hipEventRecord(ev[3], s);
   return hipGetLastError();

@@ -13,6 +13,11 @@ struct Task { int32_t row_begin, row_end, nz_begin, nz_end; };
 // A split row: C[row] = sum of partial slots [slot_begin, slot_begin + slots) in order.
 struct Fixup { int32_t row, slot_begin, slots, pad; };
 
+// Rows per multi-row residual task (the task kernel preloads their row pointers into LDS).
+constexpr int kTaskRows = 32;
+// Split rows with more slots than this are summed by one workgroup each.
+constexpr int kWideFixupSlots = 16;
+
 // A window handled by the MFMA window kernel: 16 output rows starting at row0 (rows >= m are
 // dropped), dense 16x16 fp16 tiles [tile_begin, tile_end), plus that window's residual rows.
 struct MfmaWindow { int32_t row0, tile_begin, tile_end, pad; };
@@ -25,14 +30,18 @@ struct DevicePlan {
   const uint16_t* val = nullptr;
   const Task* tasks = nullptr;
   int32_t ntasks = 0;
-  const Fixup* fixups = nullptr;
+  const Fixup* fixups = nullptr;      // split rows with <= kWideFixupSlots slots
   int32_t nfixups = 0;
+  const Fixup* wfixups = nullptr;     // split rows with more slots
+  int32_t nwfixups = 0;
   int32_t partial_slots = 0;
   const MfmaWindow* mwin = nullptr;
   int32_t nmwin = 0;
   const int32_t* tile_cols = nullptr;  // [tiles][16]
   const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16
   int32_t ntiles = 0;
+  int32_t feature_lanes = 0;   // lanes per residual lane group (0 = automatic)
+  int32_t streaming = 0;       // bit 0: non-temporal A-stream loads, bit 1: non-temporal C stores
 };
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.

@@ -315,9 +315,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
     }
   }
 
-  // Hand a tile-owning block back to the residual path when one of its rows is very long
-  // (the window kernel walks each residual row with one lane group).
-  const int row_cap = 4096;
+  // Hand a tile-owning block back to the residual path when one of its residual rows is long:
+  // the window kernel walks each residual row with one lane group, so a long row would keep the
+  // whole workgroup waiting (hub windows of power-law graphs).
+  const int row_cap = opt.window_row_cap > 0 ? opt.window_row_cap : 128;
   std::vector<Lowering::Tile> kept_tiles;
   std::vector<trs::MfmaWindow> mwin;
   {
@@ -361,11 +362,20 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   }
 
   // residual tasks over rows not owned by an MFMA window
-  const int S = opt.task_nnz > 0 ? opt.task_nnz : 64;
-  const int piece_max = std::max(S, 256);
-  const int rows_cap = 64;
+  // Entries per packed task: short rows want small tasks (more lane groups in flight, fewer row
+  // flushes per group), long rows want larger ones.  Measured on MI355X: 32 for a degree-4 mesh,
+  // 128 for R-MAT (mean non-empty row ~49) -- about four mean rows per task.
+  int S = opt.task_nnz;
+  if (S <= 0) {
+    int64_t nonempty = 0;
+    for (int32_t q = 0; q < m; ++q) nonempty += rowptr[q + 1] > rowptr[q];
+    const double mean = nonempty ? (double)nent / (double)nonempty : 1.0;
+    S = (int)std::min(128.0, std::max(32.0, 4.0 * mean));
+  }
+  const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
+  const int rows_cap = trs::kTaskRows;
   std::vector<trs::Task> pieces, packed;
-  std::vector<trs::Fixup> fix;
+  std::vector<trs::Fixup> fix, wfix;
   int32_t slots = 0;
   int64_t split_rows = 0;
   int32_t r = 0;
@@ -381,7 +391,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
         pieces.push_back({r, ~slots, b, e});
         ++slots;
       }
-      fix.push_back({r, base, np, 0});
+      (np > trs::kWideFixupSlots ? wfix : fix).push_back({r, base, np, 0});
       ++split_rows;
       ++r;
       continue;
@@ -421,6 +431,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   const size_t o_val = push_bytes(blob, val);
   const size_t o_tasks = push_bytes(blob, tasks);
   const size_t o_fix = push_bytes(blob, fix);
+  const size_t o_wfix = push_bytes(blob, wfix);
   const size_t o_mwin = push_bytes(blob, mwin);
   const size_t o_tcol = push_bytes(blob, tile_cols);
   const size_t o_ta = push_bytes(blob, tile_a);
@@ -454,12 +465,18 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   d.ntasks = (int32_t)tasks.size();
   d.fixups = reinterpret_cast<const trs::Fixup*>(base + o_fix);
   d.nfixups = (int32_t)fix.size();
+  d.wfixups = reinterpret_cast<const trs::Fixup*>(base + o_wfix);
+  d.nwfixups = (int32_t)wfix.size();
   d.partial_slots = slots;
   d.mwin = reinterpret_cast<const trs::MfmaWindow*>(base + o_mwin);
   d.nmwin = (int32_t)mwin.size();
   d.tile_cols = reinterpret_cast<const int32_t*>(base + o_tcol);
   d.tile_a = reinterpret_cast<const uint16_t*>(base + o_ta);
   d.ntiles = (int32_t)L.tiles.size();
+  d.feature_lanes = opt.feature_lanes;
+  // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
+  // consecutive iterations re-read the same col/val cache lines
+  d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   P->csr_only = csr_only;
   trs_plan_stats& s = P->stats;
   s.m = m;
@@ -505,6 +522,10 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->mfma_sptc = 1;
   o->sptc_min_fill = 0.25f;
   o->task_nnz = 0;
+  o->piece_nnz = 0;
+  o->feature_lanes = 0;
+  o->streaming = -1;
+  o->window_row_cap = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }

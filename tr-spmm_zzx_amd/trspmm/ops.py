@@ -112,10 +112,13 @@ def build_format(rowptr, col, val, part_t: int = 32, part_c: int = 32, short_siz
     return Format(h.value)
 
 
-def _options(mfma_tc: bool, mfma_sptc: bool, sptc_min_fill: float, task_nnz: int) -> nat.PlanOptions:
+def _options(mfma_tc: bool, mfma_sptc: bool, sptc_min_fill: float, task_nnz: int, **extra) -> nat.PlanOptions:
     o = nat.PlanOptions()
     nat.lib().trs_plan_options_default(ctypes.byref(o))
     o.mfma_tc, o.mfma_sptc, o.sptc_min_fill, o.task_nnz = int(mfma_tc), int(mfma_sptc), sptc_min_fill, task_nnz
+    for k, v in extra.items():
+        if v is not None:
+            setattr(o, k, int(v))
     return o
 
 
@@ -138,18 +141,25 @@ class Plan:
 
     @classmethod
     def from_format(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
-                    sptc_min_fill: float = 0.25, task_nnz: int = 0) -> "Plan":
-        o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz)
+                    sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
+                    feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
+                    window_row_cap: Optional[int] = None) -> "Plan":
+        """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
+        in include/trspmm.h (None keeps the library default)."""
+        o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
+                     feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
         return cls(h.value)
 
     @classmethod
-    def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0) -> "Plan":
+    def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0, piece_nnz: Optional[int] = None,
+                 feature_lanes: Optional[int] = None, streaming: Optional[int] = None) -> "Plan":
         rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
         col = np.ascontiguousarray(col, dtype=np.int32)
         val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
-        o = _options(False, False, 1.0, task_nnz)
+        o = _options(False, False, 1.0, task_nnz, piece_nnz=piece_nnz, feature_lanes=feature_lanes,
+                     streaming=streaming)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_csr(_ptr(rowptr), _ptr(col), _ptr(val), m, n, ctypes.byref(o),
                                                 ctypes.byref(h)), "trs_plan_create_csr")
