@@ -22,6 +22,7 @@ for _p in (ROOT, os.path.join(ROOT, "tr-spmm_zzx_amd")):
         sys.path.insert(0, _p)
 
 METRIC = "SpMM GFLOP/s (2·nnz·K) + % HBM roofline, R-MAT 2^20 nodes K=128 fp16"
+OTHER_METRIC = "SpMM GFLOP/s (2·nnz·K) + % HBM roofline, {workload} fp16"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -172,7 +173,8 @@ def main():
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"[bench] kernels {kms}, roofline {roof}")
 
-    out = {"metric": METRIC, "value": round(gflops, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
+    metric = METRIC if args.config in (2, 4) else OTHER_METRIC.format(workload=workload)
+    out = {"metric": metric, "value": round(gflops, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f16", "data": "synthetic",
            "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K,
