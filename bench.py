@@ -32,8 +32,10 @@ def log(*a):
 
 def make_workload(cfg: int):
     from trspmm import graphs
-    if cfg == 2 or cfg == 4:
+    if cfg == 2:
         return "rmat20_k128", graphs.rmat(), 128, 2
+    if cfg == 4:
+        return "rmat20_sddmm", graphs.rmat(), 128, 4
     if cfg == 3:
         return "sbm1m_k256", graphs.sbm(), 256, 3
     if cfg == 5:
@@ -78,6 +80,94 @@ def cpu_baseline(g, Bh, flops):
                       f"({t * 1e3:.1f} ms/run)"}
 
 
+def cpu_baseline_sddmm(g, Xh, Yh, flops):
+    """torch.sparse.sampled_addmm CSR fp32 on all host cores, same bounds as cpu_baseline."""
+    import numpy as np
+    import torch
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    nnz = int(g.rowptr[g.m])
+    A = torch.sparse_csr_tensor(torch.from_numpy(g.rowptr[: g.m + 1].astype(np.int64)),
+                                torch.from_numpy(g.col[:nnz].astype(np.int64)), torch.ones(nnz), size=(g.m, g.n))
+    X32 = torch.from_numpy(Xh.astype(np.float32))
+    Y32t = torch.from_numpy(Yh.astype(np.float32)).T
+    t0 = time.perf_counter()
+    torch.sparse.sampled_addmm(A, X32, Y32t, beta=0.0)
+    first = time.perf_counter() - t0
+    runs = max(1, min(5, int(20.0 / max(first, 1e-3))))
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        torch.sparse.sampled_addmm(A, X32, Y32t, beta=0.0)
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"full workload, torch.sparse.sampled_addmm CSR fp32, median of {runs} after 1 warm-up "
+                      f"({t * 1e3:.1f} ms/run)"}
+
+
+def bench_sddmm(args, workload, g, K):
+    """Config 4: SDDMM out[e] = X[row_e] . Y[col_e] on the R-MAT pattern (hybrid tiling)."""
+    import numpy as np
+    import torch
+    import trspmm
+    from trspmm import _native as nat, graphs
+    t0 = time.time()
+    fmt = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n)
+    st = plan.stats()
+    del fmt
+    log(f"[bench] sddmm plan {st} ({time.time() - t0:.1f}s)")
+    Xh = graphs.dense_operand(g.m, K, seed=4)
+    Yh = graphs.dense_operand(g.n, K, seed=5)
+    X = torch.from_numpy(Xh).cuda()
+    Y = torch.from_numpy(Yh).cuda()
+    out = torch.empty(st["nnz"], dtype=torch.float32, device="cuda")
+    for _ in range(args.warmup):
+        plan.sddmm(X, Y, out=out)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        plan.sddmm(X, Y, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    flops = 2.0 * g.nnz * K
+    gflops = flops / (ms_step * 1e-3) / 1e9
+    ms = (ctypes.c_float * 2)()
+    nat.check(nat.lib().trs_sddmm_f16_kernel_ms(plan.handle, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), K,
+                                                out.data_ptr(), int(torch.cuda.current_stream().cuda_stream), 10, ms),
+              "trs_sddmm_f16_kernel_ms")
+    kms = list(ms)
+    names = ["sddmm_tasks", "sddmm_mfma"]
+    dom = int(np.argmax(kms))
+    M, N = g.m, g.n
+    if dom == 0:   # column ids, output index when tiles exist, outputs, row pointers, tasks, X and Y once
+        nr = st["csr_nnz"]
+        bytes_k = (4 + 4 + (4 if st["mfma_tiles"] else 0)) * nr + 4 * (M + 1) + 16 * st["tasks"] \
+            + 2 * M * K + 2 * N * K
+    else:          # per tile: 16 column ids + 256 output slots; X and Y rows once; outputs
+        bytes_k = st["mfma_tiles"] * (64 + 1024) + 4 * st["mfma_nnz"] + 2 * M * K + 2 * N * K
+    achieved = bytes_k / (kms[dom] * 1e-3) / 1e9
+    alg_total = 8 * g.nnz + 4 * (M + 1) + 2 * M * K + 2 * N * K
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload),
+            "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
+            "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
+            "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    outj = {"metric": f"SDDMM GFLOP/s (2·nnz·K) + % HBM roofline, R-MAT 2^20 pattern K={K} fp16", "value": round(gflops, 2),
+            "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K, "mfma_tiles": st["mfma_tiles"],
+                       "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
+            "roofline": roof}
+    if not args.no_cpu_baseline:
+        outj["cpu_baseline"] = cpu_baseline_sddmm(g, Xh, Yh, flops)
+    print(json.dumps(outj), flush=True)
+
+
 def load_traffic(workload: str):
     path = os.path.join(ROOT, "profiles", f"spmm_tasks_{workload}_pmc.json")
     if not os.path.exists(path):
@@ -94,6 +184,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--k", type=int, default=0, help="override the configuration's feature width")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -111,7 +202,13 @@ def main():
     torch.cuda.set_device(0)
     t0 = time.time()
     workload, g, K, bseed = make_workload(args.config)
+    if args.k:
+        K = args.k
+        workload = f"{workload.rsplit('_k', 1)[0]}_k{K}" if "_k" in workload else f"{workload}_k{K}"
     log(f"[bench] graph {workload}: m={g.m} nnz={g.nnz} ({time.time() - t0:.1f}s)")
+    if args.config == 4:
+        bench_sddmm(args, workload, g, K)
+        return
     t0 = time.time()
     fmt = trspmm.build_format(g.rowptr, g.col, g.val)
     log(f"[bench] format built in {fmt.elapsed:.2f}s")
@@ -173,7 +270,7 @@ def main():
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"[bench] kernels {kms}, roofline {roof}")
 
-    metric = METRIC if args.config in (2, 4) else OTHER_METRIC.format(workload=workload)
+    metric = METRIC if args.config == 2 and K == 128 else OTHER_METRIC.format(workload=workload)
     out = {"metric": metric, "value": round(gflops, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "f16", "data": "synthetic",

@@ -91,6 +91,9 @@ typedef struct trs_plan_options {
                              them from evicting gathered B rows); 0 plain; -1 automatic (C stores) */
   int32_t window_row_cap; /* longest residual row an MFMA window may carry before its tiles go
                              back to the residual path (0 = automatic) */
+  int32_t xcd_run;        /* workgroups are remapped so each of the 8 XCDs (own L2) runs this many
+                             consecutive work items in a row; 1 = hardware round robin,
+                             0 = automatic */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);
@@ -149,8 +152,15 @@ int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_p
                                 int64_t tiles, int64_t n_s_window_tile_offset, int32_t window,
                                 int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out);
 
-/* Plain CSR plan (fp16 values): the pattern an SDDMM samples, or a pure-residual SpMM.
- * No reference counterpart (the reference has no SDDMM). */
+/* SDDMM plan over the builder output, on the SpMM tiling: dense 16x16 tiles (TC blocks, 2:4 group
+ * tiles with fill >= sptc_min_fill) run as MFMA dot products sampled at the stored entries, the
+ * rest as wave64 CSR dot products.  Outputs follow the input's CSR order (the format must come
+ * from canonical CSR).  No reference counterpart (the reference has no SDDMM). */
+int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt,
+                          trs_plan** out);
+
+/* Plain CSR SDDMM plan (fp16 values kept for the caller's reference only; SDDMM does not scale by
+ * them): outputs in the given entry order.  No reference counterpart. */
 int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_t* val,
                         int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out);
 
@@ -179,9 +189,9 @@ int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K);
 int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
-/* out[e] = sum_k X[row_e, k] * Y[col_e, k] for every stored entry e of the plan, in the plan's CSR
- * order (row-major, columns ascending).  X [m, K], Y [n, K] fp16; out float32 [nnz].
- * Only plans from trs_plan_create_csr are accepted. */
+/* out[e] = sum_k X[row_e, k] * Y[col_e, k] for every stored entry e of the plan (order: see the
+ * plan constructor).  X [m, K], Y [n, K] fp16; out float32 [nnz].  Only SDDMM plans
+ * (trs_plan_create_sddmm, trs_plan_create_csr) are accepted. */
 int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                   int32_t K, float* out, void* stream);
 
@@ -200,6 +210,11 @@ int trs_spmm_f16_timed(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_
 int trs_spmm_f16_kernel_ms(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C,
                            int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream,
                            int32_t iters, float* ms);
+
+/* SDDMM counterpart of trs_spmm_f16_kernel_ms: ms[0] = CSR dot-product kernel, ms[1] = MFMA tile
+ * kernel (averages over `iters` calls).  No reference counterpart. */
+int trs_sddmm_f16_kernel_ms(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y,
+                            int64_t ldy, int32_t K, float* out, void* stream, int32_t iters, float* ms);
 
 const char* trs_last_error(void);
 

@@ -53,3 +53,32 @@ def test_sddmm_matches_torch_sampled_addmm():
                                 torch.from_numpy(g.col[:nnz].astype(np.int64)), torch.ones(nnz), size=(g.m, g.n))
     ref = torch.sparse.sampled_addmm(A, torch.from_numpy(Xh).float(), torch.from_numpy(Yh).float().T, beta=0.0)
     assert np.allclose(out, ref.values().numpy(), atol=1e-4)
+
+
+@pytest.mark.parametrize("name,gen,K", [
+    ("sbm", lambda: graphs.sbm(communities=1024, seed=1, val_seed=2), 64),
+    ("rmat", lambda: graphs.rmat(scale=13, edge_factor=16, seed=3), 128),
+    ("er", lambda: graphs.erdos_renyi_gcn(nodes=2048, edges=16384), 40),
+    ("gridhubs", lambda: graphs.grid_hubs(side=128, hubs=4, hub_degree=5000, seed=1, val_seed=2), 32),
+])
+@pytest.mark.parametrize("mfma", [True, False])
+def test_hybrid_sddmm_matches_closed_form(name, gen, K, mfma):
+    """SDDMM on the SpMM tiling: MFMA tiles + CSR dot products, outputs in input CSR order."""
+    print("hybrid sddmm", name, K, mfma, flush=True)
+    g = gen()
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.for_sddmm(f, g.m, g.n, mfma_tc=mfma, mfma_sptc=mfma, sptc_min_fill=0.1)
+    st = plan.stats()
+    nnz = int(g.rowptr[g.m])
+    assert st["nnz"] == nnz
+    if mfma and name == "sbm":
+        assert st["mfma_tiles"] > 0 and st["mfma_nnz"] > 0
+    Xh = graphs.dense_operand(g.m, K, seed=11)
+    Yh = graphs.dense_operand(g.n, K, seed=12)
+    out = torch.full((nnz,), float("nan"), device="cuda")
+    plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda(), out=out)
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[:nnz], Xh, Yh)
+    got = out.cpu().numpy()
+    assert not np.isnan(got).any()
+    assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())

@@ -35,7 +35,10 @@ def check(C, R, what):
 
 
 def run_plan(plan, Bh, **kw):
+    """Output prefilled with NaN: an element no kernel writes fails the comparison."""
     B = torch.from_numpy(Bh).cuda()
+    if "out" not in kw:
+        kw["out"] = torch.full((plan.stats()["m"], Bh.shape[1]), float("nan"), device="cuda")
     C = plan.spmm(B, **kw)
     torch.cuda.synchronize()
     return C.cpu().numpy()
@@ -144,6 +147,18 @@ def test_rows_beyond_m_are_dropped_like_reference():
     C = run_plan(plan, Bh)
     assert C.shape == (40, 32)
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=40), "m<rows")
+
+
+@pytest.mark.parametrize("xcd_run", [1, 3, 16, 64])
+@pytest.mark.parametrize("m", [997, 40000])
+def test_xcd_remap_covers_every_work_item(xcd_run, m):
+    """Workgroup remapping must be a bijection for any grid size (NaN-prefilled output)."""
+    g = graphs.random_csr(m, 5000, 3.0 / 5000, seed=m)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    for K in (32, 128):
+        plan = trspmm.Plan.from_format(f, g.m, g.n, xcd_run=xcd_run, task_nnz=32)
+        Bh = dense_B(g.n, K, seed=1)
+        check(run_plan(plan, Bh), osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"xcd_run={xcd_run}")
 
 
 def test_deterministic_bitwise():

@@ -11,11 +11,16 @@
 //   k_spmm_fixup    sums the pieces of split rows in a fixed order (deterministic).
 //   k_spmm_mfma_win one workgroup owns a 16-row window: dense 16x16 fp16 tiles (TC blocks and
 //                   well-filled 2:4 group tiles) go through v_mfma_f32_16x16x16_f16 with the 16
-//                   gathered B rows staged in LDS, then the window's residual rows are added in LDS
-//                   and the 16 x KC tile is stored once.  Replaces the reference TC and packed
-//                   mma.sp kernels (mGCNkernel_online.cu:54-241, 812-933) and the add kernel
-//                   (:1314-1324).
-// SDDMM: k_sddmm_tasks, one lane group per task, per-entry dot products reduced across the group.
+//                   gathered B rows staged in LDS; the window's residual rows are summed in
+//                   registers, added to the MFMA share read back from LDS, and each output row is
+//                   stored once.  Replaces the reference TC and packed mma.sp kernels
+//                   (mGCNkernel_online.cu:54-241, 812-933) and the add kernel (:1314-1324).
+// SDDMM (no reference counterpart):
+//   k_sddmm_tasks   residual entries: one lane group per task, per-entry dot products reduced
+//                   across the group.
+//   k_sddmm_mfma    one wave per dense 16x16 tile: D = X[16 window rows] . Y[16 tile columns]^T
+//                   accumulated over K with v_mfma_f32_16x16x16_f16 (both operands contiguous in
+//                   K, loaded straight from global), sampled at the tile's stored entries.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
@@ -80,6 +85,21 @@ __device__ __forceinline__ T load_stream(const T* p) {
   else return *p;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (physical id i runs on XCD i % 8), and
+// each XCD has its own L2.  Remap so that every XCD executes runs of `run` consecutive logical
+// workgroups: neighbouring rows (which share B rows on mesh-like graphs) then share one L2, while
+// runs still interleave across XCDs so heavy work spread along the order stays balanced.
+// Bijective on [0, n): the first (n / (8 run)) * 8 run ids are permuted, the tail is unchanged.
+__device__ __forceinline__ int xcd_remap(int i, int n, int run) {
+  constexpr int kXcds = 8;
+  if (run <= 1) return i;
+  const int span = kXcds * run;
+  const int full = (n / span) * span;
+  if (i >= full) return i;
+  const int x = i % kXcds, j = i / kXcds;
+  return (j / run) * span + x * run + (j % run);
+}
+
 template <int VEC>
 __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
 #pragma unroll
@@ -130,7 +150,8 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
   const int li = lane % LPG;
-  const int task_id = (blockIdx.x * 4 + wave) * GPW + grp;
+  const int wg = xcd_remap(blockIdx.x, gridDim.x, P.xcd_run);
+  const int task_id = (wg * 4 + wave) * GPW + grp;
   const bool valid = task_id < P.ntasks;
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   int* rp = s_rp[wave][grp];
@@ -260,12 +281,12 @@ __global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, fl
 
 // ------------------------------------------------------------------------------------------------
 // MFMA window kernel.  KC = features per workgroup (multiple of 16, <= 256); NT = MFMA n-tiles
-// (16 features each) per wave = KC / 64 rounded up.
+// (16 features each) per wave = KC / 64 rounded up (template NTILE).
 // MFMA 16x16x16 f16 operand layout (lane l, j = 0..3):
 //   A: A[l % 16][4 * (l / 16) + j]      B: B[4 * (l / 16) + j][l % 16]
 //   D: D[4 * (l / 16) + j][l % 16]
 // Here A = the 16x16 tile (window row x tile column), B = gathered B rows (tile column x feature).
-template <int VEC, int NT>
+template <int VEC, int NTILE>
 __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                        int K, float* __restrict__ C, int64_t ldc, int KC) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -274,15 +295,15 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
   float* otile = reinterpret_cast<float*>(smem);
   _Float16* bst = reinterpret_cast<_Float16*>(otile + 16 * KCP);
 
-  const MfmaWindow w = P.mwin[blockIdx.x];
+  const MfmaWindow w = P.mwin[xcd_remap(blockIdx.x, gridDim.x, P.xcd_run)];
   const int fbase = blockIdx.y * KC;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int ntn = KC / 16;
 
-  float4_t acc[NT];
+  float4_t acc[NTILE];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NTILE; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int t = w.tile_begin; t < w.tile_end; ++t) {
     __syncthreads();
@@ -302,7 +323,7 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
     const half4_t a = *reinterpret_cast<const half4_t*>(
         reinterpret_cast<const _Float16*>(P.tile_a) + (int64_t)t * 256 + (lane & 15) * 16 + 4 * (lane >> 4));
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
+    for (int j = 0; j < NTILE; ++j) {
       const int nt = wave + 4 * j;
       if (nt < ntn) {
         half4_t b;
@@ -313,7 +334,7 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
     }
   }
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
+  for (int j = 0; j < NTILE; ++j) {
     const int nt = wave + 4 * j;
     if (nt < ntn) {
 #pragma unroll
@@ -322,7 +343,8 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
   }
   __syncthreads();
 
-  // residual rows of this window, added on top of the MFMA share
+  // residual rows of this window: a row group walks a row's entries, adds the MFMA share read
+  // back from LDS (16-byte reads) and stores the finished row once
   const int gs = KC / VEC;         // threads per row group
   const int groups = 256 / gs;     // threads past groups * gs sit this phase out
   const int g = threadIdx.x / gs;
@@ -334,26 +356,18 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
     float racc[VEC];
     zero_acc(racc);
     accumulate_row<VEC, 8>(P.col, P.val, B, ldb, f, f < K, P.rowptr[row], P.rowptr[row + 1], racc);
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) otile[rl * KCP + ff + i] += racc[i];
-  }
-  __syncthreads();
-
-  // store the 16 x KC tile once
-  const int per_row4 = KC / 4;
-  for (int idx = threadIdx.x; idx < 16 * per_row4; idx += 256) {
-    const int rl = idx / per_row4;
-    const int c4 = (idx % per_row4) * 4;
-    const int row = w.row0 + rl;
-    if (row >= P.m) continue;
-    const float* src = otile + rl * KCP + c4;
-    float* dst = C + (int64_t)row * ldc + fbase + c4;
+    if (f >= K) continue;
+    const float* src = otile + rl * KCP + ff;
     if constexpr (VEC == 8) {
-      if (fbase + c4 < K) *reinterpret_cast<float4_t*>(dst) = float4_t{src[0], src[1], src[2], src[3]};
+      const float4_t lo = reinterpret_cast<const float4_t*>(src)[0];
+      const float4_t hi = reinterpret_cast<const float4_t*>(src)[1];
+      racc[0] += lo[0]; racc[1] += lo[1]; racc[2] += lo[2]; racc[3] += lo[3];
+      racc[4] += hi[0]; racc[5] += hi[1]; racc[6] += hi[2]; racc[7] += hi[3];
     } else {
-      for (int i = 0; i < 4; ++i)
-        if (fbase + c4 + i < K) dst[i] = src[i];
+      racc[0] += src[0];
     }
+    if (P.streaming & 2) store_vec<VEC, true>(C + (int64_t)row * ldc + f, racc);
+    else store_vec<VEC, false>(C + (int64_t)row * ldc + f, racc);
   }
 }
 
@@ -365,7 +379,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   constexpr int GPW = 64 / LPG;
   constexpr int FPP = LPG * VEC;   // features per pass
   const int lane = threadIdx.x & 63;
-  const int task_id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
+  const int task_id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
   const bool valid = task_id < P.ntasks;
   const Task t = P.tasks[valid ? task_id : 0];
   const int li = lane % LPG;
@@ -405,10 +419,56 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       if (valid && li == 0) {
 #pragma unroll
         for (int i = 0; i < U; ++i)
-          if (p + i < p_hi) out[p + i] = s[i];
+          if (p + i < p_hi) out[P.res_pos ? P.res_pos[p + i] : p + i] = s[i];
       }
     }
     p_lo = p_hi;
+  }
+}
+
+// SDDMM over dense tiles, one wave per tile (4 per workgroup).  With the 16x16x16 MFMA operand
+// layout (see k_spmm_mfma_win), A = X[row0 + l % 16][k0 + 4 (l / 16) + j] and
+// B = Y[col_{l % 16}][k0 + 4 (l / 16) + j]: each lane reads 4 consecutive features of one row.
+// VEC4: K % 4 == 0 and 8-byte aligned rows (one 8-byte load per operand), else guarded scalars.
+template <bool VEC4>
+__global__ __launch_bounds__(256) void k_sddmm_mfma(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
+                                                    const uint16_t* __restrict__ Y, int64_t ldy, int K,
+                                                    float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int t = xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + (threadIdx.x >> 6);
+  if (t >= P.ntiles) return;
+  const int row = P.tile_row0[t] + (lane & 15);
+  const int col = P.tile_cols[t * 16 + (lane & 15)];
+  const bool xrow_ok = row < P.m;
+  const bool ycol_ok = col >= 0;
+  const uint16_t* xp = X + (int64_t)(xrow_ok ? row : 0) * ldx;
+  const uint16_t* yp = Y + (int64_t)(ycol_ok ? col : 0) * ldy;
+  float4_t acc{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const int k = k0 + 4 * (lane >> 4);
+    half4_t a{0, 0, 0, 0}, b{0, 0, 0, 0};
+    if constexpr (VEC4) {
+      if (k < K) {
+        if (xrow_ok) a = *reinterpret_cast<const half4_t*>(xp + k);
+        if (ycol_ok) b = *reinterpret_cast<const half4_t*>(yp + k);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (k + j < K) {
+          if (xrow_ok) a[j] = __builtin_bit_cast(_Float16, xp[k + j]);
+          if (ycol_ok) b[j] = __builtin_bit_cast(_Float16, yp[k + j]);
+        }
+      }
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc, 0, 0, 0);
+  }
+  // D[r][c] for r = 4 (l / 16) + j, c = l % 16: write the stored entries
+  const int32_t* pos = P.tile_pos + (int64_t)t * 256;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = pos[(4 * (lane >> 4) + j) * 16 + (lane & 15)];
+    if (e >= 0) out[e] = acc[j];
   }
 }
 
@@ -474,14 +534,25 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 
 template <int VEC>
 hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                            int K, float* out, hipStream_t s) {
-  if (p.ntasks <= 0) return hipSuccess;
-  const int lpg = lanes_for(K, VEC);
-  const int gpb = 4 * (64 / lpg);
-  dim3 grid((p.ntasks + gpb - 1) / gpb);
+                            int K, float* out, hipStream_t s, hipEvent_t* ev) {
+  if (ev) (void)hipEventRecord(ev[0], s);
+  if (p.ntasks > 0) {
+    const int lpg = lanes_for(K, VEC);
+    const int gpb = 4 * (64 / lpg);
+    dim3 grid((p.ntasks + gpb - 1) / gpb);
 #define TRS_SD(L) case L: hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break;
-  switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
+    switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
 #undef TRS_SD
+  }
+  if (ev) (void)hipEventRecord(ev[1], s);
+  if (p.ntiles > 0 && p.tile_pos) {
+    const bool v4 = K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
+    dim3 grid((p.ntiles + 3) / 4);
+    if (v4) hipLaunchKernelGGL((k_sddmm_mfma<true>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
+    else hipLaunchKernelGGL((k_sddmm_mfma<false>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
+  }
+  if (ev) (void)hipEventRecord(ev[2], s);
   return hipGetLastError();
 }
 
@@ -498,10 +569,10 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
 }
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, hipStream_t stream) {
+                        int K, float* out, hipStream_t stream, hipEvent_t* ev) {
   const bool v8 = K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
-  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream)
-            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream);
+  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
+            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream, ev);
 }
 
 }  // namespace trs

@@ -38,16 +38,23 @@ struct DevicePlan {
   const MfmaWindow* mwin = nullptr;
   int32_t nmwin = 0;
   const int32_t* tile_cols = nullptr;  // [tiles][16]
-  const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16
+  const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16 (SpMM)
   int32_t ntiles = 0;
+  // SDDMM plans: output index of each residual entry (null = identity) and, per tile, its first
+  // row and the output index of each of its 256 (row, column) slots (-1 = not stored)
+  const int32_t* res_pos = nullptr;
+  const int32_t* tile_row0 = nullptr;
+  const int32_t* tile_pos = nullptr;
   int32_t feature_lanes = 0;   // lanes per residual lane group (0 = automatic)
   int32_t streaming = 0;       // bit 0: non-temporal A-stream loads, bit 1: non-temporal C stores
+  int32_t xcd_run = 1;         // consecutive workgroups per XCD run (1 = hardware round robin)
 };
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                        float* partial, hipStream_t stream, hipEvent_t* ev = nullptr);
+// ev (optional): 3 events recorded before the residual kernel and after each of the two kernels.
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, hipStream_t stream);
+                        int K, float* out, hipStream_t stream, hipEvent_t* ev = nullptr);
 
 }  // namespace trs

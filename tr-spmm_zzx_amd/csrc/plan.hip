@@ -62,7 +62,7 @@ struct Lowering {
   std::vector<int32_t> row, col;
   std::vector<float> val;
   // MFMA tiles: row0, 16 columns, dense 16x16 values
-  struct Tile { int32_t row0; int32_t cols[16]; float a[256]; int nnz; };
+  struct Tile { int32_t row0; int32_t cols[16]; float a[256]; uint64_t present[4]; int nnz; };
   std::vector<Tile> tiles;
   Status st;
 
@@ -83,8 +83,17 @@ struct Lowering {
   // Tile entry; -1 columns never carry values.
   void tile_add(Tile& t, int r, int k, float v) {
     t.a[r * 16 + k] += v;
+    t.present[r / 4] |= 1ull << ((r % 4) * 16 + k);
     t.nnz++;
   }
+  static void tile_init(Tile& t, int32_t row0) {
+    t.row0 = row0;
+    std::fill(t.cols, t.cols + 16, -1);
+    std::fill(t.a, t.a + 256, 0.f);
+    std::fill(t.present, t.present + 4, 0ull);
+    t.nnz = 0;
+  }
+  static bool tile_has(const Tile& t, int r, int k) { return (t.present[r / 4] >> ((r % 4) * 16 + k)) & 1; }
 };
 
 
@@ -100,12 +109,7 @@ void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_
     const bool mfma = to_mfma && row0 % 16 == 0 && row0 >= 0;
     for (int32_t s = s0; s < s1 && L.st.ok(); s += (mfma ? 2 : 1)) {
       Lowering::Tile T;
-      if (mfma) {
-        T.row0 = row0;
-        std::fill(T.cols, T.cols + 16, -1);
-        std::fill(T.a, T.a + 256, 0.f);
-        T.nnz = 0;
-      }
+      if (mfma) Lowering::tile_init(T, row0);
       const int nsub = mfma ? std::min(2, s1 - s) : 1;
       for (int h = 0; h < nsub; ++h) {
         const int32_t sb = s + h;
@@ -192,10 +196,7 @@ void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const i
         continue;
       }
       Lowering::Tile T;
-      T.row0 = (int32_t)row0;
-      std::fill(T.cols, T.cols + 16, -1);
-      std::fill(T.a, T.a + 256, 0.f);
-      T.nnz = 0;
+      Lowering::tile_init(T, (int32_t)row0);
       for (int64_t g = base; g < end; ++g) {
         const int gi = (int)(g - base);
         for (int p = 0; p < 4; ++p) {
@@ -248,9 +249,7 @@ void lower_packed(Lowering& L, const int32_t* tcol, const int32_t* pa, const int
       const bool mfma = to_mfma && window == 16 && row0 % 16 == 0 && (float)es.size() >= min_fill * 256.f;
       Lowering::Tile T;
       if (mfma) {
-        T.row0 = (int32_t)row0;
-        T.nnz = 0;
-        std::fill(T.a, T.a + 256, 0.f);
+        Lowering::tile_init(T, (int32_t)row0);
         for (int k = 0; k < 16; ++k) {
           const int32_t c = tcol[t * 16 + k];
           if (c >= 0 && !L.check_col(c)) return;
@@ -279,36 +278,137 @@ size_t push_bytes(std::vector<unsigned char>& blob, const std::vector<T>& v) {
   return off;
 }
 
+struct Tasks {
+  std::vector<trs::Task> tasks;
+  std::vector<trs::Fixup> fix, wfix;
+  int32_t slots = 0;
+  int64_t split_rows = 0;
+  Status st;
+};
+
+// Residual work items over the rows of `rowptr` that no MFMA window owns (owned: per 16-row block,
+// empty = none).  with_fixup: long rows become pieces summed into partial slots (SpMM); otherwise
+// each piece writes its own outputs (SDDMM, whose outputs are per entry).
+Tasks build_tasks(const std::vector<int32_t>& rowptr, int32_t m, int64_t nent, const std::vector<uint8_t>& owned,
+                  bool with_fixup, const trs_plan_options& opt) {
+  Tasks T;
+  // Entries per packed task: short rows want small tasks (more lane groups in flight, fewer row
+  // flushes per group), long rows want larger ones.  Measured on MI355X: 32 for a degree-4 mesh,
+  // 128 for R-MAT (mean non-empty row ~49) -- about four mean rows per task.
+  int S = opt.task_nnz;
+  if (S <= 0) {
+    int64_t nonempty = 0;
+    for (int32_t q = 0; q < m; ++q) nonempty += rowptr[q + 1] > rowptr[q];
+    const double mean = nonempty ? (double)nent / (double)nonempty : 1.0;
+    S = (int)std::min(128.0, std::max(32.0, 4.0 * mean));
+  }
+  const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
+  const int rows_cap = trs::kTaskRows;
+  auto is_owned = [&](int32_t r) { return !owned.empty() && owned[r / 16]; };
+  std::vector<trs::Task> pieces, packed;
+  int32_t r = 0;
+  while (r < m) {
+    if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
+    const int32_t deg = rowptr[r + 1] - rowptr[r];
+    if (deg > piece_max) {
+      const int np = (deg + piece_max - 1) / piece_max;
+      const int32_t base = T.slots;
+      for (int q = 0; q < np; ++q) {
+        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
+        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
+        pieces.push_back({r, with_fixup ? ~T.slots : -1, b, e});
+        if (with_fixup) ++T.slots;
+      }
+      if (with_fixup) {
+        (np > trs::kWideFixupSlots ? T.wfix : T.fix).push_back({r, base, np, 0});
+        ++T.split_rows;
+      }
+      ++r;
+      continue;
+    }
+    // pack whole rows while the entry count stays within S (a single long row forms its own task)
+    int32_t r1 = r + 1;
+    int32_t tot = deg;
+    while (r1 < m && r1 - r < rows_cap && !is_owned(r1)) {
+      const int32_t d = rowptr[r1 + 1] - rowptr[r1];
+      if (d > piece_max || tot + d > S) break;
+      tot += d;
+      ++r1;
+    }
+    packed.push_back({r, r1, rowptr[r], rowptr[r1]});
+    r = r1;
+  }
+  T.tasks.reserve(pieces.size() + packed.size());
+  T.tasks.insert(T.tasks.end(), pieces.begin(), pieces.end());
+  T.tasks.insert(T.tasks.end(), packed.begin(), packed.end());
+  if (T.tasks.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
+  return T;
+}
+
+// Residual CSR of a lowering: row pointers and the permutation of entries into row order, each
+// row sorted by column (stable) unless keep_order.
+void residual_csr(const Lowering& L, bool keep_order, std::vector<int32_t>& rowptr, std::vector<int64_t>& perm) {
+  const int32_t m = L.m;
+  const int64_t nent = (int64_t)L.row.size();
+  std::vector<int64_t> cnt(m + 1, 0);
+  for (int64_t i = 0; i < nent; ++i) cnt[L.row[i] + 1]++;
+  for (int32_t r = 0; r < m; ++r) cnt[r + 1] += cnt[r];
+  rowptr.assign(m + 1, 0);
+  for (int32_t r = 0; r <= m; ++r) rowptr[r] = (int32_t)cnt[r];
+  std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
+  perm.assign(nent, 0);
+  for (int64_t i = 0; i < nent; ++i) perm[pos[L.row[i]]++] = i;
+  if (!keep_order)
+    for (int32_t r = 0; r < m; ++r)
+      std::stable_sort(perm.begin() + rowptr[r], perm.begin() + rowptr[r + 1],
+                       [&](int64_t x, int64_t y) { return L.col[x] < L.col[y]; });
+}
+
+// One hipMalloc holding the whole plan, filled by one copy.
+Status upload(std::vector<unsigned char>& blob, trs_plan*& P) {
+  blob.resize(std::max<size_t>(blob.size(), 256));
+  P = new trs_plan();
+  if (hipGetDevice(&P->device) != hipSuccess) {
+    delete P;
+    P = nullptr;
+    return fail(TRS_EDEVICE, "no HIP device available");
+  }
+  if (hipMalloc(&P->dmem, blob.size()) != hipSuccess) {
+    P->dmem = nullptr;
+    delete P;
+    P = nullptr;
+    (void)hipGetLastError();
+    return fail(TRS_ENOMEM, "hipMalloc of " + std::to_string(blob.size()) + " plan bytes failed");
+  }
+  P->dbytes = blob.size();
+  if (hipMemcpy(P->dmem, blob.data(), blob.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    delete P;
+    P = nullptr;
+    return fail(TRS_EDEVICE, "plan upload failed");
+  }
+  return Status{};
+}
+
 // Residual CSR + tasks + MFMA windows -> device plan.
-Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool keep_order, trs_plan** out) {
+Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   if (!L.st.ok()) return L.st;
   const int32_t m = L.m;
   const int64_t nent = (int64_t)L.row.size();
   if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
 
   // MFMA windows: 16-row blocks owning at least one tile.
-  std::vector<int32_t> block_tiles_begin, block_of_tile;
   std::sort(L.tiles.begin(), L.tiles.end(), [](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; });
   const int32_t nblocks = (m + 15) / 16;
   std::vector<uint8_t> owned(nblocks, 0);
   for (const auto& t : L.tiles) owned[t.row0 / 16] = 1;
 
   // residual CSR sorted by (row, column); stable so equal keys keep insertion order
-  std::vector<int64_t> cnt(m + 1, 0);
-  for (int64_t i = 0; i < nent; ++i) cnt[L.row[i] + 1]++;
-  for (int32_t r = 0; r < m; ++r) cnt[r + 1] += cnt[r];
-  std::vector<int32_t> rowptr(m + 1);
-  for (int32_t r = 0; r <= m; ++r) rowptr[r] = (int32_t)cnt[r];
+  std::vector<int32_t> rowptr;
   std::vector<int32_t> col(nent);
   std::vector<uint16_t> val(nent);
   {
-    std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
-    std::vector<int64_t> perm(nent);
-    for (int64_t i = 0; i < nent; ++i) perm[pos[L.row[i]]++] = i;
-    for (int32_t r = 0; r < m; ++r) {
-      auto b = perm.begin() + rowptr[r], e = perm.begin() + rowptr[r + 1];
-      if (!keep_order) std::stable_sort(b, e, [&](int64_t x, int64_t y) { return L.col[x] < L.col[y]; });
-    }
+    std::vector<int64_t> perm;
+    residual_csr(L, false, rowptr, perm);
     for (int64_t i = 0; i < nent; ++i) {
       col[i] = L.col[perm[i]];
       val[i] = trs::half_bits(L.val[perm[i]]);
@@ -339,9 +439,9 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
         if (!demote[t.row0 / 16]) { L2.tiles.push_back(t); continue; }
         for (int r = 0; r < 16; ++r)
           for (int k = 0; k < 16; ++k)
-            if (t.cols[k] >= 0 && t.a[r * 16 + k] != 0.f) L2.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
+            if (t.cols[k] >= 0 && Lowering::tile_has(t, r, k)) L2.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
       }
-      return finalize(L2, opt, csr_only, keep_order, out);
+      return finalize(L2, opt, out);
     }
   }
   for (size_t i = 0; i < L.tiles.size();) {
@@ -354,75 +454,19 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   std::vector<uint16_t> tile_a(L.tiles.size() * 256);
   int64_t mfma_nnz = 0;
   for (size_t t = 0; t < L.tiles.size(); ++t) {
-    int32_t first_valid = 0;
     for (int k = 0; k < 16; ++k) tile_cols[t * 16 + k] = L.tiles[t].cols[k];
-    (void)first_valid;
     for (int i = 0; i < 256; ++i) tile_a[t * 256 + i] = trs::half_bits(L.tiles[t].a[i]);
     mfma_nnz += L.tiles[t].nnz;
   }
 
   // residual tasks over rows not owned by an MFMA window
-  // Entries per packed task: short rows want small tasks (more lane groups in flight, fewer row
-  // flushes per group), long rows want larger ones.  Measured on MI355X: 32 for a degree-4 mesh,
-  // 128 for R-MAT (mean non-empty row ~49) -- about four mean rows per task.
-  int S = opt.task_nnz;
-  if (S <= 0) {
-    int64_t nonempty = 0;
-    for (int32_t q = 0; q < m; ++q) nonempty += rowptr[q + 1] > rowptr[q];
-    const double mean = nonempty ? (double)nent / (double)nonempty : 1.0;
-    S = (int)std::min(128.0, std::max(32.0, 4.0 * mean));
-  }
-  const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
-  const int rows_cap = trs::kTaskRows;
-  std::vector<trs::Task> pieces, packed;
-  std::vector<trs::Fixup> fix, wfix;
-  int32_t slots = 0;
-  int64_t split_rows = 0;
-  int32_t r = 0;
-  while (r < m) {
-    if (owned[r / 16]) { r = std::min(m, (r / 16 + 1) * 16); continue; }
-    const int32_t deg = rowptr[r + 1] - rowptr[r];
-    if (deg > piece_max && !csr_only) {
-      const int np = (deg + piece_max - 1) / piece_max;
-      const int32_t base = slots;
-      for (int q = 0; q < np; ++q) {
-        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
-        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
-        pieces.push_back({r, ~slots, b, e});
-        ++slots;
-      }
-      (np > trs::kWideFixupSlots ? wfix : fix).push_back({r, base, np, 0});
-      ++split_rows;
-      ++r;
-      continue;
-    }
-    if (deg > piece_max && csr_only) {   // SDDMM: pieces write their own outputs, no fixup
-      const int np = (deg + piece_max - 1) / piece_max;
-      for (int q = 0; q < np; ++q) {
-        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
-        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
-        pieces.push_back({r, -1, b, e});
-      }
-      ++r;
-      continue;
-    }
-    // pack whole rows while the entry count stays within S (a single long row forms its own task)
-    int32_t r1 = r + 1;
-    int32_t tot = deg;
-    while (r1 < m && r1 - r < rows_cap && !owned[r1 / 16]) {
-      const int32_t d = rowptr[r1 + 1] - rowptr[r1];
-      if (d > piece_max || tot + d > S) break;
-      tot += d;
-      ++r1;
-    }
-    packed.push_back({r, r1, rowptr[r], rowptr[r1]});
-    r = r1;
-  }
-  std::vector<trs::Task> tasks;
-  tasks.reserve(pieces.size() + packed.size());
-  tasks.insert(tasks.end(), pieces.begin(), pieces.end());
-  tasks.insert(tasks.end(), packed.begin(), packed.end());
-  if (tasks.size() > (size_t)INT32_MAX / 64) return fail(TRS_ERANGE, "too many tasks");
+  Tasks T = build_tasks(rowptr, m, nent, owned, true, opt);
+  if (!T.st.ok()) return T.st;
+  std::vector<trs::Task>& tasks = T.tasks;
+  std::vector<trs::Fixup>& fix = T.fix;
+  std::vector<trs::Fixup>& wfix = T.wfix;
+  const int32_t slots = T.slots;
+  const int64_t split_rows = T.split_rows;
 
   // one device allocation
   std::vector<unsigned char> blob;
@@ -435,23 +479,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   const size_t o_mwin = push_bytes(blob, mwin);
   const size_t o_tcol = push_bytes(blob, tile_cols);
   const size_t o_ta = push_bytes(blob, tile_a);
-  blob.resize(std::max<size_t>(blob.size(), 256));
-
-  trs_plan* P = new trs_plan();
-  if (hipGetDevice(&P->device) != hipSuccess) {
-    delete P;
-    return fail(TRS_EDEVICE, "no HIP device available");
-  }
-  if (hipMalloc(&P->dmem, blob.size()) != hipSuccess) {
-    P->dmem = nullptr;
-    delete P;
-    (void)hipGetLastError();
-    return fail(TRS_ENOMEM, "hipMalloc of " + std::to_string(blob.size()) + " plan bytes failed");
-  }
-  P->dbytes = blob.size();
-  if (hipMemcpy(P->dmem, blob.data(), blob.size(), hipMemcpyHostToDevice) != hipSuccess) {
-    delete P;
-    return fail(TRS_EDEVICE, "plan upload failed");
+  trs_plan* P = nullptr;
+  {
+    const Status us = upload(blob, P);
+    if (!us.ok()) return us;
   }
   unsigned char* base = static_cast<unsigned char*>(P->dmem);
   trs::DevicePlan& d = P->dp;
@@ -477,7 +508,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
-  P->csr_only = csr_only;
+  d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
+  P->csr_only = false;
   trs_plan_stats& s = P->stats;
   s.m = m;
   s.n = L.n;
@@ -494,6 +526,95 @@ Status finalize(Lowering& L, const trs_plan_options& opt, bool csr_only, bool ke
   for (const auto& w : mwin)
     for (int32_t r = w.row0; r < std::min(m, w.row0 + 16); ++r) wnnz += rowptr[r + 1] - rowptr[r];
   s.window_csr_nnz = wnnz;
+  *out = P;
+  return Status{};
+}
+
+// SDDMM plan: residual CSR (+ the output index of each entry when tiles exist) and independent
+// tiles with the output index of each stored slot.  Outputs follow the (row, column) order of all
+// entries, i.e. the input CSR order for canonical input; keep_order keeps a plain CSR as given.
+Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order, trs_plan** out) {
+  if (!L.st.ok()) return L.st;
+  const int32_t m = L.m;
+  const int64_t nent = (int64_t)L.row.size();
+  std::vector<int32_t> rowptr;
+  std::vector<int64_t> perm;
+  residual_csr(L, keep_order && L.tiles.empty(), rowptr, perm);
+  std::vector<int32_t> col(nent);
+  for (int64_t i = 0; i < nent; ++i) col[i] = L.col[perm[i]];
+
+  // tile entries in (row, column) order, merged with the residual rows
+  struct TE { int32_t row, col, slot; };   // slot = tile * 256 + r * 16 + k
+  std::vector<TE> te;
+  for (size_t t = 0; t < L.tiles.size(); ++t)
+    for (int r = 0; r < 16; ++r)
+      for (int k = 0; k < 16; ++k)
+        if (L.tiles[t].cols[k] >= 0 && Lowering::tile_has(L.tiles[t], r, k) && L.tiles[t].row0 + r < m)
+          te.push_back({L.tiles[t].row0 + r, L.tiles[t].cols[k], (int32_t)(t * 256 + r * 16 + k)});
+  std::sort(te.begin(), te.end(), [](const TE& a, const TE& b) { return a.row != b.row ? a.row < b.row : a.col < b.col; });
+  if (nent + (int64_t)te.size() > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 entries");
+  std::vector<int32_t> res_pos, tile_pos, tile_row0, tile_cols;
+  if (!te.empty()) {
+    res_pos.resize(nent);
+    tile_pos.assign(L.tiles.size() * 256, -1);
+    int32_t next = 0;
+    size_t ti = 0;
+    for (int32_t r = 0; r < m; ++r) {
+      int32_t j = rowptr[r];
+      while (j < rowptr[r + 1] || (ti < te.size() && te[ti].row == r)) {
+        const bool take_tile = ti < te.size() && te[ti].row == r && (j >= rowptr[r + 1] || te[ti].col < col[j]);
+        if (take_tile) tile_pos[te[ti++].slot] = next++;
+        else res_pos[j++] = next++;
+      }
+    }
+    for (const auto& t : L.tiles) {
+      tile_row0.push_back(t.row0);
+      tile_cols.insert(tile_cols.end(), t.cols, t.cols + 16);
+    }
+  }
+  Tasks T = build_tasks(rowptr, m, nent, {}, false, opt);
+  if (!T.st.ok()) return T.st;
+
+  std::vector<unsigned char> blob;
+  const size_t o_rowptr = push_bytes(blob, rowptr);
+  const size_t o_col = push_bytes(blob, col);
+  const size_t o_tasks = push_bytes(blob, T.tasks);
+  const size_t o_rpos = push_bytes(blob, res_pos);
+  const size_t o_trow = push_bytes(blob, tile_row0);
+  const size_t o_tcol = push_bytes(blob, tile_cols);
+  const size_t o_tpos = push_bytes(blob, tile_pos);
+  trs_plan* P = nullptr;
+  {
+    const Status us = upload(blob, P);
+    if (!us.ok()) return us;
+  }
+  unsigned char* base = static_cast<unsigned char*>(P->dmem);
+  trs::DevicePlan& d = P->dp;
+  d.m = m;
+  d.n = L.n;
+  d.nnz_csr = nent;
+  d.rowptr = reinterpret_cast<const int32_t*>(base + o_rowptr);
+  d.col = reinterpret_cast<const int32_t*>(base + o_col);
+  d.tasks = reinterpret_cast<const trs::Task*>(base + o_tasks);
+  d.ntasks = (int32_t)T.tasks.size();
+  d.res_pos = res_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_rpos);
+  d.tile_row0 = tile_row0.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_trow);
+  d.tile_cols = tile_cols.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tcol);
+  d.tile_pos = tile_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tpos);
+  d.ntiles = tile_pos.empty() ? 0 : (int32_t)L.tiles.size();
+  d.feature_lanes = opt.feature_lanes;
+  d.streaming = 0;
+  d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
+  P->csr_only = true;
+  trs_plan_stats& s = P->stats;
+  s.m = m;
+  s.n = L.n;
+  s.csr_nnz = nent;
+  s.mfma_tiles = d.ntiles;
+  s.mfma_nnz = (int64_t)te.size();
+  s.nnz = nent + (int64_t)te.size();
+  s.tasks = (int64_t)T.tasks.size();
+  s.device_bytes = (int64_t)blob.size();
   *out = P;
   return Status{};
 }
@@ -526,6 +647,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->feature_lanes = 0;
   o->streaming = -1;
   o->window_row_cap = 0;
+  o->xcd_run = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }
@@ -552,7 +674,29 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
   lower_groups(L, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
                f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
   for (size_t i = 0; i < f->spill_row.size() && L.st.ok(); ++i) L.add(f->spill_row[i], f->spill_col[i], f->spill_val[i]);
-  return report(finalize(L, o, false, false, out));
+  return report(finalize(L, o, out));
+}
+
+int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
+  if (!f || !out) return report(fail(TRS_EINVAL, "trs_plan_create_sddmm: NULL argument"));
+  *out = nullptr;
+  if (bad_dims(m, n)) return report(fail(TRS_EINVAL, "trs_plan_create_sddmm: negative m or n"));
+  if (!f->canonical)
+    return report(fail(TRS_ENOTCANON, "trs_plan_create_sddmm: input rows were not strictly increasing"));
+  const trs_plan_options o = resolve(opt);
+  Lowering L;
+  L.m = m;
+  L.n = n;
+  lower_tc(L, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
+           f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
+  lower_residual(L, f->c_off.data(), f->c_row.data(), (int64_t)f->c_row.size(), f->c_col.data(), f->c_val.data(),
+                 nullptr, (int64_t)f->c_col.size());
+  lower_residual(L, f->cs_off.data(), f->cs_row.data(), (int64_t)f->cs_row.size(), f->cs_col.data(),
+                 f->cs_val.data(), nullptr, (int64_t)f->cs_col.size());
+  lower_groups(L, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
+               f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
+  for (size_t i = 0; i < f->spill_row.size() && L.st.ok(); ++i) L.add(f->spill_row[i], f->spill_col[i], f->spill_val[i]);
+  return report(finalize_sddmm(L, o, false, out));
 }
 
 int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_options* opt, trs_plan** out) {
@@ -586,7 +730,7 @@ int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_option
                  a->window, o.mfma_sptc != 0, o.sptc_min_fill);
   }
   for (int64_t i = 0; i < a->spill_count && L.st.ok(); ++i) L.add(a->spill_row[i], a->spill_col[i], a->spill_val[i]);
-  return report(finalize(L, o, false, false, out));
+  return report(finalize(L, o, out));
 }
 
 int trs_plan_create_sptc(const int32_t* s_column, const float* s_value, const int8_t* s_pos, int64_t groups,
@@ -607,7 +751,7 @@ int trs_plan_create_sptc(const int32_t* s_column, const float* s_value, const in
   L.n = n;
   lower_groups(L, s_column, s_value, s_pos, groups, s_window, s_window ? nullptr : s_offsets,
                s_window ? 0 : n_s_offsets - 1, window, o.mfma_sptc != 0 && !s_window, o.sptc_min_fill);
-  return report(finalize(L, o, false, false, out));
+  return report(finalize(L, o, out));
 }
 
 int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_packed_a, const int32_t* s_packed_meta,
@@ -623,7 +767,7 @@ int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_p
   L.n = n;
   lower_packed(L, s_tile_column, s_packed_a, s_packed_meta, tiles, s_window_tile_offset, n_wto - 1, window,
                o.mfma_sptc != 0, o.sptc_min_fill);
-  return report(finalize(L, o, false, false, out));
+  return report(finalize(L, o, out));
 }
 
 int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_t* val, int32_t m, int32_t n,
@@ -646,7 +790,7 @@ int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_
       if (col[e] < 0 || col[e] >= n) return report(fail(TRS_ERANGE, "column index outside [0, n)"));
       L.row[e] = r; L.col[e] = col[e]; L.val[e] = f16_to_f32(val[e]);
     }
-  return report(finalize(L, o, true, true, out));
+  return report(finalize_sddmm(L, o, true, out));
 }
 
 int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s) {
@@ -675,7 +819,7 @@ static int spmm_impl(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t 
                      int64_t ws_bytes, void* stream, hipEvent_t* ev) {
   int rc = check_call(p, K);
   if (rc) return rc;
-  if (p->csr_only) return report(fail(TRS_EINVAL, "trs_spmm_f16: plan was created for SDDMM (trs_plan_create_csr)"));
+  if (p->csr_only) return report(fail(TRS_EINVAL, "trs_spmm_f16: plan was created for SDDMM"));
   if (K == 0 || p->dp.m == 0) return TRS_OK;
   if (!C || (p->dp.n > 0 && !B) || ldb < K || ldc < K)
     return report(fail(TRS_EINVAL, "trs_spmm_f16: NULL operand or leading dimension < K"));
@@ -741,22 +885,50 @@ int trs_spmm_f16_timed(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_
   return TRS_OK;
 }
 
-int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int32_t K,
-                  float* out, void* stream) {
+static int sddmm_impl(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int32_t K,
+                      float* out, void* stream, hipEvent_t* ev) {
   int rc = check_call(p, K);
   if (rc) return rc;
-  if (!p->csr_only) return report(fail(TRS_EINVAL, "trs_sddmm_f16: needs a plan from trs_plan_create_csr"));
-  if (p->dp.nnz_csr == 0) return TRS_OK;
+  if (!p->csr_only)
+    return report(fail(TRS_EINVAL, "trs_sddmm_f16: needs a plan from trs_plan_create_sddmm or trs_plan_create_csr"));
+  if (p->stats.nnz == 0) return TRS_OK;
   if (!out || !X || !Y || (K > 0 && (ldx < K || ldy < K)))
     return report(fail(TRS_EINVAL, "trs_sddmm_f16: NULL operand or leading dimension < K"));
   if (K == 0) {
-    if (hipMemsetAsync(out, 0, p->dp.nnz_csr * sizeof(float), static_cast<hipStream_t>(stream)) != hipSuccess)
+    if (hipMemsetAsync(out, 0, p->stats.nnz * sizeof(float), static_cast<hipStream_t>(stream)) != hipSuccess)
       return report(fail(TRS_EDEVICE, "hipMemsetAsync failed"));
     return TRS_OK;
   }
-  const hipError_t e = trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, static_cast<hipStream_t>(stream));
+  const hipError_t e = trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, static_cast<hipStream_t>(stream), ev);
   if (e != hipSuccess) return report(fail(TRS_EDEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e)));
   return TRS_OK;
+}
+
+int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int32_t K,
+                  float* out, void* stream) {
+  return sddmm_impl(p, X, ldx, Y, ldy, K, out, stream, nullptr);
+}
+
+int trs_sddmm_f16_kernel_ms(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                            int32_t K, float* out, void* stream, int32_t iters, float* ms) {
+  if (!ms || iters <= 0) return report(fail(TRS_EINVAL, "trs_sddmm_f16_kernel_ms: needs ms[2] and iters > 0"));
+  ms[0] = ms[1] = 0.f;
+  hipEvent_t ev[3];
+  for (auto& e : ev)
+    if (hipEventCreate(&e) != hipSuccess) return report(fail(TRS_EDEVICE, "hipEventCreate failed"));
+  int rc = TRS_OK;
+  for (int i = 0; i < iters && rc == TRS_OK; ++i) {
+    rc = sddmm_impl(p, X, ldx, Y, ldy, K, out, stream, ev);
+    if (rc) break;
+    (void)hipEventSynchronize(ev[2]);
+    for (int k = 0; k < 2; ++k) {
+      float t = 0.f;
+      (void)hipEventElapsedTime(&t, ev[k], ev[k + 1]);
+      ms[k] += t / (float)iters;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  return rc;
 }
 
 }  // extern "C"

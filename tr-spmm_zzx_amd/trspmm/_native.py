@@ -29,7 +29,8 @@ class BuildParams(ctypes.Structure):
 
 class PlanOptions(ctypes.Structure):
     _fields_ = [("mfma_tc", c_i32), ("mfma_sptc", c_i32), ("sptc_min_fill", c_f32), ("task_nnz", c_i32),
-                ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32)]
+                ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
+                ("xcd_run", c_i32)]
 
 
 class PlanStats(ctypes.Structure):
@@ -56,6 +57,7 @@ PROTOTYPES = {
     "trs_plan_create_sptc_packed": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_i32, c_i32, c_i32,
                                             ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_csr": (c_i32, [c_p, c_p, c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
+    "trs_plan_create_sddmm": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_stats_get": (c_i32, [c_p, ctypes.POINTER(PlanStats)]),
     "trs_plan_free": (None, [c_p]),
     "trs_spmm_workspace_bytes": (c_i64, [c_p, c_i32]),
@@ -65,6 +67,7 @@ PROTOTYPES = {
                                    ctypes.POINTER(c_f32)]),
     "trs_spmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_i32,
                                        ctypes.POINTER(c_f32)]),
+    "trs_sddmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p, c_i32, ctypes.POINTER(c_f32)]),
     "trs_last_error": (ctypes.c_char_p, []),
 }
 
