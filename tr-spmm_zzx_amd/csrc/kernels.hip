@@ -45,10 +45,13 @@ struct BFrag<8> {
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = __builtin_fmaf(a, (float)v[i], acc[i]);
   }
+  // v_dot2_f32_f16: two fp16 products (exact in fp32) added to an fp32 accumulator per instruction
   __device__ __forceinline__ float dot(const BFrag& o) const {
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s = __builtin_fmaf((float)v[i], (float)o.v[i], s);
+    for (int i = 0; i < 4; ++i)
+      s = __builtin_amdgcn_fdot2(half2_t{v[2 * i], v[2 * i + 1]}, half2_t{o.v[2 * i], o.v[2 * i + 1]}, s, false);
     return s;
   }
 };
@@ -372,57 +375,102 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
 }
 
 // ------------------------------------------------------------------------------------------------
+// Sum v[i] (i < U) over the LPG lanes of a group, U <= LPG (powers of two), with LPG - 1 shuffles
+// in total: log2(U) halving exchanges, after which lane li holds a partial sum of entry
+// e = li / (LPG / U), then log2(LPG / U) xor steps finish it.  Returns that entry's sum.
+template <int LPG, int U>
+__device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
+#pragma unroll
+  for (int w = U / 2, off = LPG / 2; w >= 1; w >>= 1, off >>= 1) {
+    const bool upper = (li & off) != 0;
+#pragma unroll
+    for (int i = 0; i < w; ++i) {
+      const float send = upper ? v[i] : v[i + w];
+      const float keep = upper ? v[i + w] : v[i];
+      v[i] = keep + __shfl_xor(send, off, 64);
+    }
+  }
+#pragma unroll
+  for (int off = LPG / (2 * U); off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
+  return v[0];
+}
+
+// Residual SDDMM: a lane group streams its task's entries U at a time (rows from the row pointers
+// preloaded into LDS, as in k_spmm_tasks); each lane forms partial dot products over its VEC
+// features of X[row] and Y[col] (X rows repeat across a row's entries and stay cached), and the
+// U sums are finished by reduce_scatter.  Pieces of long rows carry a single row.
 template <int VEC, int LPG, int U>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
                                                      float* __restrict__ out) {
   constexpr int GPW = 64 / LPG;
-  constexpr int FPP = LPG * VEC;   // features per pass
+  constexpr int FPP = LPG * VEC;               // features per pass
+  constexpr int UB = U < LPG ? U : LPG;        // entries per reduce_scatter batch
+  __shared__ int s_rp[4][GPW][kTaskRows + 1];
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int task_id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
-  const bool valid = task_id < P.ntasks;
-  const Task t = P.tasks[valid ? task_id : 0];
+  const int grp = lane / LPG;
   const int li = lane % LPG;
-  // rows of a task: whole rows [row_begin, row_end) or one piece of a row
-  const int rb = t.row_begin;
-  const int re = t.row_end < 0 ? t.row_begin + 1 : t.row_end;
-  int p_lo = t.nz_begin;
-  for (int r = rb; r < re; ++r) {
-    const int p_hi = t.row_end < 0 ? t.nz_end : min(t.nz_end, P.rowptr[r + 1]);
-    for (int p = p_lo; p < p_hi; p += U) {
-      float s[U];
+  const int task_id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + wave) * GPW + grp;
+  const bool valid = task_id < P.ntasks;
+  const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
+  const bool piece = t.row_end < 0;
+  int* rp = s_rp[wave][grp];
+  if (valid && !piece)
+    for (int j = li; j <= t.row_end - t.row_begin; j += LPG) rp[j] = P.rowptr[t.row_begin + j];
+  __syncthreads();
+  if (!valid) return;
+
+  int r = 0;
+  int rend = piece ? t.nz_end : rp[1];
+  for (int p = t.nz_begin; p < t.nz_end; p += U) {
+    int cc[U], rr[U];
 #pragma unroll
-      for (int i = 0; i < U; ++i) s[i] = 0.f;
-      for (int f0 = 0; f0 < K; f0 += FPP) {
-        const int f = f0 + li * VEC;
-        const bool act = valid && f < K;
-        BFrag<VEC> x;
-        if (act) x.load(X + (int64_t)r * ldx + f);
-        else x.zero();
-        int cc[U];
-#pragma unroll
-        for (int i = 0; i < U; ++i) cc[i] = (p + i < p_hi) ? P.col[p + i] : 0;
-        BFrag<VEC> y[U];
-#pragma unroll
-        for (int i = 0; i < U; ++i) {
-          if (act && p + i < p_hi) y[i].load(Y + (int64_t)cc[i] * ldy + f);
-          else y[i].zero();
+    for (int i = 0; i < U; ++i) {
+      const bool in = p + i < t.nz_end;
+      cc[i] = in ? P.col[p + i] : 0;
+      if (in && !piece) {
+        while (p + i >= rend) {
+          ++r;
+          rend = rp[r + 1];
         }
+      }
+      rr[i] = t.row_begin + r;
+    }
+    float s[U];
 #pragma unroll
-        for (int i = 0; i < U; ++i) s[i] += x.dot(y[i]);
+    for (int i = 0; i < U; ++i) s[i] = 0.f;
+    for (int f0 = 0; f0 < K; f0 += FPP) {
+      const int f = f0 + li * VEC;
+      // all Y gathers first, then one X fetch per distinct row of the chunk; the fragment each
+      // entry uses is selected in registers afterwards, so no load waits on another
+      BFrag<VEC> x[U], y[U];
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        if (f < K && p + i < t.nz_end) y[i].load(Y + (int64_t)cc[i] * ldy + f);
+        else y[i].zero();
       }
 #pragma unroll
       for (int i = 0; i < U; ++i) {
-#pragma unroll
-        for (int o = LPG / 2; o > 0; o >>= 1) s[i] += __shfl_xor(s[i], o, 64);
+        if (f < K && p + i < t.nz_end && (i == 0 || rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
+        else x[i].zero();
       }
-      if (valid && li == 0) {
+      BFrag<VEC> xe = x[0];
 #pragma unroll
-        for (int i = 0; i < U; ++i)
-          if (p + i < p_hi) out[P.res_pos ? P.res_pos[p + i] : p + i] = s[i];
+      for (int i = 0; i < U; ++i) {
+        if (i > 0 && rr[i] != rr[i - 1]) xe = x[i];
+        s[i] += xe.dot(y[i]);
       }
     }
-    p_lo = p_hi;
+#pragma unroll
+    for (int b = 0; b < U; b += UB) {
+      float v[UB];
+#pragma unroll
+      for (int i = 0; i < UB; ++i) v[i] = s[b + i];
+      const float sum = reduce_scatter<LPG, UB>(v, li);
+      const int e = b + li / (LPG / UB);
+      if (li % (LPG / UB) == 0 && p + e < t.nz_end) out[P.res_pos ? P.res_pos[p + e] : p + e] = sum;
+    }
   }
 }
 
@@ -540,7 +588,13 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     const int lpg = lanes_for(K, VEC);
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb);
-#define TRS_SD(L) case L: hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break;
+#define TRS_SD(L)                                                                                          \
+  case L:                                                                                                  \
+    if (p.sddmm_unroll == 4 || (p.sddmm_unroll == 0 && L >= 8))                                            \
+      hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
+    else                                                                                                   \
+      hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 8>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
+    break;
     switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
 #undef TRS_SD
   }

@@ -156,11 +156,12 @@ class Plan:
     @classmethod
     def for_sddmm(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
                   sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
-                  feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None) -> "Plan":
+                  feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
+                  sddmm_unroll: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
-                     feature_lanes=feature_lanes, xcd_run=xcd_run)
+                     feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
                   "trs_plan_create_sddmm")
