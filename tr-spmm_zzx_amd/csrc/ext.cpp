@@ -120,20 +120,31 @@ std::vector<torch::Tensor> block_sptc_2to4_online_with_spill(torch::Tensor row1,
                     sptc_min_util, sptc_threshold, true);
 }
 
-// Run a plan on a CPU rhs with the reference's timing semantics; returns (out CPU, ms_avg).
-std::pair<torch::Tensor, float> run_plan(trs_plan* plan, torch::Tensor rhs, int dimN, int mOri, int kOri, int epoches) {
+struct RunResult {
+  torch::Tensor out;
+  float ms = 0.f;
+  float kernel_ms[3] = {0.f, 0.f, 0.f};   // residual tasks, MFMA windows, split-row fixups
+};
+
+// Run a plan on a CPU rhs with the reference's timing semantics: 10 warm-up launches, `epoches`
+// timed launches (mGCNkernel_online.cu:1604-1674); the result of the last launch is returned.
+RunResult run_plan(trs_plan* plan, torch::Tensor rhs, int dimN, int mOri, int kOri, int epoches) {
   auto dev = torch::TensorOptions().device(torch::kCUDA);
   torch::Tensor B = rhs.reshape({kOri, dimN}).to(dev.dtype(torch::kFloat16));
   torch::Tensor C = torch::empty({mOri, dimN}, dev.dtype(torch::kFloat32));
   const int64_t wsb = trs_spmm_workspace_bytes(plan, dimN);
   torch::Tensor ws = torch::empty({std::max<int64_t>(wsb, 1)}, dev.dtype(torch::kUInt8));
   torch::cuda::synchronize();
-  float ms = 0.f;
-  ok(trs_spmm_f16_timed(plan, reinterpret_cast<const uint16_t*>(B.data_ptr()), dimN, dimN, C.data_ptr<float>(), dimN,
-                        ws.data_ptr(), wsb, nullptr, 10, epoches, &ms),
+  RunResult r;
+  const uint16_t* b = reinterpret_cast<const uint16_t*>(B.data_ptr());
+  ok(trs_spmm_f16_timed(plan, b, dimN, dimN, C.data_ptr<float>(), dimN, ws.data_ptr(), wsb, nullptr, 10, epoches, &r.ms),
      "spmm");
+  ok(trs_spmm_f16_kernel_ms(plan, b, dimN, dimN, C.data_ptr<float>(), dimN, ws.data_ptr(), wsb, nullptr, epoches,
+                            r.kernel_ms),
+     "spmm kernel timing");
   torch::cuda::synchronize();
-  return {C.cpu(), ms};
+  r.out = C.cpu();
+  return r;
 }
 
 void common_checks(int window, int dimN, int mOri, int kOri, int epoches, const torch::Tensor& rhs,
@@ -287,9 +298,11 @@ std::vector<torch::Tensor> parallel_online(
   PlanGuard pg;
   ok(trs_plan_create_parallel(&a, nullptr, &pg.p), "forward_fp16_tcu_cuda_sptc_mma_parallel_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
-  // one fused launch sequence: every share completes together
-  auto ms = torch::tensor(res.second);
-  return {res.first, ms, ms.clone(), ms.clone(), ms.clone(), ms.clone()};
+  // per-share times: the MFMA window kernel carries the TC (and dense 2:4) share, the residual
+  // task kernel the long residual parts, the fixup the split rows; 2:4 groups are folded into
+  // those two kernels, so no separate time exists for them (0)
+  return {res.out, torch::tensor(res.ms), torch::tensor(res.kernel_ms[1]), torch::tensor(res.kernel_ms[0]),
+          torch::tensor(res.kernel_ms[2]), torch::tensor(0.0f)};
 }
 
 std::vector<torch::Tensor> sptc_online(torch::Tensor s_column, torch::Tensor s_value, torch::Tensor s_pos,
@@ -320,7 +333,7 @@ std::vector<torch::Tensor> sptc_online(torch::Tensor s_column, torch::Tensor s_v
                           s_window.data_ptr<int32_t>(), nullptr, 0, window, mOri, kOri, nullptr, &pg.p),
      "forward_fp16_sptc_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
-  return {res.first, torch::tensor(res.second)};
+  return {res.out, torch::tensor(res.ms)};
 }
 
 std::vector<torch::Tensor> sptc_mma_online(torch::Tensor s_column, torch::Tensor s_value, torch::Tensor s_pos,
@@ -351,7 +364,7 @@ std::vector<torch::Tensor> sptc_mma_online(torch::Tensor s_column, torch::Tensor
                           &pg.p),
      "forward_fp16_sptc_mma_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
-  return {res.first, torch::tensor(res.second)};
+  return {res.out, torch::tensor(res.ms)};
 }
 
 std::vector<torch::Tensor> sptc_mma_packed_online(torch::Tensor s_tile_column, torch::Tensor s_packed_a,
@@ -386,7 +399,7 @@ std::vector<torch::Tensor> sptc_mma_packed_online(torch::Tensor s_tile_column, t
                                  s_window_tile_offset.numel(), window, mOri, kOri, nullptr, &pg.p),
      "forward_fp16_sptc_mma_packed_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
-  return {res.first, torch::tensor(res.second)};
+  return {res.out, torch::tensor(res.ms)};
 }
 
 }  // namespace

@@ -43,7 +43,10 @@ class Format:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            nat.lib().trs_format_free(h)
+            try:
+                nat.lib().trs_format_free(h)
+            except (TypeError, AttributeError):   # interpreter shutdown: module globals already gone
+                pass
             self._h = ctypes.c_void_p(0)
 
     @property
@@ -136,7 +139,10 @@ class Plan:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h is not None and h.value:
-            nat.lib().trs_plan_free(h)
+            try:
+                nat.lib().trs_plan_free(h)
+            except (TypeError, AttributeError):   # interpreter shutdown: module globals already gone
+                pass
             self._h = ctypes.c_void_p(0)
 
     @classmethod
