@@ -95,7 +95,7 @@ typedef struct trs_plan_options {
                              consecutive work items in a row; 1 = hardware round robin,
                              0 = automatic */
   int32_t sddmm_unroll;   /* SDDMM residual entries in flight per lane group: 4 or 8; 0 = automatic
-                             (4 when a group has >= 8 lanes, i.e. K >= 64: register pressure) */
+                             (8) */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

@@ -109,28 +109,42 @@ __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
 }
 
-// Accumulate entries [p0, p1) of one row into acc (U loads in flight).
+// Loads of one batch of U entries [p, p + U) of a stream ending at `end` (> p): column ids, fp16
+// values and the gathered B fragments.  Every load is unconditional -- indices past the end are
+// clamped to the last entry and lanes past K read features [0, VEC) -- so the batch issues as one
+// run of loads with no branch between them (a load under a branch makes the compiler wait for
+// all earlier loads first, leaving one gather in flight per wave).  Callers ignore the padded
+// slots and lanes.
+template <int VEC, int U, bool NT>
+struct Batch {
+  int32_t cc[U];
+  uint16_t vh[U];
+  BFrag<VEC> bb[U];
+  __device__ __forceinline__ void load(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
+                                       const uint16_t* __restrict__ Bf, int64_t ldb, int p, int end) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = p + i < end ? p + i : end - 1;
+      cc[i] = load_stream<NT>(col + q);
+      vh[i] = load_stream<NT>(val + q);
+    }
+#pragma unroll
+    for (int i = 0; i < U; ++i) bb[i].load(Bf + (int64_t)(uint32_t)cc[i] * ldb);
+  }
+};
+
+// Accumulate entries [p0, p1) of one row into acc (U loads in flight).  Bf = B + feature offset
+// (a valid column for lanes past K, whose sums are discarded).
 template <int VEC, int U, bool NT = false>
 __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
-                                               const uint16_t* __restrict__ B, int64_t ldb, int f, bool active,
-                                               int p0, int p1, float (&acc)[VEC]) {
+                                               const uint16_t* __restrict__ Bf, int64_t ldb, int p0, int p1,
+                                               float (&acc)[VEC]) {
   for (int p = p0; p < p1; p += U) {
-    int cc[U];
-    float vv[U];
-    BFrag<VEC> bb[U];
+    Batch<VEC, U, NT> b;
+    b.load(col, val, Bf, ldb, p, p1);
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const bool in = p + i < p1;
-      cc[i] = in ? load_stream<NT>(col + p + i) : 0;
-      vv[i] = in ? h2f(load_stream<NT>(val + p + i)) : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      if (active && p + i < p1) bb[i].load(B + (int64_t)cc[i] * ldb + f);
-      else bb[i].zero();
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) bb[i].fma(acc, vv[i]);
+    for (int i = 0; i < U; ++i)
+      if (p + i < p1) b.bb[i].fma(acc, h2f(b.vh[i]));
   }
 }
 
@@ -165,13 +179,14 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
 
   const int f = blockIdx.y * (LPG * VEC) + li * VEC;
   const bool active = f < K;
+  const uint16_t* __restrict__ Bf = B + (active ? f : 0);
   const int32_t* __restrict__ col = P.col;
   const uint16_t* __restrict__ val = P.val;
   float acc[VEC];
   zero_acc(acc);
 
   if (t.row_end < 0) {   // piece of a split row -> partial slot (re-read by the fixup: keep cached)
-    accumulate_row<VEC, U, NTL>(col, val, B, ldb, f, active, t.nz_begin, t.nz_end, acc);
+    accumulate_row<VEC, U, NTL>(col, val, Bf, ldb, t.nz_begin, t.nz_end, acc);
     if (active) store_vec<VEC>(partial + (int64_t)(~t.row_end) * K + f, acc);
     return;
   }
@@ -179,20 +194,8 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   int r = 0;                       // row index relative to row_begin
   int rend = rp[1];
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
-    int cc[U];
-    float vv[U];
-    BFrag<VEC> bb[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const bool in = p + i < t.nz_end;
-      cc[i] = in ? load_stream<NTL>(col + p + i) : 0;
-      vv[i] = in ? h2f(load_stream<NTL>(val + p + i)) : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < U; ++i) {
-      if (active && p + i < t.nz_end) bb[i].load(B + (int64_t)cc[i] * ldb + f);
-      else bb[i].zero();
-    }
+    Batch<VEC, U, NTL> b;
+    b.load(col, val, Bf, ldb, p, t.nz_end);
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       if (p + i < t.nz_end) {
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
           ++r;
           rend = rp[r + 1];
         }
-        bb[i].fma(acc, vv[i]);
+        b.bb[i].fma(acc, h2f(b.vh[i]));
       }
     }
   }
@@ -317,7 +320,7 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
       const int ff = (idx % per_row) * VEC;
       const int c = P.tile_cols[t * 16 + k];
       BFrag<VEC> b;
-      if (c >= 0 && fbase + ff < K) b.load(B + (int64_t)c * ldb + fbase + ff);
+      if (c >= 0 && fbase + ff < K) b.load(B + (int64_t)(uint32_t)c * ldb + fbase + ff);
       else b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
       else bst[k * KCB + ff] = b.v;
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
     if (row >= P.m) break;
     float racc[VEC];
     zero_acc(racc);
-    accumulate_row<VEC, 8>(P.col, P.val, B, ldb, f, f < K, P.rowptr[row], P.rowptr[row + 1], racc);
+    accumulate_row<VEC, 8>(P.col, P.val, B + (f < K ? f : 0), ldb, P.rowptr[row], P.rowptr[row + 1], racc);
     if (f >= K) continue;
     const float* src = otile + rl * KCP + ff;
     if constexpr (VEC == 8) {
@@ -426,9 +429,10 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U], rr[U];
 #pragma unroll
+    for (int i = 0; i < U; ++i) cc[i] = P.col[p + i < t.nz_end ? p + i : t.nz_end - 1];   // unconditional loads
+#pragma unroll
     for (int i = 0; i < U; ++i) {
       const bool in = p + i < t.nz_end;
-      cc[i] = in ? P.col[p + i] : 0;
       if (in && !piece) {
         while (p + i >= rend) {
           ++r;
@@ -442,14 +446,13 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
     for (int i = 0; i < U; ++i) s[i] = 0.f;
     for (int f0 = 0; f0 < K; f0 += FPP) {
       const int f = f0 + li * VEC;
-      // all Y gathers first, then one X fetch per distinct row of the chunk; the fragment each
-      // entry uses is selected in registers afterwards, so no load waits on another
+      // all Y gathers first, unconditional so they issue back to back (lanes past K read features
+      // [0, VEC) and padded slots repeat the last entry; both are discarded), then one X fetch per
+      // distinct row of the chunk; the fragment each entry uses is selected in registers
       BFrag<VEC> x[U], y[U];
+      const uint16_t* __restrict__ Yf = Y + (f < K ? f : 0);
 #pragma unroll
-      for (int i = 0; i < U; ++i) {
-        if (f < K && p + i < t.nz_end) y[i].load(Y + (int64_t)cc[i] * ldy + f);
-        else y[i].zero();
-      }
+      for (int i = 0; i < U; ++i) y[i].load(Yf + (int64_t)(uint32_t)cc[i] * ldy);
 #pragma unroll
       for (int i = 0; i < U; ++i) {
         if (f < K && p + i < t.nz_end && (i == 0 || rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
@@ -540,15 +543,20 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   if (p.ntasks > 0) {
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb, passes);
+    // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
+    // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
+    // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
 #define TRS_TASKS(L)                                                                                      \
-  case L:                                                                                                 \
+  case L: {                                                                                               \
+    constexpr int U = L >= 16 ? 2 : 8;                                                                    \
     switch (p.streaming & 3) {                                                                            \
-      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 0>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 1>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 2>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, 8, 3>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
     }                                                                                                     \
-    break;
+    break;                                                                                                \
+  }
     switch (lpg) { TRS_TASKS(1) TRS_TASKS(2) TRS_TASKS(4) TRS_TASKS(8) TRS_TASKS(16) TRS_TASKS(32) TRS_TASKS(64) }
 #undef TRS_TASKS
   }
@@ -590,7 +598,7 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     dim3 grid((p.ntasks + gpb - 1) / gpb);
 #define TRS_SD(L)                                                                                          \
   case L:                                                                                                  \
-    if (p.sddmm_unroll == 4 || (p.sddmm_unroll == 0 && L >= 8))                                            \
+    if (p.sddmm_unroll == 4)                                                                               \
       hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
     else                                                                                                   \
       hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 8>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
