@@ -26,7 +26,8 @@ typedef enum trs_status {
   TRS_ENOMEM = 2,     /* host or device allocation failed */
   TRS_EDEVICE = 3,    /* HIP runtime error (no GPU, launch failure, ...) */
   TRS_ENOTCANON = 4,  /* CSR rows not strictly increasing: a plan cannot be built from it */
-  TRS_ERANGE = 5      /* index outside [0, rows) / [0, cols), or size beyond int32 addressing */
+  TRS_ERANGE = 5,     /* index outside [0, rows) / [0, cols), or size beyond int32 addressing */
+  TRS_EIO = 6         /* format file cannot be opened / written, or is not a valid format file */
 } trs_status;
 
 /* ---------------------------------------------------------------------------------------------
@@ -69,6 +70,15 @@ int32_t trs_format_window(const trs_format* f);
 int32_t trs_format_rows(const trs_format* f);
 int32_t trs_format_canonical(const trs_format* f); /* 1 if every row had increasing columns */
 void trs_format_free(trs_format* f);
+
+/* Format cache.  No counterpart in the reference, which rebuilds the format on every run
+ * (spmm/tr_csr_fp16/mdataset2_online.py:100-113); for callers that reuse a graph across runs.
+ * One versioned little-endian file holds all 32 slots, rows, window, the canonical flag and the
+ * build time, with a 64-bit checksum.  trs_format_write writes to "<path>.tmp" and renames, so a
+ * reader never sees a partial file; trs_format_read refuses truncated, corrupted or other-version
+ * files with TRS_EIO.  A read format is used exactly like a built one. */
+int trs_format_write(const trs_format* f, const char* path);
+int trs_format_read(const char* path, trs_format** out);
 
 /* ---------------------------------------------------------------------------------------------
  * Plans.  A plan lowers format arrays to the device layout the kernels read (dense 16x16 fp16

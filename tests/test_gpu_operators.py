@@ -100,3 +100,48 @@ def test_operator_argument_errors():
         L6.forward_fp16_sptc_online(t[17], t[19].double(), t[20], t[21], x, 16, 32, g.m, g.n, 1)
     with pytest.raises(RuntimeError, match="CPU"):
         L6.forward_fp16_sptc_mma_packed_online(t[25].cuda(), t[26], t[27], t[28], x, 16, 32, g.m, g.n, 1)
+
+
+def test_reference_harness_flow_through_dataset(tmp_path, monkeypatch):
+    """spmm/tr_csr_fp16/test_tr_csr_online.py:77-152 on top of this library: dataset class ->
+    parallel operator with the dataset's attributes, checked against the oracle's reading of the
+    same arrays, and with the dataset's spill against the full CSR SpMM."""
+    import Libra6SpMMOnline as L6
+    from tr_csr_fp16.mdataset2_online import GCN_dataset_tcu_sptc_cuda_online
+    say("harness flow")
+    g = graphs.sbm(communities=300, seed=7, val_seed=8)
+    rows = np.repeat(np.arange(g.m_pad), np.diff(g.rowptr))
+    (tmp_path / "d").mkdir()
+    np.savez(tmp_path / "d" / "sbm.npz", src_li=rows, dst_li=g.col.astype(np.int64),
+             num_nodes_src=np.int64(g.m), num_nodes_dst=np.int64(g.n))
+    monkeypatch.setenv("TR_DATA_ROOT", str(tmp_path))
+    monkeypatch.delenv("TR_FORMAT_CACHE", raising=False)
+    monkeypatch.delenv("LIBRA_TCA_REORDER", raising=False)
+    torch.manual_seed(3)
+    d = GCN_dataset_tcu_sptc_cuda_online("sbm", 64, 8, 32, 32, 3, "d", 16, 16)
+    args = (d.t_rowNew_offsetTensor, d.t_blockTensor, d.t_columnTensor, d.t_valueTensor, d.t_window_rowTensor,
+            d.t_atomicTensor, d.t_binaryTensor, d.c_row_offsetTensor, d.c_rowTensor, d.c_atomicTensor,
+            d.c_colTensor, d.c_valueTensor, d.c_row_offsetTensor_short, d.c_rowTensor_short,
+            d.c_atomicTensor_short, d.c_colTensor_short, d.c_valueTensor_short, d.s_columnTensor,
+            d.s_valueTensor, d.s_posTensor, d.s_offsetTensor, d.s_tile_windowTensor, d.s_tile_columnTensor,
+            d.s_packed_aTensor, d.s_packed_metaTensor, d.s_window_tile_offsetTensor, d.x,
+            d.parts_t, d.parts_c, d.partsize_c, d.parts_c_short, d.window, d.x.size(1), d.num_nodes_ori,
+            d.num_nodes_dst, 3)
+    out, ms, tc, cl, cs, sp = L6.forward_fp16_tcu_cuda_sptc_mma_parallel_online(*args)
+    assert out.shape == (g.m, 64) and float(ms) > 0
+    t = [getattr(d, n) for n in ("t_rowNew_offsetTensor", "t_blockTensor", "t_columnTensor", "t_valueTensor",
+                                 "t_window_rowTensor", "t_atomicTensor", "t_binaryTensor", "c_row_offsetTensor",
+                                 "c_rowTensor", "c_atomicTensor", "c_colTensor", "c_valueTensor",
+                                 "c_row_offsetTensor_short", "c_rowTensor_short", "c_atomicTensor_short",
+                                 "c_colTensor_short", "c_valueTensor_short", "s_columnTensor", "s_maskTensor",
+                                 "s_valueTensor", "s_posTensor", "s_windowTensor", "s_offsetTensor",
+                                 "s_tile_windowTensor", "s_tile_groupTensor", "s_tile_columnTensor",
+                                 "s_packed_aTensor", "s_packed_metaTensor", "s_window_tile_offsetTensor")]
+    e = osp.spmm_error(out.numpy(), format_reference(t, g, d.x, False))
+    assert e["elementwise_ok"], e
+    sr, sc, sv = (torch.from_numpy(a) for a in d.spill)
+    full = L6.forward_fp16_tcu_cuda_sptc_mma_parallel_online(*args, spill_row=sr, spill_col=sc, spill_val=sv)[0]
+    vals16 = d.degrees.numpy().astype(np.float16).astype(np.float32)   # the operator computes in fp16
+    e = osp.spmm_error(full.numpy(), osp.csr_spmm(d.row_pointers.numpy(), d.column_index.numpy(), vals16,
+                                                  d.x.numpy(), m=g.m))
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e

@@ -6,4 +6,4 @@ Layers
   ops        Format (builder output), Plan (device plan), spmm / sddmm on torch device tensors
 Drop-in module names live next to this package: Libra5BlockOnline, Libra6SpMMOnline.
 """
-from .ops import Format, Plan, build_format, spmm, sddmm  # noqa: F401
+from .ops import Format, Plan, build_format, build_format_cached, spmm, sddmm  # noqa: F401

@@ -49,6 +49,8 @@ PROTOTYPES = {
     "trs_format_rows": (c_i32, [c_p]),
     "trs_format_canonical": (c_i32, [c_p]),
     "trs_format_free": (None, [c_p]),
+    "trs_format_write": (c_i32, [c_p, ctypes.c_char_p]),
+    "trs_format_read": (c_i32, [ctypes.c_char_p, c_pp]),
     "trs_plan_options_default": (None, [ctypes.POINTER(PlanOptions)]),
     "trs_plan_create": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_parallel": (c_i32, [c_p, ctypes.POINTER(PlanOptions), c_pp]),

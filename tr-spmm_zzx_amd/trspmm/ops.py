@@ -7,6 +7,8 @@ libtrspmm.so; there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import hashlib
+import os
 from typing import Optional, Sequence
 
 import numpy as np
@@ -91,6 +93,31 @@ class Format:
     def spill(self) -> tuple:
         return self.slot(29), self.slot(30), self.slot(31)
 
+    @property
+    def rows(self) -> int:
+        return int(nat.lib().trs_format_rows(self._h))
+
+    def save(self, path) -> None:
+        """Write the format to a cache file (trs_format_write: versioned, checksummed)."""
+        nat.check(nat.lib().trs_format_write(self._h, os.fsencode(path)), "trs_format_write")
+
+    @classmethod
+    def load(cls, path) -> "Format":
+        """Read a format written by :meth:`save`; raises TrsError for missing, truncated or
+        corrupted files."""
+        h = ctypes.c_void_p()
+        nat.check(nat.lib().trs_format_read(os.fsencode(path), ctypes.byref(h)), "trs_format_read")
+        return cls(h.value)
+
+    def tensors(self) -> list:
+        """The reference builder's return list: 29 CPU tensors + the build time as a float64
+        scalar tensor (block_online.cpp:844-870)."""
+        return [torch.from_numpy(a) for a in self.arrays()] + [torch.tensor(self.elapsed, dtype=torch.float64)]
+
+
+_BUILD_DEFAULTS = dict(part_t=32, part_c=32, short_size=3, density=8, window=16, wide=16, tc_min_util=0.0,
+                       sptc_min_util=0.5, sptc_threshold=12, skip_tc=None, unit_min_nnz=None, num_threads=0)
+
 
 def build_format(rowptr, col, val, part_t: int = 32, part_c: int = 32, short_size: int = 3, density: int = 8,
                  window: int = 16, wide: int = 16, tc_min_util: float = 0.0, sptc_min_util: float = 0.5,
@@ -113,6 +140,50 @@ def build_format(rowptr, col, val, part_t: int = 32, part_c: int = 32, short_siz
     nat.check(nat.lib().trs_build_online(_ptr(rowptr), _ptr(col), _ptr(val), rowptr.shape[0] - 1, col.shape[0],
                                          ctypes.byref(p), ctypes.byref(h)), "trs_build_online")
     return Format(h.value)
+
+
+def _env_setting(name: str) -> str:
+    v = os.environ.get(name)
+    return "unset" if v is None else v
+
+
+def format_cache_key(rowptr, col, val, **params) -> str:
+    """Hex digest identifying a builder run: the CSR bytes, every parameter, and the environment
+    settings the builder reads when a parameter is left to the environment."""
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    col = np.ascontiguousarray(col, dtype=np.int32)
+    val = np.ascontiguousarray(val, dtype=np.float32)
+    h = hashlib.sha256()
+    for a in (rowptr, col, val):
+        h.update(np.int64(a.shape[0]).tobytes())
+        h.update(a.tobytes())
+    full = dict(_BUILD_DEFAULTS, **params)
+    full.pop("num_threads", None)             # does not change the output
+    if full.get("skip_tc") is None:
+        full["env_skip_tc"] = _env_setting("LIBRA_SKIP_TC")
+    if full.get("unit_min_nnz") is None:
+        full["env_unit_min_nnz"] = _env_setting("LIBRA_SPTC_UNIT_MIN_NNZ")
+    h.update(repr(sorted(full.items())).encode())
+    return h.hexdigest()
+
+
+def build_format_cached(rowptr, col, val, cache_dir, **params) -> Format:
+    """build_format with a file cache: a format built before for the same CSR, parameters and
+    environment is read back instead of rebuilt (the returned Format's ``from_cache`` says which).
+    A cache file that cannot be read is rebuilt and overwritten."""
+    os.makedirs(cache_dir, exist_ok=True)
+    path = os.path.join(cache_dir, "format-" + format_cache_key(rowptr, col, val, **params)[:40] + ".trsf")
+    if os.path.exists(path):
+        try:
+            f = Format.load(path)
+            f.from_cache = True
+            return f
+        except nat.TrsError:
+            pass
+    f = build_format(rowptr, col, val, **params)
+    f.save(path)
+    f.from_cache = False
+    return f
 
 
 def _options(mfma_tc: bool, mfma_sptc: bool, sptc_min_fill: float, task_nnz: int, **extra) -> nat.PlanOptions:
