@@ -1,6 +1,7 @@
 """Headline benchmark: hybrid fp16 SpMM on the R-MAT 2^20-node graph at K = 128 (one MI355X).
 
     python bench.py [--steps K] [--warmup W] [--config 2|3|5|4] [--no-cpu-baseline]
+                    [--scramble SEED] [--reorder tca]
 
 A step is one SpMM C = A B over the whole graph with A (device plan) and B already resident in
 HBM.  Prints one JSON line with GFLOP/s (2 nnz K / t), the roofline object of the dominant kernel
@@ -43,6 +44,35 @@ def make_workload(cfg: int):
     if cfg == 1:
         return "er4096_k64", graphs.erdos_renyi_gcn(), 64, 1
     raise SystemExit(f"unknown config {cfg}")
+
+
+def scramble(g, seed: int):
+    """Relabel the nodes of a square graph with a seeded random permutation (rows and columns):
+    the same matrix up to P A P^T, with any locality of the node numbering destroyed."""
+    import numpy as np
+    from trspmm import graphs, reorder
+    assert g.m == g.n, "scramble needs a square graph"
+    perm = np.random.default_rng(seed).permutation(g.m)          # new label -> old label
+    inv = np.empty(g.m, dtype=np.int64)
+    inv[perm] = np.arange(g.m)
+    rp, col, val = reorder.permute_rows(g.rowptr[: g.m + 1], g.col, perm, g.val)
+    col = inv[col]
+    rows = np.repeat(np.arange(g.m, dtype=np.int64), np.diff(rp))
+    o = np.lexsort((col, rows))
+    rowptr = np.concatenate([rp, np.full(g.m_pad - g.m, rp[-1], dtype=np.int32)])
+    return graphs.Graph(g.name + "_scrambled", g.m, g.n, rowptr, col[o].astype(np.int32), val[o])
+
+
+def tca_reorder(g):
+    """Row reorder of the reference's optional TCA step (LIBRA_TCA_REORDER=1); returns the
+    reordered graph and the seconds it took."""
+    from trspmm import graphs, reorder
+    t0 = time.time()
+    order = reorder.tca_order(g.rowptr[: g.m + 1], g.col, ncols=g.n)
+    rp, col, val = reorder.permute_rows(g.rowptr[: g.m + 1], g.col, order, g.val)
+    import numpy as np
+    rowptr = np.concatenate([rp, np.full(g.m_pad - g.m, rp[-1], dtype=np.int32)])
+    return graphs.Graph(g.name + "_tca", g.m, g.n, rowptr, col, val), time.time() - t0
 
 
 def kernel_ms(plan, B, C, ws, need, iters=10):
@@ -185,6 +215,10 @@ def main():
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--k", type=int, default=0, help="override the configuration's feature width")
+    ap.add_argument("--scramble", type=int, default=None, metavar="SEED",
+                    help="relabel the graph's nodes with a random permutation first")
+    ap.add_argument("--reorder", choices=["none", "tca"], default="none",
+                    help="TCA row reorder before the builder (timed, reported under 'preprocess')")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -206,13 +240,26 @@ def main():
         K = args.k
         workload = f"{workload.rsplit('_k', 1)[0]}_k{K}" if "_k" in workload else f"{workload}_k{K}"
     log(f"[bench] graph {workload}: m={g.m} nnz={g.nnz} ({time.time() - t0:.1f}s)")
+    pre = {}
+    if args.scramble is not None:
+        g = scramble(g, args.scramble)
+        workload += "_scrambled"
+    if args.reorder == "tca":
+        g, pre["reorder_s"] = tca_reorder(g)
+        workload += "_tca"
+        log(f"[bench] TCA reorder {pre['reorder_s']:.2f}s")
     if args.config == 4:
         bench_sddmm(args, workload, g, K)
         return
     t0 = time.time()
     fmt = trspmm.build_format(g.rowptr, g.col, g.val)
     log(f"[bench] format built in {fmt.elapsed:.2f}s")
+    pre["build_s"] = round(fmt.elapsed, 3)
+    t1 = time.time()
     plan = trspmm.Plan.from_format(fmt, g.m, g.n)
+    pre["plan_s"] = round(time.time() - t1, 3)
+    if "reorder_s" in pre:
+        pre["reorder_s"] = round(pre["reorder_s"], 3)
     st = plan.stats()
     del fmt
     log(f"[bench] plan {st} ({time.time() - t0:.1f}s)")
@@ -276,7 +323,7 @@ def main():
            "vs_baseline": None, "dtype": "f16", "data": "synthetic",
            "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K,
                       "mfma_tiles": st["mfma_tiles"], "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
-           "roofline": roof}
+           "roofline": roof, "preprocess": pre}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(g, Bh, flops)
         log(f"[bench] cpu baseline {out['cpu_baseline']}")

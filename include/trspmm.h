@@ -81,6 +81,36 @@ int trs_format_write(const trs_format* f, const char* path);
 int trs_format_read(const char* path, trs_format** out);
 
 /* ---------------------------------------------------------------------------------------------
+ * Row reorder.
+ * Replaces apply_tca_reorder (spmm/tr_csr_fp16/tr_tca_reorder.py:44-357), which the reference
+ * dataset layer runs before the builder when LIBRA_TCA_REORDER=1 (mdataset2_online.py:72-95):
+ * rows with similar column sets are clustered (MinHash-LSH candidate pairs scored by exact
+ * Jaccard, greedy union-find merging in order of similarity, clusters closing at `thres` rows;
+ * then the clusters' column unions clustered the same way up to `cluster_thres` clusters) and
+ * laid out cluster by cluster.  Deterministic for given parameters and thread-count independent.
+ * ------------------------------------------------------------------------------------------- */
+typedef struct trs_reorder_params {
+  int32_t thres;          /* rows at which a level-1 cluster closes (16) */
+  int32_t cluster_thres;  /* level-1 clusters at which a level-2 group closes (128) */
+  int32_t num_perm;       /* MinHash permutations (128); LSH bands x rows per band are chosen
+                             for lsh_threshold like the reference's LSH library does */
+  float lsh_threshold;    /* Jaccard similarity the LSH banding targets (0.2) */
+  int32_t bucket_span;    /* LSH buckets larger than bucket_span + 1 pair each member with the
+                             next bucket_span members only (64) */
+  int32_t num_threads;    /* host threads; 0 = OpenMP default */
+  int32_t exhaustive;     /* 1: every pair of non-empty sets is a candidate (small inputs, tests) */
+  int32_t reserved;
+  uint64_t seed;          /* MinHash permutation seed (2022) */
+} trs_reorder_params;
+
+void trs_reorder_params_default(trs_reorder_params* p);
+
+/* rowptr[rows+1], col[nnz] on the host, columns in [0, ncols).  order[new_row] = old_row, a
+ * permutation of [0, rows). */
+int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t ncols,
+                    const trs_reorder_params* params, int32_t* order);
+
+/* ---------------------------------------------------------------------------------------------
  * Plans.  A plan lowers format arrays to the device layout the kernels read (dense 16x16 fp16
  * MFMA tiles + an fp16 CSR residual with load-balanced row tasks), validates every index on the
  * host, and uploads once.  m = output rows (mOri), n = rows of the dense operand (kOri).

@@ -10,6 +10,8 @@ Contents
                                    (TR-source/Block/block_online.cpp:545-871) + spill tracking
   spmm.py                          CSR SpMM / SDDMM in float64, and the meaning of every format
                                    array (the semantic spec the GPU plan must honour)
+  tca.py                           the TCA row reorder's clustering and ordering rules
+                                   (spmm/tr_csr_fp16/tr_tca_reorder.py) over exhaustive candidates
   Makefile                         builds _build/liboracle_builder.so and, where the reference
                                    sources exist, _ref/Libra5BlockOnline (the reference builder)
 

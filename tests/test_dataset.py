@@ -184,3 +184,23 @@ def test_dataset_paths(tmp_path, monkeypatch):
     monkeypatch.setenv("TR_RESULTS_DIR", str(tmp_path / "res"))
     p = tr_paths.result_path("a", "b.csv")
     assert p.parent.is_dir() and p.name == "b.csv"
+
+
+def test_dataset_with_tca_reorder(tmp_path, monkeypatch):
+    """LIBRA_TCA_REORDER=1: rows are permuted before the builder (mdataset2_online.py:72-95);
+    the padded rows stay last and every row keeps its column set."""
+    src, dst = _write_dataset(tmp_path, nodes=1000)
+    monkeypatch.setenv("TR_DATA_ROOT", str(tmp_path))
+    monkeypatch.delenv("TR_FORMAT_CACHE", raising=False)
+    monkeypatch.setenv("LIBRA_TCA_REORDER", "1")
+    torch.manual_seed(0)
+    ds = _dataset()
+    order = ds.reorder_id
+    assert order is not None and np.array_equal(np.sort(order), np.arange(1000))
+    ref = sp.coo_matrix((np.ones(len(src)), (src, dst)), shape=(1008, 1000)).tocsr()
+    ref.sort_indices()
+    rp, ci = ds.row_pointers.numpy(), ds.column_index.numpy()
+    assert rp.shape == (1009,) and rp[-1] == ref.nnz and np.all(rp[1001:] == rp[1000])
+    for k in range(0, 1000, 37):
+        assert np.array_equal(ci[rp[k]:rp[k + 1]], ref.indices[ref.indptr[order[k]]:ref.indptr[order[k] + 1]])
+    assert ds.edge_index.shape == (2, ref.nnz)

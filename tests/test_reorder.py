@@ -1,0 +1,125 @@
+"""TCA row reorder (trs_tca_reorder) on the CPU: permutation and determinism properties, the
+clustering rules against the oracle restatement (exhaustive candidates), hand-derived cases that
+pin that restatement, and recovery of planted communities with LSH candidates."""
+import numpy as np
+import pytest
+
+import trspmm
+from trspmm import graphs, reorder, _native as nat
+from oracle import tca as otca
+
+
+def csr(rows_sets):
+    rp = np.zeros(len(rows_sets) + 1, dtype=np.int32)
+    rp[1:] = np.cumsum([len(s) for s in rows_sets])
+    col = np.array([c for s in rows_sets for c in sorted(s)], dtype=np.int32)
+    return rp, col
+
+
+# hand-derived from the reference's rules (tr_tca_reorder.py:145-210, :282-340)
+def test_oracle_hand_cases():
+    # sim-1 pairs (0,2) and (1,3) merge first (key order), each closes at thres=2; the two
+    # clusters have Jaccard 0 but are still candidates and share one level-2 group
+    rp, col = csr([{5}, {1, 2}, {5}, {1, 2}])
+    assert otca.tca_order(rp, col, thres=2) == [0, 2, 1, 3]
+    # equal sizes: the second end folds into the first -> roots 0 then 1; thres=3 lets the
+    # sim-0.5 pair merge into the closed-at-3 check later
+    rp, col = csr([{1, 2}, {7}, {1, 2}, {1, 3}, {7}])
+    # pairs: (0,2)=1, (1,4)=1, (0,3)=1/3, (2,3)=1/3; (0,2) -> {0,2}; (1,4) -> {1,4}; (0,3): 0 root,
+    # 3 root -> size 2 vs 1 -> 3 into 0 -> size 3 closes; (2,3): not roots, root 0 closed -> skip
+    assert otca.cluster([frozenset(s) for s in ({1, 2}, {7}, {1, 2}, {1, 3}, {7})], 3) == [0, 1, 0, 0, 1]
+    assert otca.tca_order(rp, col, thres=3) == [0, 2, 3, 1, 4]
+    # identical disjoint groups of 16 rows come out as contiguous groups
+    sets = [{100 * (i % 5) + j for j in range(4)} for i in range(80)]
+    order = otca.tca_order(*csr(sets), thres=16)
+    assert [o % 5 for o in order] == sorted(o % 5 for o in order)
+    # empty rows are never paired: all-empty input keeps the identity order
+    rp = np.zeros(9, dtype=np.int32)
+    assert otca.tca_order(rp, np.zeros(0, np.int32)) == list(range(8))
+
+
+def random_clustered(rows, seed):
+    rng = np.random.default_rng(seed)
+    sets = []
+    for i in range(rows):
+        if rng.random() < 0.08:
+            sets.append(set())
+            continue
+        base = (i * 7 // 3) % 11
+        s = {base * 20 + int(x) for x in rng.integers(0, 12, size=rng.integers(2, 8))}
+        s |= {int(x) for x in rng.integers(0, 400, size=rng.integers(0, 3))}
+        sets.append(s)
+    return csr(sets)
+
+
+@pytest.mark.parametrize("seed,rows,thres,cthres", [(1, 60, 16, 128), (2, 90, 4, 3), (3, 120, 8, 2),
+                                                    (4, 75, 2, 5), (5, 40, 1, 1)])
+def test_native_matches_oracle_exhaustive(seed, rows, thres, cthres):
+    rp, col = random_clustered(rows, seed)
+    got = reorder.tca_order(rp, col, ncols=420, thres=thres, cluster_thres=cthres, exhaustive=True)
+    want = otca.tca_order(rp, col, thres=thres, cluster_thres=cthres)
+    assert got.tolist() == want
+
+
+def test_planted_oracle_case_matches_native():
+    rp, col = csr([{5}, {1, 2}, {5}, {1, 2}])
+    assert reorder.tca_order(rp, col, thres=2, exhaustive=True).tolist() == [0, 2, 1, 3]
+
+
+def scrambled_sbm(communities, seed):
+    g = graphs.sbm(communities=communities, seed=seed, val_seed=seed + 1)
+    m = g.m
+    perm = np.random.default_rng(seed).permutation(m)          # new label -> old label
+    inv = np.empty(m, np.int64)
+    inv[perm] = np.arange(m)
+    rp, c = reorder.permute_rows(g.rowptr[: m + 1], g.col, perm)
+    return rp, inv[c].astype(np.int32), perm
+
+
+def test_lsh_recovers_communities_and_is_deterministic():
+    rp, col, perm = scrambled_sbm(600, 4)
+    a = reorder.tca_order(rp, col)
+    assert np.array_equal(np.sort(a), np.arange(rp.shape[0] - 1))
+    b = reorder.tca_order(rp, col, num_threads=1)
+    assert np.array_equal(a, b)                                  # thread-count independent
+    comm = (perm[a] // 16).reshape(-1, 16)
+    dominant = np.mean([np.bincount(w).max() / 16 for w in comm])
+    base = (perm // 16).reshape(-1, 16)
+    assert np.mean([np.bincount(w).max() / 16 for w in base]) < 0.2
+    assert dominant > 0.6, dominant
+    c = reorder.tca_order(rp, col, seed=7)                       # another MinHash seed: a permutation too
+    assert np.array_equal(np.sort(c), np.arange(rp.shape[0] - 1))
+
+
+def test_reorder_raises_dense_share():
+    rp, col, perm = scrambled_sbm(400, 9)
+    val = np.ones(col.shape[0], np.float32)
+    before = trspmm.build_format(rp, col, val).slot(3).size
+    order = reorder.tca_order(rp, col)
+    rp2, col2, val2 = reorder.permute_rows(rp, col, order, val)
+    after = trspmm.build_format(rp2, col2, val2).slot(3).size
+    assert before == 0 and after > 0.1 * col.shape[0], (before, after)
+
+
+def test_apply_tca_reorder_interface():
+    rp, col, perm = scrambled_sbm(100, 2)
+    # padded rows past num_nodes are ignored, as the reference slices num_nodes rows
+    m = rp.shape[0] - 1
+    rp_pad = np.concatenate([rp, np.full(16, rp[-1], np.int32)])
+    new_ptr, new_col, rid = reorder.apply_tca_reorder(rp_pad, col, m, thres=16, verbose=False)
+    assert new_ptr.shape == (m + 1,) and new_ptr.dtype == np.int32 and new_col.dtype == np.int32
+    assert rid.shape == (m,) and np.array_equal(np.sort(rid), np.arange(m))
+    for k in (0, 5, m - 1):
+        old = rid[k]
+        assert np.array_equal(new_col[new_ptr[k]:new_ptr[k + 1]], col[rp[old]:rp[old + 1]])
+
+
+def test_reorder_errors():
+    rp, col = csr([{1}, {2}])
+    with pytest.raises(nat.TrsError):
+        reorder.tca_order(rp, col, ncols=2)                      # column 2 out of range
+    with pytest.raises(nat.TrsError):
+        reorder.tca_order(np.array([0, 2, 1], np.int32), np.array([0, 1], np.int32))
+    with pytest.raises(nat.TrsError):
+        reorder.tca_order(rp, col, thres=0)
+    assert reorder.tca_order(np.zeros(1, np.int32), np.zeros(0, np.int32)).shape == (0,)

@@ -1,0 +1,383 @@
+// TCA row reorder (trs_tca_reorder in include/trspmm.h): rows with similar column sets are
+// clustered so that they land in the same 16-row windows, which raises the dense-tile share of the
+// format and the reuse of gathered B rows.  Same procedure as the reference's
+// spmm/tr_csr_fp16/tr_tca_reorder.py:44-357, native and deterministic:
+//
+//   level 1  sets = the rows' column lists.  Candidate pairs from MinHash LSH (b bands of r
+//            signature values, (b, r) minimising the equally weighted false-positive and
+//            false-negative areas for the Jaccard threshold, as the reference's LSH library
+//            does), scored by exact Jaccard, merged greedily in order of similarity by a
+//            union-find whose clusters close once they reach `thres` rows (:145-210)
+//   level 2  sets = the column unions of the level-1 clusters, same procedure, clusters close at
+//            `cluster_thres` level-1 clusters (:212-323)
+//   order    level-2 groups in order of their first cluster, level-1 clusters inside a group in
+//            index order, rows of a cluster in ascending order (:325-340)
+//
+// Deviations (both forced by scale or by the reference being non-deterministic):
+//   * MinHash values come from a fixed 64-bit mixing hash per permutation instead of the LSH
+//     library's SHA-1 of the decimal string, so candidate sets differ from the reference's;
+//   * an LSH bucket with more than `bucket_span` + 1 sets pairs each set with the next
+//     `bucket_span` sets of the bucket only (the reference pairs all, O(bucket^2));
+//   * equal similarities pop in (pair key) order; the reference's queue order for ties depends on
+//     Python's per-process string hashing.
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <queue>
+#include <vector>
+
+#include <omp.h>
+
+#include "format.hpp"
+
+namespace {
+
+// Sets in CSR form: elements of set i are e[off[i] .. off[i+1]), sorted, unique.
+struct Sets {
+  std::vector<int64_t> off;
+  std::vector<int32_t> e;
+  int32_t size() const { return (int32_t)off.size() - 1; }
+  int64_t len(int32_t i) const { return off[i + 1] - off[i]; }
+};
+
+uint64_t mix64(uint64_t x) {   // splitmix64 finaliser
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+double jaccard(const Sets& S, int32_t a, int32_t b) {
+  const int32_t *x = S.e.data() + S.off[a], *xe = S.e.data() + S.off[a + 1];
+  const int32_t *y = S.e.data() + S.off[b], *ye = S.e.data() + S.off[b + 1];
+  const int64_t na = xe - x, nb = ye - y;
+  if (na == 0 || nb == 0) return 0.0;
+  int64_t inter = 0;
+  while (x < xe && y < ye) {
+    if (*x < *y) ++x;
+    else if (*y < *x) ++y;
+    else { ++inter; ++x; ++y; }
+  }
+  const int64_t uni = na + nb - inter;
+  return uni > 0 ? (double)inter / (double)uni : 0.0;
+}
+
+// Area of the LSH false-positive / false-negative probability over [lo, hi] (Simpson, fine grid).
+double area(double lo, double hi, int b, int r, bool positive) {
+  const int n = 2000;
+  const double h = (hi - lo) / n;
+  auto f = [&](double s) {
+    const double p = 1.0 - std::pow(1.0 - std::pow(s, r), b);   // P(candidate | similarity s)
+    return positive ? p : 1.0 - p;
+  };
+  double acc = f(lo) + f(hi);
+  for (int i = 1; i < n; ++i) acc += f(lo + i * h) * (i % 2 ? 4.0 : 2.0);
+  return acc * h / 3.0;
+}
+
+void lsh_bands(double t, int num_perm, int& bands, int& rows) {
+  double best = 1e300;
+  bands = 1;
+  rows = 1;
+  for (int b = 1; b <= num_perm; ++b)
+    for (int r = 1; r <= num_perm / b; ++r) {
+      const double err = 0.5 * area(0.0, t, b, r, true) + 0.5 * area(t, 1.0, b, r, false);
+      if (err < best) { best = err; bands = b; rows = r; }
+    }
+}
+
+struct Pair {
+  double sim;
+  int32_t p1, p2;   // orientation matters: equal-size merges fold p2 into p1
+};
+uint64_t pair_key(int32_t a, int32_t b, int64_t n) {
+  return a < b ? (uint64_t)a * (uint64_t)n + (uint64_t)b : (uint64_t)b * (uint64_t)n + (uint64_t)a;
+}
+
+// Open-addressing set of pair keys (the reference's `sset`), with tombstones.
+class KeySet {
+ public:
+  explicit KeySet(size_t expect) {
+    size_t cap = 1024;
+    while (cap < expect * 2 + 16) cap <<= 1;
+    slot_.assign(cap, kEmpty);
+  }
+  bool contains(uint64_t k) const {
+    for (size_t i = hash(k);; i = (i + 1) & (slot_.size() - 1)) {
+      if (slot_[i] == k) return true;
+      if (slot_[i] == kEmpty) return false;
+    }
+  }
+  void insert(uint64_t k) {
+    if ((used_ + 1) * 2 > slot_.size()) grow();
+    size_t tomb = SIZE_MAX;
+    for (size_t i = hash(k);; i = (i + 1) & (slot_.size() - 1)) {
+      if (slot_[i] == k) return;
+      if (slot_[i] == kTomb && tomb == SIZE_MAX) tomb = i;
+      if (slot_[i] == kEmpty) {
+        if (tomb != SIZE_MAX) slot_[tomb] = k;
+        else { slot_[i] = k; ++used_; }
+        return;
+      }
+    }
+  }
+  void erase(uint64_t k) {
+    for (size_t i = hash(k);; i = (i + 1) & (slot_.size() - 1)) {
+      if (slot_[i] == k) { slot_[i] = kTomb; return; }
+      if (slot_[i] == kEmpty) return;
+    }
+  }
+
+ private:
+  static constexpr uint64_t kEmpty = ~0ull, kTomb = ~0ull - 1;
+  size_t hash(uint64_t k) const { return (size_t)mix64(k) & (slot_.size() - 1); }
+  void grow() {
+    std::vector<uint64_t> old;
+    old.swap(slot_);
+    slot_.assign(old.size() * 2, kEmpty);
+    used_ = 0;
+    for (uint64_t k : old)
+      if (k != kEmpty && k != kTomb) insert(k);
+  }
+  std::vector<uint64_t> slot_;
+  size_t used_ = 0;
+};
+
+// Candidate pairs (a < b) of non-empty sets: MinHash LSH, or every pair when exhaustive.
+std::vector<std::pair<int32_t, int32_t>> candidates(const Sets& S, const trs_reorder_params& prm) {
+  const int32_t n = S.size();
+  std::vector<std::pair<int32_t, int32_t>> out;
+  if (prm.exhaustive) {
+    for (int32_t a = 0; a < n; ++a)
+      if (S.len(a))
+        for (int32_t b = a + 1; b < n; ++b)
+          if (S.len(b)) out.push_back({a, b});
+    return out;
+  }
+  int bands, r;
+  lsh_bands(prm.lsh_threshold, prm.num_perm, bands, r);
+  const int used = bands * r;
+  std::vector<uint64_t> coef(used);
+  for (int k = 0; k < used; ++k) coef[k] = mix64(prm.seed * 0x2545f4914f6cdd1dull + (uint64_t)k + 1);
+  // signatures: per set, the minimum of the k-th hash over its elements
+  std::vector<uint32_t> sig((size_t)n * used, 0xffffffffu);
+#pragma omp parallel for schedule(dynamic, 256)
+  for (int32_t i = 0; i < n; ++i) {
+    uint32_t* s = sig.data() + (size_t)i * used;
+    for (int64_t j = S.off[i]; j < S.off[i + 1]; ++j) {
+      const uint64_t base = mix64((uint64_t)(uint32_t)S.e[j]);
+      for (int k = 0; k < used; ++k) {
+        const uint32_t h = (uint32_t)(mix64(base ^ coef[k]) >> 32);
+        if (h < s[k]) s[k] = h;
+      }
+    }
+  }
+  // per band: (band key, set) sorted; runs of equal keys are buckets
+  std::vector<std::vector<std::pair<int32_t, int32_t>>> per_band(bands);
+  const int span = std::max(1, prm.bucket_span);
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int t = 0; t < bands; ++t) {
+    std::vector<std::pair<uint64_t, int32_t>> kv;
+    kv.reserve(n);
+    for (int32_t i = 0; i < n; ++i) {
+      if (!S.len(i)) continue;
+      uint64_t h = 0x84222325cbf29ce4ull ^ (uint64_t)t;
+      for (int k = 0; k < r; ++k) h = mix64(h ^ sig[(size_t)i * used + t * r + k]);
+      kv.push_back({h, i});
+    }
+    std::sort(kv.begin(), kv.end());
+    auto& dst = per_band[t];
+    for (size_t a = 0; a < kv.size();) {
+      size_t e = a;
+      while (e < kv.size() && kv[e].first == kv[a].first) ++e;
+      for (size_t x = a; x < e; ++x)
+        for (size_t y = x + 1; y < e && y <= x + (size_t)span; ++y) dst.push_back({kv[x].second, kv[y].second});
+      a = e;
+    }
+  }
+  size_t total = 0;
+  for (auto& v : per_band) total += v.size();
+  std::vector<uint64_t> keys;
+  keys.reserve(total);
+  for (auto& v : per_band) {
+    for (auto& p : v) keys.push_back(pair_key(p.first, p.second, n));
+    std::vector<std::pair<int32_t, int32_t>>().swap(v);
+  }
+  std::sort(keys.begin(), keys.end());
+  keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+  out.resize(keys.size());
+  for (size_t i = 0; i < keys.size(); ++i) out[i] = {(int32_t)(keys[i] / (uint64_t)n), (int32_t)(keys[i] % (uint64_t)n)};
+  return out;
+}
+
+// Greedy union-find clustering of the sets (tr_tca_reorder.py:145-210 / :282-323); returns the
+// root of every set.
+std::vector<int32_t> cluster(const Sets& S, int32_t thres, const trs_reorder_params& prm) {
+  const int32_t n = S.size();
+  const auto cand = candidates(S, prm);
+  std::vector<Pair> init(cand.size());
+#pragma omp parallel for schedule(dynamic, 4096)
+  for (int64_t i = 0; i < (int64_t)cand.size(); ++i)
+    init[i] = {jaccard(S, cand[i].first, cand[i].second), cand[i].first, cand[i].second};
+  // max similarity first; ties by pair key, then orientation
+  auto later = [n](const Pair& x, const Pair& y) {
+    if (x.sim != y.sim) return x.sim < y.sim;
+    const uint64_t kx = pair_key(x.p1, x.p2, n), ky = pair_key(y.p1, y.p2, n);
+    if (kx != ky) return kx > ky;
+    return x.p1 > y.p1;
+  };
+  KeySet queued(init.size());
+  for (const auto& p : init) queued.insert(pair_key(p.p1, p.p2, n));
+  std::priority_queue<Pair, std::vector<Pair>, decltype(later)> pq(later, std::move(init));
+
+  std::vector<int32_t> id(n), sz(n, 1);
+  std::vector<uint8_t> closed(n, 0);
+  for (int32_t i = 0; i < n; ++i) id[i] = i;
+  auto root = [&](int32_t i) {
+    while (i != id[i]) {
+      id[i] = id[id[i]];
+      i = id[i];
+    }
+    return i;
+  };
+  int64_t open_clusters = n;
+  while (!pq.empty() && open_clusters > 0) {
+    const Pair it = pq.top();
+    pq.pop();
+    queued.erase(pair_key(it.p1, it.p2, n));
+    const int32_t p1 = it.p1, p2 = it.p2;
+    if (p1 == id[p1] && p2 == id[p2]) {
+      if (closed[p1] || closed[p2]) continue;
+      int32_t into = p1, from = p2;
+      if (sz[p1] < sz[p2]) { into = p2; from = p1; }
+      id[from] = into;
+      --open_clusters;
+      sz[into] += sz[from];
+      if (sz[into] >= thres) {
+        closed[into] = 1;
+        --open_clusters;
+      }
+    } else {
+      const int32_t r1 = root(p1), r2 = root(p2);
+      if (closed[r1] || closed[r2]) continue;
+      const uint64_t k = pair_key(r1, r2, n);
+      if (r1 != r2 && !queued.contains(k)) {
+        pq.push({jaccard(S, r1, r2), r1, r2});
+        queued.insert(k);
+      }
+    }
+  }
+  std::vector<int32_t> out(n);
+  for (int32_t i = 0; i < n; ++i) out[i] = root(i);
+  return out;
+}
+
+// Groups of a root array in first-appearance order, members ascending.
+std::vector<std::vector<int32_t>> groups_of(const std::vector<int32_t>& roots) {
+  const int32_t n = (int32_t)roots.size();
+  std::vector<int32_t> gid(n, -1);
+  std::vector<std::vector<int32_t>> g;
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t r = roots[i];
+    if (gid[r] < 0) {
+      gid[r] = (int32_t)g.size();
+      g.emplace_back();
+    }
+    g[gid[r]].push_back(i);
+  }
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+void trs_reorder_params_default(trs_reorder_params* p) {
+  if (!p) return;
+  p->thres = 16;
+  p->cluster_thres = 128;
+  p->num_perm = 128;
+  p->lsh_threshold = 0.2f;
+  p->bucket_span = 64;
+  p->num_threads = 0;
+  p->exhaustive = 0;
+  p->seed = 2022;
+}
+
+int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t ncols,
+                    const trs_reorder_params* params, int32_t* order) {
+  trs_reorder_params prm;
+  trs_reorder_params_default(&prm);
+  if (params) prm = *params;
+  if (rows < 0 || nnz < 0 || ncols < 0 || !order || (rows > 0 && !rowptr) || (nnz > 0 && !col)) {
+    trs::set_error("trs_tca_reorder: bad arguments");
+    return TRS_EINVAL;
+  }
+  if (prm.thres < 1 || prm.cluster_thres < 1 || prm.num_perm < 1 || prm.num_perm > 1024 ||
+      !(prm.lsh_threshold > 0.0f && prm.lsh_threshold < 1.0f)) {
+    trs::set_error("trs_tca_reorder: thres, cluster_thres >= 1, num_perm in 1..1024, lsh_threshold in (0, 1)");
+    return TRS_EINVAL;
+  }
+  if (rows == 0) return TRS_OK;
+  if (rowptr[0] != 0 || rowptr[rows] != nnz) {
+    trs::set_error("trs_tca_reorder: rowptr must start at 0 and end at nnz");
+    return TRS_EINVAL;
+  }
+  for (int32_t i = 0; i < rows; ++i)
+    if (rowptr[i + 1] < rowptr[i]) {
+      trs::set_error("trs_tca_reorder: rowptr not monotone");
+      return TRS_EINVAL;
+    }
+  for (int64_t j = 0; j < nnz; ++j)
+    if (col[j] < 0 || col[j] >= ncols) {
+      trs::set_error("trs_tca_reorder: column index out of range");
+      return TRS_ERANGE;
+    }
+  const int saved_threads = omp_get_max_threads();
+  if (prm.num_threads > 0) omp_set_num_threads(prm.num_threads);
+  try {
+    // level 1: rows as sets (sorted, duplicates merged)
+    Sets R;
+    R.off.assign(rows + 1, 0);
+    R.e.reserve(nnz);
+    for (int32_t i = 0; i < rows; ++i) {
+      const size_t s = R.e.size();
+      R.e.insert(R.e.end(), col + rowptr[i], col + rowptr[i + 1]);
+      std::sort(R.e.begin() + s, R.e.end());
+      R.e.erase(std::unique(R.e.begin() + s, R.e.end()), R.e.end());
+      R.off[i + 1] = (int64_t)R.e.size();
+    }
+    const auto clusters = groups_of(cluster(R, prm.thres, prm));
+
+    // level 2: clusters as the union of their rows' sets
+    Sets C;
+    C.off.assign(clusters.size() + 1, 0);
+    for (size_t c = 0; c < clusters.size(); ++c) {
+      const size_t s = C.e.size();
+      for (int32_t row : clusters[c]) C.e.insert(C.e.end(), R.e.begin() + R.off[row], R.e.begin() + R.off[row + 1]);
+      std::sort(C.e.begin() + s, C.e.end());
+      C.e.erase(std::unique(C.e.begin() + s, C.e.end()), C.e.end());
+      C.off[c + 1] = (int64_t)C.e.size();
+    }
+    const auto super = groups_of(cluster(C, prm.cluster_thres, prm));
+
+    int32_t k = 0;
+    for (const auto& grp : super)
+      for (int32_t c : grp)
+        for (int32_t row : clusters[c]) order[k++] = row;
+    if (k != rows) {
+      trs::set_error("trs_tca_reorder: internal error (order is not a permutation)");
+      if (prm.num_threads > 0) omp_set_num_threads(saved_threads);
+      return TRS_EINVAL;
+    }
+  } catch (const std::bad_alloc&) {
+    if (prm.num_threads > 0) omp_set_num_threads(saved_threads);
+    trs::set_error("trs_tca_reorder: out of memory");
+    return TRS_ENOMEM;
+  }
+  if (prm.num_threads > 0) omp_set_num_threads(saved_threads);
+  return TRS_OK;
+}
+
+}  // extern "C"

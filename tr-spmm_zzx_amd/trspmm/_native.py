@@ -39,6 +39,12 @@ class PlanStats(ctypes.Structure):
                 ("device_bytes", c_i64), ("mfma_windows", c_i64), ("window_csr_nnz", c_i64)]
 
 
+class ReorderParams(ctypes.Structure):
+    _fields_ = [("thres", c_i32), ("cluster_thres", c_i32), ("num_perm", c_i32), ("lsh_threshold", ctypes.c_float),
+                ("bucket_span", c_i32), ("num_threads", c_i32), ("exhaustive", c_i32), ("reserved", c_i32),
+                ("seed", ctypes.c_uint64)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/trspmm.h
 PROTOTYPES = {
     "trs_build_params_default": (None, [ctypes.POINTER(BuildParams)]),
@@ -50,6 +56,8 @@ PROTOTYPES = {
     "trs_format_canonical": (c_i32, [c_p]),
     "trs_format_free": (None, [c_p]),
     "trs_format_write": (c_i32, [c_p, ctypes.c_char_p]),
+    "trs_reorder_params_default": (None, [ctypes.POINTER(ReorderParams)]),
+    "trs_tca_reorder": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, ctypes.POINTER(ReorderParams), c_p]),
     "trs_format_read": (c_i32, [ctypes.c_char_p, c_pp]),
     "trs_plan_options_default": (None, [ctypes.POINTER(PlanOptions)]),
     "trs_plan_create": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
