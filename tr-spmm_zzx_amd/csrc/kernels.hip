@@ -103,6 +103,24 @@ __device__ __forceinline__ int xcd_remap(int i, int n, int run) {
   return (j / run) * span + x * run + (j % run);
 }
 
+// Row pointers rowptr[row_begin .. row_end] of a multi-row task into the lane group's LDS slice:
+// all loads are issued before the first store (indices clamped to the task's last pointer), so
+// the preload costs one memory round trip instead of one per pointer each lane handles.
+template <int LPG>
+__device__ __forceinline__ void preload_rowptr(const int32_t* __restrict__ rowptr, int row_begin, int nrows, int li,
+                                               int* rp) {
+  constexpr int PER_LANE = (kTaskRows + 1 + LPG - 1) / LPG;
+  int v[PER_LANE];
+#pragma unroll
+  for (int k = 0; k < PER_LANE; ++k) {
+    const int j = li + k * LPG;
+    v[k] = rowptr[row_begin + (j <= nrows ? j : nrows)];
+  }
+#pragma unroll
+  for (int k = 0; k < PER_LANE; ++k)
+    if (li + k * LPG <= nrows) rp[li + k * LPG] = v[k];
+}
+
 template <int VEC>
 __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
 #pragma unroll
@@ -115,36 +133,78 @@ __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
 // run of loads with no branch between them (a load under a branch makes the compiler wait for
 // all earlier loads first, leaving one gather in flight per wave).  Callers ignore the padded
 // slots and lanes.
+//
+// With PF (pipelined) the stream runs one batch deep: the column ids and values of batch b + 1 are
+// loaded right after batch b's gathers are issued, so they arrive while batch b is consumed and a
+// batch costs one memory round trip (its gathers) instead of two.  Whether that pays depends on
+// the shape (see the launchers): it costs registers and raises the number of requests in flight.
 template <int VEC, int U, bool NT>
 struct Batch {
   int32_t cc[U];
   uint16_t vh[U];
   BFrag<VEC> bb[U];
-  __device__ __forceinline__ void load(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
-                                       const uint16_t* __restrict__ Bf, int64_t ldb, int p, int end) {
+  // column ids and values of entries [p, p + U) of a stream [.., end), end > 0; slots at or past
+  // `end` repeat entry end - 1
+  __device__ __forceinline__ void load_a(const int32_t* __restrict__ col, const uint16_t* __restrict__ val, int p,
+                                         int end) {
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const int q = p + i < end ? p + i : end - 1;
       cc[i] = load_stream<NT>(col + q);
       vh[i] = load_stream<NT>(val + q);
     }
+  }
+  __device__ __forceinline__ void gather(const uint16_t* __restrict__ Bf, int64_t ldb) {
 #pragma unroll
     for (int i = 0; i < U; ++i) bb[i].load(Bf + (int64_t)(uint32_t)cc[i] * ldb);
+  }
+  // after gather(): fetch the next batch's column ids and values into n
+  __device__ __forceinline__ void prefetch_next(Batch& n, const int32_t* __restrict__ col,
+                                                const uint16_t* __restrict__ val, int p, int end) const {
+    n.load_a(col, val, p + U, end);
+  }
+  __device__ __forceinline__ void advance(const Batch& n) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      cc[i] = n.cc[i];
+      vh[i] = n.vh[i];
+    }
+  }
+  // one step of a stream over [.., end) at batch start p (first = start of the stream, whose
+  // column ids and values a pipelined stream loaded up front): loads of this batch (+ prefetch)
+  template <bool PF>
+  __device__ __forceinline__ void step_begin(Batch& n, const int32_t* __restrict__ col,
+                                             const uint16_t* __restrict__ val, const uint16_t* __restrict__ Bf,
+                                             int64_t ldb, int p, int end) {
+    if constexpr (PF) {
+      gather(Bf, ldb);
+      prefetch_next(n, col, val, p, end);
+    } else {
+      load_a(col, val, p, end);
+      gather(Bf, ldb);
+    }
+  }
+  template <bool PF>
+  __device__ __forceinline__ void step_end(const Batch& n) {
+    if constexpr (PF) advance(n);
   }
 };
 
 // Accumulate entries [p0, p1) of one row into acc (U loads in flight).  Bf = B + feature offset
 // (a valid column for lanes past K, whose sums are discarded).
-template <int VEC, int U, bool NT = false>
+template <int VEC, int U, bool NT, bool PF>
 __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
                                                const uint16_t* __restrict__ Bf, int64_t ldb, int p0, int p1,
                                                float (&acc)[VEC]) {
+  if (p0 >= p1) return;
+  Batch<VEC, U, NT> b, n;
+  if constexpr (PF) b.load_a(col, val, p0, p1);
   for (int p = p0; p < p1; p += U) {
-    Batch<VEC, U, NT> b;
-    b.load(col, val, Bf, ldb, p, p1);
+    b.template step_begin<PF>(n, col, val, Bf, ldb, p, p1);
 #pragma unroll
     for (int i = 0; i < U; ++i)
       if (p + i < p1) b.bb[i].fma(acc, h2f(b.vh[i]));
+    b.template step_end<PF>(n);
   }
 }
 
@@ -153,7 +213,9 @@ __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, 
 constexpr int kNtLoads = 1;
 constexpr int kNtStores = 2;
 
-template <int VEC, int LPG, int U, int NT>
+// PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
+// together with the row pointers, before the barrier.
+template <int VEC, int LPG, int U, int NT, bool PF>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                     int K, float* __restrict__ C, int64_t ldc,
                                                     float* __restrict__ partial) {
@@ -171,22 +233,31 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const int task_id = (wg * 4 + wave) * GPW + grp;
   const bool valid = task_id < P.ntasks;
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
+  const int32_t* __restrict__ col = P.col;
+  const uint16_t* __restrict__ val = P.val;
   int* rp = s_rp[wave][grp];
-  if (valid && t.row_end >= 0)
-    for (int j = li; j <= t.row_end - t.row_begin; j += LPG) rp[j] = P.rowptr[t.row_begin + j];
+  if (valid && t.row_end >= 0) preload_rowptr<LPG>(P.rowptr, t.row_begin, t.row_end - t.row_begin, li, rp);
+  Batch<VEC, U, NTL> b, n;
+  if constexpr (PF) {
+    if (valid && t.nz_begin < t.nz_end) b.load_a(col, val, t.nz_begin, t.nz_end);
+  }
   __syncthreads();
   if (!valid) return;
 
   const int f = blockIdx.y * (LPG * VEC) + li * VEC;
   const bool active = f < K;
   const uint16_t* __restrict__ Bf = B + (active ? f : 0);
-  const int32_t* __restrict__ col = P.col;
-  const uint16_t* __restrict__ val = P.val;
   float acc[VEC];
   zero_acc(acc);
 
   if (t.row_end < 0) {   // piece of a split row -> partial slot (re-read by the fixup: keep cached)
-    accumulate_row<VEC, U, NTL>(col, val, Bf, ldb, t.nz_begin, t.nz_end, acc);
+    for (int p = t.nz_begin; p < t.nz_end; p += U) {
+      b.template step_begin<PF>(n, col, val, Bf, ldb, p, t.nz_end);
+#pragma unroll
+      for (int i = 0; i < U; ++i)
+        if (p + i < t.nz_end) b.bb[i].fma(acc, h2f(b.vh[i]));
+      b.template step_end<PF>(n);
+    }
     if (active) store_vec<VEC>(partial + (int64_t)(~t.row_end) * K + f, acc);
     return;
   }
@@ -194,8 +265,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   int r = 0;                       // row index relative to row_begin
   int rend = rp[1];
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
-    Batch<VEC, U, NTL> b;
-    b.load(col, val, Bf, ldb, p, t.nz_end);
+    b.template step_begin<PF>(n, col, val, Bf, ldb, p, t.nz_end);
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       if (p + i < t.nz_end) {
@@ -208,6 +278,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
         b.bb[i].fma(acc, h2f(b.vh[i]));
       }
     }
+    b.template step_end<PF>(n);
   }
   for (; t.row_begin + r < t.row_end; ++r) {
     if (active) store_vec<VEC, NTS>(C + (int64_t)(t.row_begin + r) * ldc + f, acc);
@@ -361,7 +432,10 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
     if (row >= P.m) break;
     float racc[VEC];
     zero_acc(racc);
-    accumulate_row<VEC, 8>(P.col, P.val, B + (f < K ? f : 0), ldb, P.rowptr[row], P.rowptr[row + 1], racc);
+    // pipelined residual rows pay for the widest windows only (same-box A/B on SBM: K=256
+    // 1.05 -> 1.01 ms; K=128 0.520 -> 0.544, K=64 0.286 -> 0.304)
+    accumulate_row<VEC, 8, false, (NTILE >= 4)>(P.col, P.val, B + (f < K ? f : 0), ldb, P.rowptr[row],
+                                                 P.rowptr[row + 1], racc);
     if (f >= K) continue;
     const float* src = otile + rl * KCP + ff;
     if constexpr (VEC == 8) {
@@ -419,8 +493,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   const bool piece = t.row_end < 0;
   int* rp = s_rp[wave][grp];
-  if (valid && !piece)
-    for (int j = li; j <= t.row_end - t.row_begin; j += LPG) rp[j] = P.rowptr[t.row_begin + j];
+  if (valid && !piece) preload_rowptr<LPG>(P.rowptr, t.row_begin, t.row_end - t.row_begin, li, rp);
   __syncthreads();
   if (!valid) return;
 
@@ -546,19 +619,29 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
     // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
     // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
+    // pipelined stream for narrow groups with long tasks only (same-box A/B: R-MAT K=32/64
+    // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks) +6%)
+    const bool pf = lpg <= 8 && p.task_nnz >= 64;
+#define TRS_TASKS_NT(L, U, PF)                                                                            \
+    switch (p.streaming & 3) {                                                                            \
+      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+    }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
     constexpr int U = L >= 16 ? 2 : 8;                                                                    \
-    switch (p.streaming & 3) {                                                                            \
-      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+    if constexpr (L <= 8) {                                                                               \
+      if (pf) { TRS_TASKS_NT(L, U, true) } else { TRS_TASKS_NT(L, U, false) }                             \
+    } else {                                                                                              \
+      TRS_TASKS_NT(L, U, false)                                                                           \
     }                                                                                                     \
     break;                                                                                                \
   }
     switch (lpg) { TRS_TASKS(1) TRS_TASKS(2) TRS_TASKS(4) TRS_TASKS(8) TRS_TASKS(16) TRS_TASKS(32) TRS_TASKS(64) }
 #undef TRS_TASKS
+#undef TRS_TASKS_NT
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {

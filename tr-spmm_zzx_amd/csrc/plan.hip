@@ -283,6 +283,7 @@ struct Tasks {
   std::vector<trs::Fixup> fix, wfix;
   int32_t slots = 0;
   int64_t split_rows = 0;
+  int32_t task_nnz = 0;   // entries per packed task (S)
   Status st;
 };
 
@@ -302,6 +303,7 @@ Tasks build_tasks(const std::vector<int32_t>& rowptr, int32_t m, int64_t nent, c
     const double mean = nonempty ? (double)nent / (double)nonempty : 1.0;
     S = (int)std::min(128.0, std::max(32.0, 4.0 * mean));
   }
+  T.task_nnz = S;
   const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
   const int rows_cap = trs::kTaskRows;
   auto is_owned = [&](int32_t r) { return !owned.empty() && owned[r / 16]; };
@@ -507,6 +509,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   d.feature_lanes = opt.feature_lanes;
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
+  d.task_nnz = T.task_nnz;
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   P->csr_only = false;
