@@ -227,13 +227,14 @@ int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K);
 
 /* C[m, K] (float32, row stride ldc) = A_plan (m x n) * B[n, K] (fp16, row stride ldb).
  * Every element of C is written exactly once per call (no prior zeroing needed, no atomics).
- * fp16 products, fp32 accumulation. */
+ * fp16 products, fp32 accumulation.  ldb < 2^31 (TRS_ERANGE otherwise). */
 int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
 /* out[e] = sum_k X[row_e, k] * Y[col_e, k] for every stored entry e of the plan (order: see the
  * plan constructor).  X [m, K], Y [n, K] fp16; out float32 [nnz].  Only SDDMM plans
- * (trs_plan_create_sddmm, trs_plan_create_csr) are accepted. */
+ * (trs_plan_create_sddmm, trs_plan_create_csr) are accepted.  ldy < 2^31 (TRS_ERANGE otherwise).
+ * Kernels only (no memset nodes), so the call can be captured in a HIP graph. */
 int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                   int32_t K, float* out, void* stream);
 

@@ -82,3 +82,14 @@ def test_hybrid_sddmm_matches_closed_form(name, gen, K, mfma):
     got = out.cpu().numpy()
     assert not np.isnan(got).any()
     assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
+
+
+def test_sddmm_zero_width_writes_zeros():
+    g = graphs.random_csr(100, 90, 0.05, seed=6)
+    plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)
+    X = torch.zeros(g.m, 0, dtype=torch.float16, device="cuda")
+    Y = torch.zeros(g.n, 0, dtype=torch.float16, device="cuda")
+    out = torch.full((g.nnz,), float("nan"), device="cuda")
+    plan.sddmm(X, Y, out=out)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0

@@ -177,3 +177,33 @@ def test_plan_from_plain_csr_is_sddmm_only():
     B = torch.zeros(g.n, 16, dtype=torch.float16, device="cuda")
     with pytest.raises(RuntimeError, match="SDDMM"):
         plan.spmm(B)
+
+
+@pytest.mark.parametrize("K", [16, 32, 64, 128])
+@pytest.mark.parametrize("task_nnz", [32, 128])
+def test_pipelined_and_plain_streams_agree(K, task_nnz):
+    """Tasks of >= 64 entries take the pipelined residual stream for K <= 64 (quad-shared column
+    loads for K = 16, 32), shorter ones the plain stream: both against the oracle, and bitwise
+    equal to each other (same summation order)."""
+    say("streams", K, task_nnz)
+    g = graphs.rmat(scale=12, edge_factor=16, seed=8)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, K, seed=3)
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m)
+    C = run_plan(trspmm.Plan.from_format(f, g.m, g.n, task_nnz=task_nnz), Bh)
+    check(C, R, f"K={K} S={task_nnz}")
+
+
+def test_leading_dimension_beyond_int32_is_refused():
+    from trspmm import _native as nat
+    import ctypes
+    g = graphs.random_csr(64, 64, 0.1, seed=2)
+    plan = trspmm.Plan.from_format(trspmm.build_format(g.rowptr, g.col, g.val), g.m, g.n)
+    B = torch.zeros(g.n, 16, dtype=torch.float16, device="cuda")
+    C = torch.zeros(g.m, 16, device="cuda")
+    need = plan.workspace_bytes(16)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    rc = nat.lib().trs_spmm_f16(plan.handle, B.data_ptr(), 1 << 31, 16, C.data_ptr(), 16, ws.data_ptr(), need,
+                                int(torch.cuda.current_stream().cuda_stream))
+    assert rc == 5, nat.lib().trs_last_error()          # TRS_ERANGE, nothing launched
+    assert "2^31" in nat.lib().trs_last_error().decode()

@@ -82,6 +82,12 @@ __device__ __forceinline__ void store_vec(float* dst, const float (&acc)[VEC]) {
   }
 }
 
+// Element offset of row `row` (validated non-negative) in an operand with leading dimension ld
+// (the host guarantees ld < 2^31): one 32 x 32 -> 64-bit multiply per gather.
+__device__ __forceinline__ uint64_t row_offset(int32_t row, int64_t ld) {
+  return (uint64_t)(uint32_t)row * (uint64_t)(uint32_t)ld;
+}
+
 template <bool NT, class T>
 __device__ __forceinline__ T load_stream(const T* p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
@@ -138,7 +144,31 @@ __device__ __forceinline__ void zero_acc(float (&acc)[VEC]) {
 // loaded right after batch b's gathers are issued, so they arrive while batch b is consumed and a
 // batch costs one memory round trip (its gathers) instead of two.  Whether that pays depends on
 // the shape (see the launchers): it costs registers and raises the number of requests in flight.
-template <int VEC, int U, bool NT>
+//
+// G = 2 or 4: the stream is shared by an aligned group of G lanes (one quad or half-quad), which
+// load the batch cooperatively -- lane j of the group loads entries p + j, p + j + G, ... -- and
+// exchange them with DPP quad broadcasts.  Every load instruction of a wave then carries G times
+// fewer column/value requests (a wave with 4-lane groups serves 16 tasks, whose streams sit in 16
+// different cache lines).
+template <int G>
+__device__ __forceinline__ int group_bcast(int v, int k) {   // lane k's v, to every lane of the group
+  static_assert(G == 2 || G == 4, "quad broadcasts");
+  if constexpr (G == 4) {
+    switch (k) {   // quad_perm [k, k, k, k]
+      case 0: return __builtin_amdgcn_mov_dpp(v, 0x00, 0xf, 0xf, false);
+      case 1: return __builtin_amdgcn_mov_dpp(v, 0x55, 0xf, 0xf, false);
+      case 2: return __builtin_amdgcn_mov_dpp(v, 0xaa, 0xf, 0xf, false);
+      default: return __builtin_amdgcn_mov_dpp(v, 0xff, 0xf, 0xf, false);
+    }
+  } else {
+    switch (k) {   // quad_perm [k, k, 2 + k, 2 + k]
+      case 0: return __builtin_amdgcn_mov_dpp(v, 0xa0, 0xf, 0xf, false);
+      default: return __builtin_amdgcn_mov_dpp(v, 0xf5, 0xf, 0xf, false);
+    }
+  }
+}
+
+template <int VEC, int U, bool NT, int G = 0>
 struct Batch {
   int32_t cc[U];
   uint16_t vh[U];
@@ -147,16 +177,33 @@ struct Batch {
   // `end` repeat entry end - 1
   __device__ __forceinline__ void load_a(const int32_t* __restrict__ col, const uint16_t* __restrict__ val, int p,
                                          int end) {
+    if constexpr ((G == 2 || G == 4) && U % G == 0) {
+      constexpr int R = U / G;
+      const int j = (int)(threadIdx.x & (G - 1));
+      int c[R], v[R];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-      const int q = p + i < end ? p + i : end - 1;
-      cc[i] = load_stream<NT>(col + q);
-      vh[i] = load_stream<NT>(val + q);
+      for (int r = 0; r < R; ++r) {
+        const int q = p + r * G + j < end ? p + r * G + j : end - 1;
+        c[r] = load_stream<NT>(col + q);
+        v[r] = load_stream<NT>(val + q);
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        cc[i] = group_bcast<G>(c[i / G], i % G);
+        vh[i] = (uint16_t)group_bcast<G>(v[i / G], i % G);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        const int q = p + i < end ? p + i : end - 1;
+        cc[i] = load_stream<NT>(col + q);
+        vh[i] = load_stream<NT>(val + q);
+      }
     }
   }
   __device__ __forceinline__ void gather(const uint16_t* __restrict__ Bf, int64_t ldb) {
 #pragma unroll
-    for (int i = 0; i < U; ++i) bb[i].load(Bf + (int64_t)(uint32_t)cc[i] * ldb);
+    for (int i = 0; i < U; ++i) bb[i].load(Bf + row_offset(cc[i], ldb));
   }
   // after gather(): fetch the next batch's column ids and values into n
   __device__ __forceinline__ void prefetch_next(Batch& n, const int32_t* __restrict__ col,
@@ -237,7 +284,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const uint16_t* __restrict__ val = P.val;
   int* rp = s_rp[wave][grp];
   if (valid && t.row_end >= 0) preload_rowptr<LPG>(P.rowptr, t.row_begin, t.row_end - t.row_begin, li, rp);
-  Batch<VEC, U, NTL> b, n;
+  Batch<VEC, U, NTL, (LPG == 2 || LPG == 4) ? LPG : 0> b, n;
   if constexpr (PF) {
     if (valid && t.nz_begin < t.nz_end) b.load_a(col, val, t.nz_begin, t.nz_end);
   }
@@ -364,7 +411,9 @@ __global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, fl
 //   D: D[4 * (l / 16) + j][l % 16]
 // Here A = the 16x16 tile (window row x tile column), B = gathered B rows (tile column x feature).
 template <int VEC, int NTILE>
-__global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
+// Occupancy floor for KC <= 128: the register budget of 6 waves per SIMD (measured: 5 waves cost
+// 6% on SBM K=128).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTILE >= 4 ? 1 : 6))) void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                        int K, float* __restrict__ C, int64_t ldc, int KC) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int KCP = KC + 4;   // fp32 output tile row stride
@@ -391,7 +440,7 @@ __global__ __launch_bounds__(256) void k_spmm_mfma_win(DevicePlan P, const uint1
       const int ff = (idx % per_row) * VEC;
       const int c = P.tile_cols[t * 16 + k];
       BFrag<VEC> b;
-      if (c >= 0 && fbase + ff < K) b.load(B + (int64_t)(uint32_t)c * ldb + fbase + ff);
+      if (c >= 0 && fbase + ff < K) b.load(B + row_offset(c, ldb) + fbase + ff);
       else b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
       else bst[k * KCB + ff] = b.v;
@@ -525,7 +574,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       BFrag<VEC> x[U], y[U];
       const uint16_t* __restrict__ Yf = Y + (f < K ? f : 0);
 #pragma unroll
-      for (int i = 0; i < U; ++i) y[i].load(Yf + (int64_t)(uint32_t)cc[i] * ldy);
+      for (int i = 0; i < U; ++i) y[i].load(Yf + row_offset(cc[i], ldy));
 #pragma unroll
       for (int i = 0; i < U; ++i) {
         if (f < K && p + i < t.nz_end && (i == 0 || rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
@@ -703,7 +752,18 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+__global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
+}
+
 }  // namespace
+
+hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_zero_fill, dim3((unsigned)blocks), dim3(256), 0, stream, out, n);
+  return hipGetLastError();
+}
 
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                        float* partial, hipStream_t stream, hipEvent_t* ev) {

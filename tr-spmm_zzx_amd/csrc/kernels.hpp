@@ -55,6 +55,8 @@ struct DevicePlan {
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                        float* partial, hipStream_t stream, hipEvent_t* ev = nullptr);
+// out[0, n) = 0 with a kernel (not a memset node: callers may capture the stream in a graph).
+hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream);
 // ev (optional): 3 events recorded before the residual kernel and after each of the two kernels.
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                         int K, float* out, hipStream_t stream, hipEvent_t* ev = nullptr);

@@ -843,6 +843,7 @@ static int spmm_impl(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t 
   if (K == 0 || p->dp.m == 0) return TRS_OK;
   if (!C || (p->dp.n > 0 && !B) || ldb < K || ldc < K)
     return report(fail(TRS_EINVAL, "trs_spmm_f16: NULL operand or leading dimension < K"));
+  if (ldb > INT32_MAX) return report(fail(TRS_ERANGE, "trs_spmm_f16: leading dimension of B beyond 2^31 - 1"));
   const int64_t need = trs_spmm_workspace_bytes(p, K);
   if (ws_bytes < need || (need > 0 && !ws))
     return report(fail(TRS_EINVAL, "trs_spmm_f16: workspace smaller than trs_spmm_workspace_bytes"));
@@ -912,13 +913,15 @@ static int sddmm_impl(const trs_plan* p, const uint16_t* X, int64_t ldx, const u
   if (!p->csr_only)
     return report(fail(TRS_EINVAL, "trs_sddmm_f16: needs a plan from trs_plan_create_sddmm or trs_plan_create_csr"));
   if (p->stats.nnz == 0) return TRS_OK;
-  if (!out || !X || !Y || (K > 0 && (ldx < K || ldy < K)))
-    return report(fail(TRS_EINVAL, "trs_sddmm_f16: NULL operand or leading dimension < K"));
-  if (K == 0) {
-    if (hipMemsetAsync(out, 0, p->stats.nnz * sizeof(float), static_cast<hipStream_t>(stream)) != hipSuccess)
-      return report(fail(TRS_EDEVICE, "hipMemsetAsync failed"));
+  if (!out) return report(fail(TRS_EINVAL, "trs_sddmm_f16: NULL output"));
+  if (K == 0) {   // empty dot products; X and Y may be empty (NULL) then
+    if (trs::launch_zero_fill(out, p->stats.nnz, static_cast<hipStream_t>(stream)) != hipSuccess)
+      return report(fail(TRS_EDEVICE, "zero-fill launch failed"));
     return TRS_OK;
   }
+  if (!X || !Y || ldx < K || ldy < K)
+    return report(fail(TRS_EINVAL, "trs_sddmm_f16: NULL operand or leading dimension < K"));
+  if (ldy > INT32_MAX) return report(fail(TRS_ERANGE, "trs_sddmm_f16: leading dimension of Y beyond 2^31 - 1"));
   const hipError_t e = trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, static_cast<hipStream_t>(stream), ev);
   if (e != hipSuccess) return report(fail(TRS_EDEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e)));
   return TRS_OK;
