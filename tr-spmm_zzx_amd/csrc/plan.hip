@@ -21,6 +21,7 @@
 #include <map>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "format.hpp"
@@ -55,6 +56,31 @@ struct Status {
 };
 
 Status fail(int code, const std::string& m) { return Status{code, m}; }
+
+// Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
+int lowering_threads() {
+  const unsigned h = std::thread::hardware_concurrency();
+  return (int)std::max(1u, std::min(h, 32u));
+}
+
+// fn(begin, end, t) on `parts` contiguous pieces of [0, n) given by cut(t) (cut(0) = 0,
+// cut(parts) = n), one thread each; serial below `serial_below` elements.
+template <class Cut, class Fn>
+void parallel_parts(int parts, int64_t n, int64_t serial_below, Cut&& cut, Fn&& fn) {
+  if (parts <= 1 || n < serial_below) {
+    fn((int64_t)0, n, 0);
+    return;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(parts);
+  for (int t = 0; t < parts; ++t) pool.emplace_back([&, t] { fn(cut(t), cut(t + 1), t); });
+  for (auto& th : pool) th.join();
+}
+template <class Fn>
+void parallel_chunks(int64_t n, Fn&& fn) {
+  const int T = lowering_threads();
+  parallel_parts(T, n, 1 << 16, [&](int t) { return n * t / T; }, fn);
+}
 
 // Host-side staging of one plan.
 struct Lowering {
@@ -160,9 +186,50 @@ void lower_residual(Lowering& L, const int32_t* off, const int32_t* rows, int64_
 }
 
 // 2:4 groups (s_column / s_value / s_pos) grouped in tiles of 4 per window as the reference packs them.
+void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
+                        const int32_t* s_win, const int32_t* s_off, int64_t w_begin, int64_t w_end, int window,
+                        bool to_mfma, float min_fill);
+
+// Windows are independent: ranges of windows (balanced by group count) are lowered in parallel
+// into private buffers and appended in window order, so the result equals the serial one.
 void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
                   const int32_t* s_win, const int32_t* s_off, int64_t nwin, int window, bool to_mfma,
                   float min_fill) {
+  if (!s_off || groups < (1 << 16)) {
+    lower_groups_range(L, s_col, s_val, s_pos, groups, s_win, s_off, 0, nwin, window, to_mfma, min_fill);
+    return;
+  }
+  for (int64_t w = 0; w < nwin; ++w)
+    if (s_off[w] < 0 || s_off[w + 1] < s_off[w] || s_off[w + 1] > groups) {
+      L.st = fail(TRS_EINVAL, "s_offsets out of range");
+      return;
+    }
+  const int T = lowering_threads();
+  std::vector<int64_t> wcut(T + 1, nwin);
+  wcut[0] = 0;
+  for (int t = 1; t < T; ++t)
+    wcut[t] = std::upper_bound(s_off, s_off + nwin + 1, (int32_t)(groups * t / T)) - s_off - 1;
+  for (int t = 1; t <= T; ++t) wcut[t] = std::max(wcut[t], wcut[t - 1]);
+  std::vector<Lowering> part(T);
+  for (auto& q : part) {
+    q.m = L.m;
+    q.n = L.n;
+  }
+  parallel_parts(T, nwin, 0, [&](int t) { return wcut[t]; }, [&](int64_t wb, int64_t we, int t) {
+    lower_groups_range(part[t], s_col, s_val, s_pos, groups, s_win, s_off, wb, we, window, to_mfma, min_fill);
+  });
+  for (auto& q : part) {
+    if (!q.st.ok() && L.st.ok()) L.st = q.st;
+    L.row.insert(L.row.end(), q.row.begin(), q.row.end());
+    L.col.insert(L.col.end(), q.col.begin(), q.col.end());
+    L.val.insert(L.val.end(), q.val.begin(), q.val.end());
+    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
+  }
+}
+
+void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
+                        const int32_t* s_win, const int32_t* s_off, int64_t w_begin, int64_t w_end, int window,
+                        bool to_mfma, float min_fill) {
   auto group_row0 = [&](int64_t g, int64_t w) { return (int64_t)(s_win ? s_win[g] : w) * window; };
   auto emit_group = [&](int64_t g, int64_t row0) {
     for (int lr = 0; lr < window; ++lr)
@@ -177,14 +244,14 @@ void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const i
   };
   if (!s_off || !to_mfma || window != 16) {
     if (s_off) {
-      for (int64_t w = 0; w < nwin && L.st.ok(); ++w)
+      for (int64_t w = w_begin; w < w_end && L.st.ok(); ++w)
         for (int64_t g = s_off[w]; g < s_off[w + 1]; ++g) emit_group(g, group_row0(g, w));
     } else {
       for (int64_t g = 0; g < groups && L.st.ok(); ++g) emit_group(g, group_row0(g, 0));
     }
     return;
   }
-  for (int64_t w = 0; w < nwin && L.st.ok(); ++w) {
+  for (int64_t w = w_begin; w < w_end && L.st.ok(); ++w) {
     for (int64_t base = s_off[w]; base < s_off[w + 1] && L.st.ok(); base += 4) {
       const int64_t end = std::min<int64_t>(base + 4, s_off[w + 1]);
       int kept = 0;
@@ -270,13 +337,24 @@ void lower_packed(Lowering& L, const int32_t* tcol, const int32_t* pa, const int
   }
 }
 
-template <class T>
-size_t push_bytes(std::vector<unsigned char>& blob, const std::vector<T>& v) {
-  size_t off = (blob.size() + 255) & ~size_t(255);
-  blob.resize(off + v.size() * sizeof(T));
-  if (!v.empty()) std::memcpy(blob.data() + off, v.data(), v.size() * sizeof(T));
-  return off;
-}
+// Layout of a plan's single device allocation: arrays at 256-byte aligned offsets, copied from
+// their host vectors by upload() (which must run while the vectors are alive).
+struct Blob {
+  struct Piece {
+    const void* src;
+    size_t off, bytes;
+  };
+  std::vector<Piece> pieces;
+  size_t total = 0;
+  template <class T>
+  size_t add(const std::vector<T>& v) {
+    const size_t off = (total + 255) & ~size_t(255);
+    pieces.push_back({v.data(), off, v.size() * sizeof(T)});
+    total = off + v.size() * sizeof(T);
+    return off;
+  }
+  size_t size() const { return std::max<size_t>(total, 256); }
+};
 
 struct Tasks {
   std::vector<trs::Task> tasks;
@@ -348,27 +426,54 @@ Tasks build_tasks(const std::vector<int32_t>& rowptr, int32_t m, int64_t nent, c
 }
 
 // Residual CSR of a lowering: row pointers and the permutation of entries into row order, each
-// row sorted by column (stable) unless keep_order.
+// row sorted by column (ties in insertion order) unless keep_order.  Stable counting sort by row
+// with per-thread histograms, then the rows sorted in parallel (pieces balanced by entries).
 void residual_csr(const Lowering& L, bool keep_order, std::vector<int32_t>& rowptr, std::vector<int64_t>& perm) {
   const int32_t m = L.m;
   const int64_t nent = (int64_t)L.row.size();
-  std::vector<int64_t> cnt(m + 1, 0);
-  for (int64_t i = 0; i < nent; ++i) cnt[L.row[i] + 1]++;
-  for (int32_t r = 0; r < m; ++r) cnt[r + 1] += cnt[r];
-  rowptr.assign(m + 1, 0);
-  for (int32_t r = 0; r <= m; ++r) rowptr[r] = (int32_t)cnt[r];
-  std::vector<int64_t> pos(cnt.begin(), cnt.end() - 1);
-  perm.assign(nent, 0);
-  for (int64_t i = 0; i < nent; ++i) perm[pos[L.row[i]]++] = i;
-  if (!keep_order)
-    for (int32_t r = 0; r < m; ++r)
-      std::stable_sort(perm.begin() + rowptr[r], perm.begin() + rowptr[r + 1],
-                       [&](int64_t x, int64_t y) { return L.col[x] < L.col[y]; });
+  const int T = nent >= (1 << 20) ? lowering_threads() : 1;
+  auto cut = [&](int t) { return nent * t / T; };
+  std::vector<std::vector<int32_t>> cnt(T, std::vector<int32_t>((size_t)m, 0));
+  parallel_parts(T, nent, 0, cut, [&](int64_t b, int64_t e, int t) {
+    int32_t* c = cnt[t].data();
+    for (int64_t i = b; i < e; ++i) c[L.row[i]]++;
+  });
+  // rows in order; inside a row, thread pieces in order: entries keep their insertion order
+  rowptr.assign((size_t)m + 1, 0);
+  int64_t acc = 0;
+  for (int32_t r = 0; r < m; ++r) {
+    rowptr[r] = (int32_t)acc;
+    for (int t = 0; t < T; ++t) {
+      const int32_t c = cnt[t][r];
+      cnt[t][r] = (int32_t)acc;
+      acc += c;
+    }
+  }
+  rowptr[m] = (int32_t)acc;
+  perm.resize((size_t)nent);
+  parallel_parts(T, nent, 0, cut, [&](int64_t b, int64_t e, int t) {
+    int32_t* c = cnt[t].data();
+    for (int64_t i = b; i < e; ++i) perm[(size_t)c[L.row[i]]++] = i;
+  });
+  std::vector<std::vector<int32_t>>().swap(cnt);
+  if (keep_order) return;
+  // rows split into pieces of about nent / T entries
+  std::vector<int32_t> row_cut(T + 1, m);
+  row_cut[0] = 0;
+  for (int t = 1; t < T; ++t)
+    row_cut[t] = (int32_t)(std::upper_bound(rowptr.begin(), rowptr.end(), (int32_t)(nent * t / T)) - rowptr.begin() - 1);
+  for (int t = 1; t <= T; ++t) row_cut[t] = std::max(row_cut[t], row_cut[t - 1]);
+  parallel_parts(T, (int64_t)m, 0, [&](int t) { return (int64_t)row_cut[t]; }, [&](int64_t rb, int64_t re, int) {
+    for (int64_t r = rb; r < re; ++r) {
+      auto b = perm.begin() + rowptr[r], e = perm.begin() + rowptr[r + 1];
+      auto less = [&](int64_t x, int64_t y) { return L.col[x] != L.col[y] ? L.col[x] < L.col[y] : x < y; };
+      if (!std::is_sorted(b, e, less)) std::sort(b, e, less);
+    }
+  });
 }
 
-// One hipMalloc holding the whole plan, filled by one copy.
-Status upload(std::vector<unsigned char>& blob, trs_plan*& P) {
-  blob.resize(std::max<size_t>(blob.size(), 256));
+// One hipMalloc holding the whole plan, filled array by array.
+Status upload(const Blob& blob, trs_plan*& P) {
   P = new trs_plan();
   if (hipGetDevice(&P->device) != hipSuccess) {
     delete P;
@@ -383,10 +488,14 @@ Status upload(std::vector<unsigned char>& blob, trs_plan*& P) {
     return fail(TRS_ENOMEM, "hipMalloc of " + std::to_string(blob.size()) + " plan bytes failed");
   }
   P->dbytes = blob.size();
-  if (hipMemcpy(P->dmem, blob.data(), blob.size(), hipMemcpyHostToDevice) != hipSuccess) {
-    delete P;
-    P = nullptr;
-    return fail(TRS_EDEVICE, "plan upload failed");
+  for (const auto& pc : blob.pieces) {
+    if (pc.bytes == 0) continue;
+    if (hipMemcpy(static_cast<unsigned char*>(P->dmem) + pc.off, pc.src, pc.bytes, hipMemcpyHostToDevice) !=
+        hipSuccess) {
+      delete P;
+      P = nullptr;
+      return fail(TRS_EDEVICE, "plan upload failed");
+    }
   }
   return Status{};
 }
@@ -395,57 +504,61 @@ Status upload(std::vector<unsigned char>& blob, trs_plan*& P) {
 Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   if (!L.st.ok()) return L.st;
   const int32_t m = L.m;
-  const int64_t nent = (int64_t)L.row.size();
-  if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
 
-  // MFMA windows: 16-row blocks owning at least one tile.
-  std::sort(L.tiles.begin(), L.tiles.end(), [](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; });
+  // MFMA windows: 16-row blocks owning at least one tile (tile order inside a window kept).
+  std::stable_sort(L.tiles.begin(), L.tiles.end(),
+                   [](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; });
   const int32_t nblocks = (m + 15) / 16;
   std::vector<uint8_t> owned(nblocks, 0);
   for (const auto& t : L.tiles) owned[t.row0 / 16] = 1;
 
-  // residual CSR sorted by (row, column); stable so equal keys keep insertion order
+  // Hand a tile-owning block back to the residual path when one of its residual rows is long:
+  // the window kernel walks each residual row with one lane group, so a long row would keep the
+  // whole workgroup waiting (hub windows of power-law graphs).  Decided on the residual row
+  // lengths before the demoted tiles' entries join the residual.
+  const int row_cap = opt.window_row_cap > 0 ? opt.window_row_cap : 128;
+  if (!L.tiles.empty()) {
+    std::vector<int32_t> len((size_t)m, 0);
+    for (int32_t r : L.row) len[r]++;
+    std::vector<uint8_t> demote(nblocks, 0);
+    bool any_demote = false;
+    for (int32_t b = 0; b < nblocks; ++b) {
+      if (!owned[b]) continue;
+      for (int32_t r = b * 16; r < std::min(m, b * 16 + 16); ++r)
+        if (len[r] > row_cap) demote[b] = 1;
+      any_demote |= demote[b] != 0;
+    }
+    if (any_demote) {
+      std::vector<Lowering::Tile> kept;
+      for (const auto& t : L.tiles) {
+        if (!demote[t.row0 / 16]) { kept.push_back(t); continue; }
+        owned[t.row0 / 16] = 0;
+        for (int r = 0; r < 16; ++r)
+          for (int k = 0; k < 16; ++k)
+            if (t.cols[k] >= 0 && Lowering::tile_has(t, r, k)) L.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
+      }
+      L.tiles.swap(kept);
+      if (!L.st.ok()) return L.st;
+    }
+  }
+  const int64_t nent = (int64_t)L.row.size();
+  if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
+
+  // residual CSR sorted by (row, column); equal keys keep insertion order
   std::vector<int32_t> rowptr;
   std::vector<int32_t> col(nent);
   std::vector<uint16_t> val(nent);
   {
     std::vector<int64_t> perm;
     residual_csr(L, false, rowptr, perm);
-    for (int64_t i = 0; i < nent; ++i) {
-      col[i] = L.col[perm[i]];
-      val[i] = trs::half_bits(L.val[perm[i]]);
-    }
-  }
-
-  // Hand a tile-owning block back to the residual path when one of its residual rows is long:
-  // the window kernel walks each residual row with one lane group, so a long row would keep the
-  // whole workgroup waiting (hub windows of power-law graphs).
-  const int row_cap = opt.window_row_cap > 0 ? opt.window_row_cap : 128;
-  std::vector<Lowering::Tile> kept_tiles;
-  std::vector<trs::MfmaWindow> mwin;
-  {
-    std::vector<uint8_t> demote(nblocks, 0);
-    for (int32_t b = 0; b < nblocks; ++b) {
-      if (!owned[b]) continue;
-      for (int32_t r = b * 16; r < std::min(m, b * 16 + 16); ++r)
-        if (rowptr[r + 1] - rowptr[r] > row_cap) demote[b] = 1;
-    }
-    bool any_demote = false;
-    for (int32_t b = 0; b < nblocks; ++b) any_demote |= demote[b] != 0;
-    if (any_demote) {
-      // re-lower demoted tiles as entries and rebuild the residual CSR
-      Lowering L2;
-      L2.m = L.m; L2.n = L.n;
-      L2.row = L.row; L2.col = L.col; L2.val = L.val;
-      for (const auto& t : L.tiles) {
-        if (!demote[t.row0 / 16]) { L2.tiles.push_back(t); continue; }
-        for (int r = 0; r < 16; ++r)
-          for (int k = 0; k < 16; ++k)
-            if (t.cols[k] >= 0 && Lowering::tile_has(t, r, k)) L2.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
+    parallel_chunks(nent, [&](int64_t b, int64_t e, int) {
+      for (int64_t i = b; i < e; ++i) {
+        col[i] = L.col[perm[i]];
+        val[i] = trs::half_bits(L.val[perm[i]]);
       }
-      return finalize(L2, opt, out);
-    }
+    });
   }
+  std::vector<trs::MfmaWindow> mwin;
   for (size_t i = 0; i < L.tiles.size();) {
     size_t j = i;
     while (j < L.tiles.size() && L.tiles[j].row0 == L.tiles[i].row0) ++j;
@@ -471,16 +584,16 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   const int64_t split_rows = T.split_rows;
 
   // one device allocation
-  std::vector<unsigned char> blob;
-  const size_t o_rowptr = push_bytes(blob, rowptr);
-  const size_t o_col = push_bytes(blob, col);
-  const size_t o_val = push_bytes(blob, val);
-  const size_t o_tasks = push_bytes(blob, tasks);
-  const size_t o_fix = push_bytes(blob, fix);
-  const size_t o_wfix = push_bytes(blob, wfix);
-  const size_t o_mwin = push_bytes(blob, mwin);
-  const size_t o_tcol = push_bytes(blob, tile_cols);
-  const size_t o_ta = push_bytes(blob, tile_a);
+  Blob blob;
+  const size_t o_rowptr = blob.add(rowptr);
+  const size_t o_col = blob.add(col);
+  const size_t o_val = blob.add(val);
+  const size_t o_tasks = blob.add(tasks);
+  const size_t o_fix = blob.add(fix);
+  const size_t o_wfix = blob.add(wfix);
+  const size_t o_mwin = blob.add(mwin);
+  const size_t o_tcol = blob.add(tile_cols);
+  const size_t o_ta = blob.add(tile_a);
   trs_plan* P = nullptr;
   {
     const Status us = upload(blob, P);
@@ -559,7 +672,9 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   std::vector<int64_t> perm;
   residual_csr(L, keep_order && L.tiles.empty(), rowptr, perm);
   std::vector<int32_t> col(nent);
-  for (int64_t i = 0; i < nent; ++i) col[i] = L.col[perm[i]];
+  parallel_chunks(nent, [&](int64_t b, int64_t e, int) {
+    for (int64_t i = b; i < e; ++i) col[i] = L.col[perm[i]];
+  });
 
   // tile entries in (row, column) order, merged with the residual rows
   struct TE { int32_t row, col, slot; };   // slot = tile * 256 + r * 16 + k
@@ -593,14 +708,14 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   Tasks T = build_tasks(rowptr, m, nent, {}, false, opt);
   if (!T.st.ok()) return T.st;
 
-  std::vector<unsigned char> blob;
-  const size_t o_rowptr = push_bytes(blob, rowptr);
-  const size_t o_col = push_bytes(blob, col);
-  const size_t o_tasks = push_bytes(blob, T.tasks);
-  const size_t o_rpos = push_bytes(blob, res_pos);
-  const size_t o_trow = push_bytes(blob, tile_row0);
-  const size_t o_tcol = push_bytes(blob, tile_cols);
-  const size_t o_tpos = push_bytes(blob, tile_pos);
+  Blob blob;
+  const size_t o_rowptr = blob.add(rowptr);
+  const size_t o_col = blob.add(col);
+  const size_t o_tasks = blob.add(T.tasks);
+  const size_t o_rpos = blob.add(res_pos);
+  const size_t o_trow = blob.add(tile_row0);
+  const size_t o_tcol = blob.add(tile_cols);
+  const size_t o_tpos = blob.add(tile_pos);
   trs_plan* P = nullptr;
   {
     const Status us = upload(blob, P);
