@@ -86,6 +86,37 @@ def kernel_ms(plan, B, C, ws, need, iters=10):
     return list(ms)
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cold_ms(run, steps: int, flush_mib: int = 1024) -> float:
+    """Median time of one step with L2 and MALL flushed first: a write of flush_mib MiB before
+    every step, timed on the step alone with events around it."""
+    import numpy as np
+    import torch
+    scratch = torch.empty(flush_mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    ts = []
+    for _ in range(steps):
+        scratch.fill_(1.0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run()
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    del scratch
+    return float(np.median(ts))
+
+
 def cpu_baseline(g, Bh, flops):
     """torch.sparse.mm CSR fp32 on all host cores: 1 warm-up + median of up to 5 runs, bounded to
     about 20 s of CPU time (fewer runs on a slow host)."""
@@ -107,7 +138,7 @@ def cpu_baseline(g, Bh, flops):
     t = float(np.median(ts))
     return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
             "sample": f"full workload, torch.sparse.mm CSR fp32, median of {runs} after 1 warm-up "
-                      f"({t * 1e3:.1f} ms/run)"}
+                      f"({t * 1e3:.1f} ms/run) on {cpu_model()}"}
 
 
 def cpu_baseline_sddmm(g, Xh, Yh, flops):
@@ -133,7 +164,7 @@ def cpu_baseline_sddmm(g, Xh, Yh, flops):
     t = float(np.median(ts))
     return {"value": round(flops / t / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
             "sample": f"full workload, torch.sparse.sampled_addmm CSR fp32, median of {runs} after 1 warm-up "
-                      f"({t * 1e3:.1f} ms/run)"}
+                      f"({t * 1e3:.1f} ms/run) on {cpu_model()}"}
 
 
 def bench_sddmm(args, workload, g, K):
@@ -171,6 +202,7 @@ def bench_sddmm(args, workload, g, K):
                                                 out.data_ptr(), int(torch.cuda.current_stream().cuda_stream), 10, ms),
               "trs_sddmm_f16_kernel_ms")
     kms = list(ms)
+    ms_cold = cold_ms(lambda: plan.sddmm(X, Y, out=out), max(5, min(args.steps, 10)))
     names = ["sddmm_tasks", "sddmm_mfma"]
     dom = int(np.argmax(kms))
     M, N = g.m, g.n
@@ -192,7 +224,9 @@ def bench_sddmm(args, workload, g, K):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
             "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K, "mfma_tiles": st["mfma_tiles"],
                        "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
-            "roofline": roof}
+            "roofline": roof,
+            "cold": {"ms_per_step": round(ms_cold, 5), "value": round(flops / (ms_cold * 1e-3) / 1e9, 2),
+                     "note": "median step with a 1 GiB write before each (L2 and MALL flushed)"}}
     if not args.no_cpu_baseline:
         outj["cpu_baseline"] = cpu_baseline_sddmm(g, Xh, Yh, flops)
     print(json.dumps(outj), flush=True)
@@ -316,6 +350,8 @@ def main():
             "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     log(f"[bench] kernels {kms}, roofline {roof}")
+    ms_cold = cold_ms(lambda: plan.spmm(B, out=C, workspace=ws), max(5, min(args.steps, 10)))
+    log(f"[bench] cold (L2 + MALL flushed) {ms_cold:.4f} ms/step")
 
     metric = METRIC if args.config == 2 and K == 128 else OTHER_METRIC.format(workload=workload)
     out = {"metric": metric, "value": round(gflops, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -323,7 +359,9 @@ def main():
            "vs_baseline": None, "dtype": "f16", "data": "synthetic",
            "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K,
                       "mfma_tiles": st["mfma_tiles"], "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
-           "roofline": roof, "preprocess": pre}
+           "roofline": roof, "preprocess": pre,
+           "cold": {"ms_per_step": round(ms_cold, 5), "value": round(flops / (ms_cold * 1e-3) / 1e9, 2),
+                    "note": "median step with a 1 GiB write before each (L2 and MALL flushed)"}}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(g, Bh, flops)
         log(f"[bench] cpu baseline {out['cpu_baseline']}")
