@@ -93,3 +93,15 @@ def test_sddmm_zero_width_writes_zeros():
     plan.sddmm(X, Y, out=out)
     torch.cuda.synchronize()
     assert torch.count_nonzero(out).item() == 0
+
+
+def test_sddmm_nonfinite_Y_reaches_only_entries_that_use_it():
+    g = graphs.rmat(scale=11, edge_factor=8, seed=6)
+    plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)   # CSR dots only
+    K = 64
+    Xh = graphs.dense_operand(g.m, K, seed=1)
+    Yh = graphs.dense_operand(g.n, K, seed=2)
+    hub = int(np.argmax(np.bincount(g.col, minlength=g.n)))
+    Yh[hub, 5] = np.float16(np.nan)
+    out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()).cpu().numpy()
+    assert np.array_equal(~np.isfinite(out), g.col[: g.nnz] == hub)

@@ -207,3 +207,33 @@ def test_leading_dimension_beyond_int32_is_refused():
                                 int(torch.cuda.current_stream().cuda_stream))
     assert rc == 5, nat.lib().trs_last_error()          # TRS_ERANGE, nothing launched
     assert "2^31" in nat.lib().trs_last_error().decode()
+
+
+@pytest.mark.parametrize("K", [8, 24, 32, 128, 200])
+def test_nonfinite_B_reaches_only_rows_that_use_it(K):
+    """Padded batch slots re-read a real B row and lanes past K read real features (branch-free
+    loads): a NaN / Inf in B must show up exactly in the outputs whose rows reference that B row
+    (and only in its own feature column), never elsewhere.  Residual path only: a dense MFMA tile
+    multiplies its absent entries as zeros, so 0 x Inf spreads a non-finite B row over the tile's
+    window, as the reference's dense TC blocks do."""
+    say("nonfinite", K)
+    g = graphs.rmat(scale=11, edge_factor=8, seed=5)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    for task_nnz in (32, 128):
+        plan = trspmm.Plan.from_format(f, g.m, g.n, mfma_tc=False, mfma_sptc=False, task_nnz=task_nnz)
+        Bh = dense_B(g.n, K, seed=4)
+        hub = int(np.argmax(np.bincount(g.col, minlength=g.n)))    # most referenced B row
+        lone = int(np.argmin(np.where(np.bincount(g.col, minlength=g.n) > 0,
+                                      np.bincount(g.col, minlength=g.n), 1 << 30)))
+        Bh[hub, K - 1] = np.float16(np.nan)
+        Bh[lone, 0] = np.float16(np.inf)
+        C = run_plan(plan, Bh)
+        rows = np.repeat(np.arange(g.m_pad), np.diff(g.rowptr))[: g.nnz]
+        uses_hub = np.zeros(g.m, bool)
+        uses_hub[rows[(g.col == hub) & (rows < g.m)]] = True
+        uses_lone = np.zeros(g.m, bool)
+        uses_lone[rows[(g.col == lone) & (rows < g.m)]] = True
+        bad = ~np.isfinite(C)
+        assert np.array_equal(bad[:, K - 1], uses_hub), "NaN column"
+        assert np.array_equal(bad[:, 0], uses_lone), "Inf column"
+        assert not bad[:, 1:K - 1].any(), "non-finite values leaked into other features"

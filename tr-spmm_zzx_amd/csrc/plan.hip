@@ -195,15 +195,16 @@ void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, c
 void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
                   const int32_t* s_win, const int32_t* s_off, int64_t nwin, int window, bool to_mfma,
                   float min_fill) {
+  if (s_off)
+    for (int64_t w = 0; w < nwin; ++w)
+      if (s_off[w] < 0 || s_off[w + 1] < s_off[w] || s_off[w + 1] > groups) {
+        L.st = fail(TRS_EINVAL, "s_offsets out of range");
+        return;
+      }
   if (!s_off || groups < (1 << 16)) {
     lower_groups_range(L, s_col, s_val, s_pos, groups, s_win, s_off, 0, nwin, window, to_mfma, min_fill);
     return;
   }
-  for (int64_t w = 0; w < nwin; ++w)
-    if (s_off[w] < 0 || s_off[w + 1] < s_off[w] || s_off[w + 1] > groups) {
-      L.st = fail(TRS_EINVAL, "s_offsets out of range");
-      return;
-    }
   const int T = lowering_threads();
   std::vector<int64_t> wcut(T + 1, nwin);
   wcut[0] = 0;
