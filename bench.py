@@ -2,6 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config 2|3|5|4] [--no-cpu-baseline]
                     [--scramble SEED] [--reorder tca]
+    python bench.py --ceiling-probe      # practical copy / random-gather rates of the box
 
 A step is one SpMM C = A B over the whole graph with A (device plan) and B already resident in
 HBM.  Prints one JSON line with GFLOP/s (2 nnz K / t), the roofline object of the dominant kernel
@@ -232,6 +233,54 @@ def bench_sddmm(args, workload, g, K):
     print(json.dumps(outj), flush=True)
 
 
+def ceiling_probe():
+    """Reference points for the roofline fractions: a 2 GiB device copy, and uniform-random row
+    gathers through the residual SpMM kernel (1M rows x d random columns, no column reuse) for
+    several operand sizes and row widths.  One JSON line per probe."""
+    import numpy as np
+    import torch
+    import trspmm
+    from trspmm import graphs
+
+    def timeit(fn, n=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    src = torch.ones(512 << 20, dtype=torch.float32, device="cuda")   # 2 GiB
+    dst = torch.empty_like(src)
+    ms = timeit(lambda: dst.copy_(src))
+    print(json.dumps({"probe": "device copy 2 GiB fp32", "ms": round(ms, 4),
+                      "TB/s read+write": round(4 * 2**30 / ms / 1e9, 3)}), flush=True)
+    del src, dst
+    rng = np.random.default_rng(0)
+    m = 1 << 20
+    for n, K, d in [(8 << 20, 128, 32), (2 << 20, 128, 32), (1 << 20, 128, 32), (8 << 20, 64, 32),
+                    (1 << 20, 64, 32), (8 << 20, 32, 32), (1 << 20, 32, 32), (4 << 20, 32, 32)]:
+        keys = np.unique(rng.integers(0, m * n, size=m * d, dtype=np.int64))
+        rowptr, col = graphs.csr_from_keys(keys, m, n, m)
+        g = graphs.Graph("probe", m, n, rowptr, col, np.ones(len(keys), np.float32))
+        f = trspmm.build_format(g.rowptr, g.col, g.val, skip_tc=True)
+        plan = trspmm.Plan.from_format(f, m, n, mfma_tc=False, mfma_sptc=False)
+        B = torch.ones(n, K, dtype=torch.float16, device="cuda")
+        C = torch.empty(m, K, device="cuda")
+        ms = timeit(lambda: plan.spmm(B, out=C))
+        gathered = len(keys) * K * 2
+        print(json.dumps({"probe": f"random row gather: B {n >> 20}M x {K} fp16 ({n * K * 2 / 1e6:.0f} MB), "
+                                   f"{len(keys) / m:.1f} random columns per row", "ms": round(ms, 4),
+                          "gathered TB/s": round(gathered / ms / 1e9, 3),
+                          "C write TB/s": round(m * K * 4 / ms / 1e9, 3)}), flush=True)
+        del plan, B, C, f
+
+
 def load_traffic(workload: str):
     path = os.path.join(ROOT, "profiles", f"spmm_tasks_{workload}_pmc.json")
     if not os.path.exists(path):
@@ -253,6 +302,8 @@ def main():
                     help="relabel the graph's nodes with a random permutation first")
     ap.add_argument("--reorder", choices=["none", "tca"], default="none",
                     help="TCA row reorder before the builder (timed, reported under 'preprocess')")
+    ap.add_argument("--ceiling-probe", action="store_true",
+                    help="print the box's copy and random-gather rates (one JSON line each) and exit")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -268,6 +319,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.ceiling_probe:
+        ceiling_probe()
+        return
     t0 = time.time()
     workload, g, K, bseed = make_workload(args.config)
     if args.k:
