@@ -410,11 +410,12 @@ __global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, fl
 //   A: A[l % 16][4 * (l / 16) + j]      B: B[4 * (l / 16) + j][l % 16]
 //   D: D[4 * (l / 16) + j][l % 16]
 // Here A = the 16x16 tile (window row x tile column), B = gathered B rows (tile column x feature).
-template <int VEC, int NTILE>
 // Occupancy floor for KC <= 128: the register budget of 6 waves per SIMD (measured: 5 waves cost
 // 6% on SBM K=128).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTILE >= 4 ? 1 : 6))) void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
-                                                       int K, float* __restrict__ C, int64_t ldc, int KC) {
+template <int VEC, int NTILE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTILE >= 4 ? 1 : 6)))
+void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, int K, float* __restrict__ C,
+                     int64_t ldc, int KC) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int KCP = KC + 4;   // fp32 output tile row stride
   const int KCB = KC + 8;   // fp16 staged-B row stride (keeps 16-byte alignment)
@@ -433,15 +434,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTILE >= 4 
 
   for (int t = w.tile_begin; t < w.tile_end; ++t) {
     __syncthreads();
-    // stage the 16 gathered B rows (features [fbase, fbase + KC)) into LDS
+    // stage the 16 gathered B rows (features [fbase, fbase + KC)) into LDS; loads unconditional
+    // (empty column slots read row 0, features past K read the row's last VEC) and then zeroed
     const int per_row = KC / VEC;
     for (int idx = threadIdx.x; idx < 16 * per_row; idx += 256) {
       const int k = idx / per_row;
       const int ff = (idx % per_row) * VEC;
       const int c = P.tile_cols[t * 16 + k];
+      const bool in = c >= 0 && fbase + ff < K;
       BFrag<VEC> b;
-      if (c >= 0 && fbase + ff < K) b.load(B + row_offset(c, ldb) + fbase + ff);
-      else b.zero();
+      b.load(B + row_offset(c >= 0 ? c : 0, ldb) + (fbase + ff < K ? fbase + ff : K - VEC));
+      if (!in) b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
       else bst[k * KCB + ff] = b.v;
     }
