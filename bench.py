@@ -118,6 +118,28 @@ def cold_ms(run, steps: int, flush_mib: int = 1024) -> float:
     return float(np.median(ts))
 
 
+def pcie_inclusive_ms(plan, Bh, C, ws, steps: int = 5) -> float:
+    """Median time of host-to-host SpMM as the drop-in operators see it: B copied from pinned host
+    memory, the SpMM, C copied back to pinned host memory (plan already resident)."""
+    import numpy as np
+    import torch
+    Bp = torch.from_numpy(Bh).pin_memory()
+    Cp = torch.empty(C.shape, dtype=C.dtype).pin_memory()
+    Bd = torch.empty(Bp.shape, dtype=Bp.dtype, device="cuda")
+    ts = []
+    for _ in range(steps + 1):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        Bd.copy_(Bp, non_blocking=True)
+        plan.spmm(Bd, out=C, workspace=ws)
+        Cp.copy_(C, non_blocking=True)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return float(np.median(ts[1:]))
+
+
 def cpu_baseline(g, Bh, flops):
     """torch.sparse.mm CSR fp32 on all host cores: 1 warm-up + median of up to 5 runs, bounded to
     about 20 s of CPU time (fewer runs on a slow host)."""
@@ -406,6 +428,8 @@ def main():
     log(f"[bench] kernels {kms}, roofline {roof}")
     ms_cold = cold_ms(lambda: plan.spmm(B, out=C, workspace=ws), max(5, min(args.steps, 10)))
     log(f"[bench] cold (L2 + MALL flushed) {ms_cold:.4f} ms/step")
+    ms_pcie = pcie_inclusive_ms(plan, Bh, C, ws)
+    log(f"[bench] host-to-host (B in, C out over PCIe) {ms_pcie:.3f} ms/step")
 
     metric = METRIC if args.config == 2 and K == 128 else OTHER_METRIC.format(workload=workload)
     out = {"metric": metric, "value": round(gflops, 2), "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -415,7 +439,9 @@ def main():
                       "mfma_tiles": st["mfma_tiles"], "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
            "roofline": roof, "preprocess": pre,
            "cold": {"ms_per_step": round(ms_cold, 5), "value": round(flops / (ms_cold * 1e-3) / 1e9, 2),
-                    "note": "median step with a 1 GiB write before each (L2 and MALL flushed)"}}
+                    "note": "median step with a 1 GiB write before each (L2 and MALL flushed)"},
+           "host_to_host": {"ms_per_step": round(ms_pcie, 4), "value": round(flops / (ms_pcie * 1e-3) / 1e9, 2),
+                            "note": "B from pinned host memory, SpMM, C to pinned host memory (not `value`)"}}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(g, Bh, flops)
         log(f"[bench] cpu baseline {out['cpu_baseline']}")
