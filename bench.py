@@ -64,12 +64,12 @@ def scramble(g, seed: int):
     return graphs.Graph(g.name + "_scrambled", g.m, g.n, rowptr, col[o].astype(np.int32), val[o])
 
 
-def tca_reorder(g):
-    """Row reorder of the reference's optional TCA step (LIBRA_TCA_REORDER=1); returns the
-    reordered graph and the seconds it took."""
+def tca_reorder(g, align_window: int = 0):
+    """Row reorder of the reference's optional TCA step (LIBRA_TCA_REORDER=1), or its
+    window-aligned variant; returns the reordered graph and the seconds it took."""
     from trspmm import graphs, reorder
     t0 = time.time()
-    order = reorder.tca_order(g.rowptr[: g.m + 1], g.col, ncols=g.n)
+    order = reorder.tca_order(g.rowptr[: g.m + 1], g.col, ncols=g.n, align_window=align_window)
     rp, col, val = reorder.permute_rows(g.rowptr[: g.m + 1], g.col, order, g.val)
     import numpy as np
     rowptr = np.concatenate([rp, np.full(g.m_pad - g.m, rp[-1], dtype=np.int32)])
@@ -322,8 +322,9 @@ def main():
     ap.add_argument("--k", type=int, default=0, help="override the configuration's feature width")
     ap.add_argument("--scramble", type=int, default=None, metavar="SEED",
                     help="relabel the graph's nodes with a random permutation first")
-    ap.add_argument("--reorder", choices=["none", "tca"], default="none",
-                    help="TCA row reorder before the builder (timed, reported under 'preprocess')")
+    ap.add_argument("--reorder", choices=["none", "tca", "tca-aligned"], default="none",
+                    help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
+                         "tca-aligned keeps clusters inside 16-row windows")
     ap.add_argument("--ceiling-probe", action="store_true",
                     help="print the box's copy and random-gather rates (one JSON line each) and exit")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -354,9 +355,9 @@ def main():
     if args.scramble is not None:
         g = scramble(g, args.scramble)
         workload += "_scrambled"
-    if args.reorder == "tca":
-        g, pre["reorder_s"] = tca_reorder(g)
-        workload += "_tca"
+    if args.reorder != "none":
+        g, pre["reorder_s"] = tca_reorder(g, 16 if args.reorder == "tca-aligned" else 0)
+        workload += "_" + args.reorder.replace("-", "_")
         log(f"[bench] TCA reorder {pre['reorder_s']:.2f}s")
     if args.config == 4:
         bench_sddmm(args, workload, g, K)

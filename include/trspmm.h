@@ -99,7 +99,10 @@ typedef struct trs_reorder_params {
                              next bucket_span members only (64) */
   int32_t num_threads;    /* host threads; 0 = OpenMP default */
   int32_t exhaustive;     /* 1: every pair of non-empty sets is a candidate (small inputs, tests) */
-  int32_t reserved;
+  int32_t align_window;   /* 0: the reference's layout.  W > 0 (no reference counterpart): level-1
+                             clusters never exceed W rows (thres is ignored) and are packed
+                             first-fit decreasing into whole W-row windows per level-2 group, so
+                             clusters do not straddle windows */
   uint64_t seed;          /* MinHash permutation seed (2022) */
 } trs_reorder_params;
 

@@ -28,8 +28,10 @@ def jaccard(a: frozenset, b: frozenset) -> float:
     return inter / union if union else 0.0
 
 
-def cluster(sets: list, thres: int) -> list:
-    """Root of every set after the greedy union-find clustering (exhaustive candidates)."""
+def cluster(sets: list, thres: int, capped: bool = False) -> list:
+    """Root of every set after the greedy union-find clustering (exhaustive candidates).
+    capped (the library's window-aligned extension, no reference counterpart): merges that would
+    exceed `thres` members are skipped."""
     n = len(sets)
     key = lambda a, b: (min(a, b) * n + max(a, b))   # noqa: E731
     heap, queued = [], set()
@@ -58,6 +60,8 @@ def cluster(sets: list, thres: int) -> list:
         if p1 == cid[p1] and p2 == cid[p2]:
             if closed[p1] or closed[p2]:
                 continue
+            if capped and size[p1] + size[p2] > thres:
+                continue
             into, frm = (p2, p1) if size[p1] < size[p2] else (p1, p2)
             cid[frm] = into
             open_clusters -= 1
@@ -85,11 +89,47 @@ def groups(roots: list) -> list:
     return out
 
 
-def tca_order(rowptr, col, thres: int = 16, cluster_thres: int = 128) -> list:
+def aligned_order(clusters: list, supers: list, W: int) -> list:
+    """Window-aligned layout (extension): per level-2 group, first-fit-decreasing packing of its
+    clusters into W-row bins; full bins in group order, the clusters of partial bins packed again
+    at the end with full bins first."""
+    def pack(ids):
+        bins, fill = [], []
+        for c in sorted(ids, key=lambda c: -len(clusters[c])):   # sorted() is stable
+            for b in range(len(bins)):
+                if fill[b] + len(clusters[c]) <= W:
+                    bins[b].append(c)
+                    fill[b] += len(clusters[c])
+                    break
+            else:
+                bins.append([c])
+                fill.append(len(clusters[c]))
+        return bins, fill
+
+    order, leftover = [], []
+    for grp in supers:
+        bins, fill = pack(grp)
+        for b, f in zip(bins, fill):
+            if f == W:
+                order += [r for c in b for r in clusters[c]]
+            else:
+                leftover += b
+    bins, fill = pack(leftover)
+    order += [r for b, f in zip(bins, fill) if f == W for c in b for r in clusters[c]]
+    order += [r for b, f in zip(bins, fill) if f != W for c in b for r in clusters[c]]
+    return order
+
+
+def tca_order(rowptr, col, thres: int = 16, cluster_thres: int = 128, align_window: int = 0) -> list:
     """order[new_row] = old_row, both levels, exhaustive candidates."""
     rows = len(rowptr) - 1
     sets = [frozenset(int(c) for c in col[rowptr[i]:rowptr[i + 1]]) for i in range(rows)]
-    clusters = groups(cluster(sets, thres))
+    if align_window > 0:
+        clusters = groups(cluster(sets, align_window, capped=True))
+    else:
+        clusters = groups(cluster(sets, thres))
     csets = [frozenset().union(*(sets[r] for r in cl)) for cl in clusters]
     supers = groups(cluster(csets, cluster_thres))
+    if align_window > 0:
+        return aligned_order(clusters, supers, align_window)
     return [r for grp in supers for c in grp for r in clusters[c]]

@@ -123,3 +123,37 @@ def test_reorder_errors():
     with pytest.raises(nat.TrsError):
         reorder.tca_order(rp, col, thres=0)
     assert reorder.tca_order(np.zeros(1, np.int32), np.zeros(0, np.int32)).shape == (0,)
+
+
+# ---- window-aligned extension (no reference counterpart) ----
+
+def test_oracle_aligned_hand_case():
+    # thres 4: sim-1 pairs {0,2} and {1,3} merge; {0,2} + {4} would make 3 <= 4 -> merges; the
+    # size-3 and size-2 clusters pack into bins of 4 as [3] and [2] (3 + 2 > 4)
+    rp, col = csr([{5}, {1, 2}, {5}, {1, 2}, {5, 9}])
+    clusters = otca.groups(otca.cluster([frozenset(s) for s in ({5}, {1, 2}, {5}, {1, 2}, {5, 9})], 4, capped=True))
+    assert clusters == [[0, 2, 4], [1, 3]]
+    assert otca.tca_order(rp, col, align_window=4) == [0, 2, 4, 1, 3]
+
+
+@pytest.mark.parametrize("seed,rows,W,cthres", [(1, 60, 16, 128), (2, 90, 4, 3), (3, 120, 8, 2), (6, 77, 5, 4)])
+def test_native_aligned_matches_oracle_exhaustive(seed, rows, W, cthres):
+    rp, col = random_clustered(rows, seed)
+    got = reorder.tca_order(rp, col, ncols=420, cluster_thres=cthres, exhaustive=True, align_window=W)
+    want = otca.tca_order(rp, col, cluster_thres=cthres, align_window=W)
+    assert got.tolist() == want
+
+
+def test_aligned_windows_recover_communities():
+    rp, col, perm = scrambled_sbm(600, 4)
+    m = rp.shape[0] - 1
+    plain = reorder.tca_order(rp, col)
+    aligned = reorder.tca_order(rp, col, align_window=16)
+    assert np.array_equal(np.sort(aligned), np.arange(m))
+    def purity(order):
+        comm = (perm[order] // 16).reshape(-1, 16)
+        return np.mean([np.bincount(w).max() / 16 for w in comm])
+    assert purity(aligned) > purity(plain) and purity(aligned) > 0.85, (purity(aligned), purity(plain))
+    val = np.ones(col.shape[0], np.float32)
+    tc = lambda o: trspmm.build_format(*reorder.permute_rows(rp, col, o, val)).slot(3).size
+    assert tc(aligned) > tc(plain)

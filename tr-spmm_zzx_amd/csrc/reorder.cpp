@@ -20,6 +20,9 @@
 //     `bucket_span` sets of the bucket only (the reference pairs all, O(bucket^2));
 //   * equal similarities pop in (pair key) order; the reference's queue order for ties depends on
 //     Python's per-process string hashing.
+// Extension (align_window = W > 0, no reference counterpart): level-1 merges that would exceed W
+// rows are skipped, and the clusters are packed into whole W-row windows (aligned_order), so a
+// cluster never straddles two windows.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -212,8 +215,9 @@ std::vector<std::pair<int32_t, int32_t>> candidates(const Sets& S, const trs_reo
 }
 
 // Greedy union-find clustering of the sets (tr_tca_reorder.py:145-210 / :282-323); returns the
-// root of every set.
-std::vector<int32_t> cluster(const Sets& S, int32_t thres, const trs_reorder_params& prm) {
+// root of every set.  capped: a merge that would exceed `thres` members is skipped (window-aligned
+// mode) instead of performed and closed.
+std::vector<int32_t> cluster(const Sets& S, int32_t thres, const trs_reorder_params& prm, bool capped = false) {
   const int32_t n = S.size();
   const auto cand = candidates(S, prm);
   std::vector<Pair> init(cand.size());
@@ -249,6 +253,7 @@ std::vector<int32_t> cluster(const Sets& S, int32_t thres, const trs_reorder_par
     const int32_t p1 = it.p1, p2 = it.p2;
     if (p1 == id[p1] && p2 == id[p2]) {
       if (closed[p1] || closed[p2]) continue;
+      if (capped && sz[p1] + sz[p2] > thres) continue;
       int32_t into = p1, from = p2;
       if (sz[p1] < sz[p2]) { into = p2; from = p1; }
       id[from] = into;
@@ -271,6 +276,47 @@ std::vector<int32_t> cluster(const Sets& S, int32_t thres, const trs_reorder_par
   std::vector<int32_t> out(n);
   for (int32_t i = 0; i < n; ++i) out[i] = root(i);
   return out;
+}
+
+// Window-aligned layout: within each level-2 group, clusters (each <= W rows) are packed first-fit
+// decreasing into bins of W rows; full bins are laid out in group order, the clusters of partial
+// bins are packed again at the end (full bins first), so only the tail windows mix leftovers.
+std::vector<int32_t> aligned_order(const std::vector<std::vector<int32_t>>& clusters,
+                                   const std::vector<std::vector<int32_t>>& super, int32_t W) {
+  std::vector<int32_t> order;
+  auto pack = [&](const std::vector<int32_t>& ids, std::vector<std::vector<int32_t>>& bins, std::vector<int32_t>& fill) {
+    std::vector<int32_t> s(ids);
+    std::stable_sort(s.begin(), s.end(), [&](int32_t a, int32_t b) { return clusters[a].size() > clusters[b].size(); });
+    for (int32_t c : s) {
+      const int32_t sz = (int32_t)clusters[c].size();
+      size_t b = 0;
+      while (b < bins.size() && fill[b] + sz > W) ++b;
+      if (b == bins.size()) { bins.emplace_back(); fill.push_back(0); }
+      bins[b].push_back(c);
+      fill[b] += sz;
+    }
+  };
+  auto emit = [&](const std::vector<int32_t>& bin) {
+    for (int32_t c : bin) order.insert(order.end(), clusters[c].begin(), clusters[c].end());
+  };
+  std::vector<int32_t> leftover;
+  for (const auto& grp : super) {
+    std::vector<std::vector<int32_t>> bins;
+    std::vector<int32_t> fill;
+    pack(grp, bins, fill);
+    for (size_t b = 0; b < bins.size(); ++b) {
+      if (fill[b] == W) emit(bins[b]);
+      else leftover.insert(leftover.end(), bins[b].begin(), bins[b].end());
+    }
+  }
+  std::vector<std::vector<int32_t>> bins;
+  std::vector<int32_t> fill;
+  pack(leftover, bins, fill);
+  for (size_t b = 0; b < bins.size(); ++b)
+    if (fill[b] == W) emit(bins[b]);
+  for (size_t b = 0; b < bins.size(); ++b)
+    if (fill[b] != W) emit(bins[b]);
+  return order;
 }
 
 // Groups of a root array in first-appearance order, members ascending.
@@ -302,6 +348,7 @@ void trs_reorder_params_default(trs_reorder_params* p) {
   p->bucket_span = 64;
   p->num_threads = 0;
   p->exhaustive = 0;
+  p->align_window = 0;
   p->seed = 2022;
 }
 
@@ -315,8 +362,9 @@ int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int
     return TRS_EINVAL;
   }
   if (prm.thres < 1 || prm.cluster_thres < 1 || prm.num_perm < 1 || prm.num_perm > 1024 ||
-      !(prm.lsh_threshold > 0.0f && prm.lsh_threshold < 1.0f)) {
-    trs::set_error("trs_tca_reorder: thres, cluster_thres >= 1, num_perm in 1..1024, lsh_threshold in (0, 1)");
+      !(prm.lsh_threshold > 0.0f && prm.lsh_threshold < 1.0f) || prm.align_window < 0) {
+    trs::set_error("trs_tca_reorder: thres, cluster_thres >= 1, num_perm in 1..1024, lsh_threshold in (0, 1), "
+                   "align_window >= 0");
     return TRS_EINVAL;
   }
   if (rows == 0) return TRS_OK;
@@ -348,7 +396,9 @@ int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int
       R.e.erase(std::unique(R.e.begin() + s, R.e.end()), R.e.end());
       R.off[i + 1] = (int64_t)R.e.size();
     }
-    const auto clusters = groups_of(cluster(R, prm.thres, prm));
+    const bool aligned = prm.align_window > 0;
+    const int32_t thres1 = aligned ? prm.align_window : prm.thres;
+    const auto clusters = groups_of(cluster(R, thres1, prm, aligned));
 
     // level 2: clusters as the union of their rows' sets
     Sets C;
@@ -363,9 +413,14 @@ int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int
     const auto super = groups_of(cluster(C, prm.cluster_thres, prm));
 
     int32_t k = 0;
-    for (const auto& grp : super)
-      for (int32_t c : grp)
-        for (int32_t row : clusters[c]) order[k++] = row;
+    if (aligned) {
+      const auto o = aligned_order(clusters, super, prm.align_window);
+      for (int32_t row : o) order[k++] = row;
+    } else {
+      for (const auto& grp : super)
+        for (int32_t c : grp)
+          for (int32_t row : clusters[c]) order[k++] = row;
+    }
     if (k != rows) {
       trs::set_error("trs_tca_reorder: internal error (order is not a permutation)");
       if (prm.num_threads > 0) omp_set_num_threads(saved_threads);

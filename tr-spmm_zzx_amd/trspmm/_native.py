@@ -41,7 +41,7 @@ class PlanStats(ctypes.Structure):
 
 class ReorderParams(ctypes.Structure):
     _fields_ = [("thres", c_i32), ("cluster_thres", c_i32), ("num_perm", c_i32), ("lsh_threshold", ctypes.c_float),
-                ("bucket_span", c_i32), ("num_threads", c_i32), ("exhaustive", c_i32), ("reserved", c_i32),
+                ("bucket_span", c_i32), ("num_threads", c_i32), ("exhaustive", c_i32), ("align_window", c_i32),
                 ("seed", ctypes.c_uint64)]
 
 

@@ -20,8 +20,9 @@ def _ptr(a: np.ndarray) -> ctypes.c_void_p:
 
 def tca_order(rowptr, col, ncols: int | None = None, thres: int = 16, cluster_thres: int = 128,
               num_perm: int = 128, lsh_threshold: float = 0.2, bucket_span: int = 64, exhaustive: bool = False,
-              seed: int = 2022, num_threads: int = 0) -> np.ndarray:
-    """order[new_row] = old_row for the rows of the CSR (rowptr[rows+1], col[nnz])."""
+              seed: int = 2022, num_threads: int = 0, align_window: int = 0) -> np.ndarray:
+    """order[new_row] = old_row for the rows of the CSR (rowptr[rows+1], col[nnz]).
+    align_window=W > 0 keeps clusters inside whole W-row windows (no reference counterpart)."""
     rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
     col = np.ascontiguousarray(col, dtype=np.int32)
     rows = rowptr.shape[0] - 1
@@ -31,6 +32,7 @@ def tca_order(rowptr, col, ncols: int | None = None, thres: int = 16, cluster_th
     nat.lib().trs_reorder_params_default(ctypes.byref(p))
     p.thres, p.cluster_thres, p.num_perm, p.lsh_threshold = thres, cluster_thres, num_perm, lsh_threshold
     p.bucket_span, p.exhaustive, p.seed, p.num_threads = bucket_span, int(bool(exhaustive)), seed, num_threads
+    p.align_window = align_window
     order = np.empty(max(rows, 0), dtype=np.int32)
     nat.check(nat.lib().trs_tca_reorder(_ptr(rowptr), _ptr(col), rows, col.shape[0], int(ncols), ctypes.byref(p),
                                         _ptr(order)), "trs_tca_reorder")
@@ -52,12 +54,13 @@ def permute_rows(rowptr, col, order, *extra):
     return tuple(out)
 
 
-def apply_tca_reorder(row_ptr, col_ind, num_nodes, thres=16, verbose=True):
-    """Reorder the first ``num_nodes`` rows; returns (new_row_ptr, new_col_ind, reorder_id)."""
+def apply_tca_reorder(row_ptr, col_ind, num_nodes, thres=16, verbose=True, align_window=0):
+    """Reorder the first ``num_nodes`` rows; returns (new_row_ptr, new_col_ind, reorder_id).
+    align_window (not in the reference): see tca_order."""
     t0 = time.time()
     row_ptr = np.asarray(row_ptr, dtype=np.int32)[: num_nodes + 1]
     col_ind = np.asarray(col_ind, dtype=np.int32)[: int(row_ptr[-1])] if num_nodes > 0 else np.zeros(0, np.int32)
-    order = tca_order(row_ptr, col_ind, thres=thres)
+    order = tca_order(row_ptr, col_ind, thres=thres, align_window=align_window)
     new_ptr, new_col = permute_rows(row_ptr, col_ind, order)
     if verbose:
         print(f"TCA: total reorder time = {time.time() - t0:.2f}s")
