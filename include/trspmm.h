@@ -114,6 +114,40 @@ int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int
                     const trs_reorder_params* params, int32_t* order);
 
 /* ---------------------------------------------------------------------------------------------
+ * Statistics-only 2:4 matching ("dual routing").
+ * Replaces matching_utils.match_2to4 (TR-source/Block/block_matching_window_para_dr.cpp:361-451,
+ * built by TR-source/setup_24matching.py:8-12): per window of window_size rows, columns carry a
+ * 16-bit row mask; a sliding 1:2 pairing (32 positions, overlap <= t_max) and a 2:4 grouping of the
+ * pairs (1024 positions, conflict-free masks) are counted, and the unmatched columns are routed to
+ * dense TC blocks of dense_threshold columns or to padded 2:4 groups.  No format arrays: counts only.
+ * Counters are 64-bit (the reference's 32-bit ones wrap on very large inputs); otherwise the totals
+ * equal the reference's, including its mask of local rows >= 16 (a shift of 1 by local_row mod 32,
+ * kept to 16 bits).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct trs_match_stats {
+  int64_t total_rows, total_cols, total_nnz;
+  double sparsity;                 /* 1 - total_nnz / (total_rows * total_cols) */
+  int64_t num_row_panels;          /* windows */
+  int64_t num_sptc_groups;         /* 2:4 groups (matched and fallback) */
+  int64_t num_tc_blocks;           /* dense blocks of dense_threshold columns */
+  int64_t num_16x16_blocks;        /* groups rounded up to 4 per window */
+  int64_t block_padding_groups;
+  int64_t fine_fallback;           /* columns without a 1:2 partner */
+  int64_t coarse_fallback;         /* columns of pairs without a 2:4 partner */
+  int64_t fake_zeros;              /* padding slots of all groups */
+  int64_t tc_total_nnz, tc_block_count, tc_block_max_nnz;
+  int64_t tc_block_min_nnz;        /* 999999 when there is no TC block, as in the reference */
+} trs_match_stats;
+
+/* rowptr[rows+1], col[nnz] on the host (rows need not be sorted; duplicates count once);
+ * total_cols = max(col) + 1.  TRS_EINVAL for window_size outside [1, 64], dense_threshold < 1,
+ * rows <= 0 or no column (the reference's "invalid matrix dimensions"), or a rowptr that is not
+ * monotone within [0, nnz]; TRS_ERANGE for a negative column.  num_threads 0 = OpenMP default;
+ * the result does not depend on it. */
+int trs_match_2to4(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t window_size,
+                   int32_t dense_threshold, int32_t t_max, int32_t num_threads, trs_match_stats* out);
+
+/* ---------------------------------------------------------------------------------------------
  * Plans.  A plan lowers format arrays to the device layout the kernels read (dense 16x16 fp16
  * MFMA tiles + an fp16 CSR residual with load-balanced row tasks), validates every index on the
  * host, and uploads once.  m = output rows (mOri), n = rows of the dense operand (kOri).

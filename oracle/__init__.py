@@ -12,8 +12,11 @@ Contents
                                    array (the semantic spec the GPU plan must honour)
   tca.py                           the TCA row reorder's clustering and ordering rules
                                    (spmm/tr_csr_fp16/tr_tca_reorder.py) over exhaustive candidates
+  matching.py                      the statistics-only 2:4 matcher
+                                   (TR-source/Block/block_matching_window_para_dr.cpp)
   Makefile                         builds _build/liboracle_builder.so and, where the reference
                                    sources exist, _ref/Libra5BlockOnline (the reference builder)
+                                   and _ref/matching_utils (the reference matcher)
 
 Parity status of each function is stated in its docstring ("pinned by ...").
 """

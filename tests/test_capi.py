@@ -32,6 +32,8 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(nat.BuildParams) == 12 * 4
     assert ctypes.sizeof(nat.PlanOptions) == 40
     assert ctypes.sizeof(nat.PlanStats) == 12 * 8
+    assert ctypes.sizeof(nat.ReorderParams) == 40
+    assert ctypes.sizeof(nat.MatchStats) == 16 * 8
 
 
 def _plan_csr(rowptr, col, val, m, n):

@@ -6,6 +6,7 @@ Layers
   ops        Format (builder output, cache files), Plan (device plan), spmm / sddmm on torch
              device tensors
   reorder    TCA row reorder (clusters rows with similar column sets into windows)
-Drop-in module names live next to this package: Libra5BlockOnline, Libra6SpMMOnline.
+  matching   statistics-only 2:4 matcher (counts of pairs, groups, dense blocks, padding)
+Drop-in module names live next to this package: Libra5BlockOnline, Libra6SpMMOnline, matching_utils.
 """
 from .ops import Format, Plan, build_format, build_format_cached, spmm, sddmm  # noqa: F401

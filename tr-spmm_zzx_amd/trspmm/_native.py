@@ -45,6 +45,14 @@ class ReorderParams(ctypes.Structure):
                 ("seed", ctypes.c_uint64)]
 
 
+class MatchStats(ctypes.Structure):
+    _fields_ = [("total_rows", c_i64), ("total_cols", c_i64), ("total_nnz", c_i64), ("sparsity", c_f64),
+                ("num_row_panels", c_i64), ("num_sptc_groups", c_i64), ("num_tc_blocks", c_i64),
+                ("num_16x16_blocks", c_i64), ("block_padding_groups", c_i64), ("fine_fallback", c_i64),
+                ("coarse_fallback", c_i64), ("fake_zeros", c_i64), ("tc_total_nnz", c_i64),
+                ("tc_block_count", c_i64), ("tc_block_max_nnz", c_i64), ("tc_block_min_nnz", c_i64)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/trspmm.h
 PROTOTYPES = {
     "trs_build_params_default": (None, [ctypes.POINTER(BuildParams)]),
@@ -59,6 +67,7 @@ PROTOTYPES = {
     "trs_reorder_params_default": (None, [ctypes.POINTER(ReorderParams)]),
     "trs_tca_reorder": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, ctypes.POINTER(ReorderParams), c_p]),
     "trs_format_read": (c_i32, [ctypes.c_char_p, c_pp]),
+    "trs_match_2to4": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(MatchStats)]),
     "trs_plan_options_default": (None, [ctypes.POINTER(PlanOptions)]),
     "trs_plan_create": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_parallel": (c_i32, [c_p, ctypes.POINTER(PlanOptions), c_pp]),
