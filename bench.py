@@ -15,6 +15,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -256,9 +257,19 @@ def bench_sddmm(args, workload, g, K):
 
 
 def ceiling_probe():
-    """Reference points for the roofline fractions: a 2 GiB device copy, and uniform-random row
-    gathers through the residual SpMM kernel (1M rows x d random columns, no column reuse) for
-    several operand sizes and row widths.  One JSON line per probe."""
+    """Reference points for the roofline fractions: streaming read / write / copy kernels
+    (./bench_stream_probe, built by __graft_entry__.build(), run first in a child process of its
+    own), a 2 GiB torch device copy, and uniform-random row gathers through the residual SpMM
+    kernel (1M rows x d random columns, no column reuse) for several operand sizes and row widths.
+    One JSON line per probe."""
+    probe = os.path.join(ROOT, "bench_stream_probe")
+    if not os.path.exists(probe):
+        sys.exit(f"{probe} is not built: run __graft_entry__.build()")
+    r = subprocess.run([probe], capture_output=True, text=True, timeout=300)
+    sys.stdout.write(r.stdout)
+    sys.stdout.flush()
+    if r.returncode != 0:
+        sys.exit(f"bench_stream_probe failed ({r.returncode}): {r.stderr[-500:]}")
     import numpy as np
     import torch
     import trspmm

@@ -194,6 +194,37 @@ def test_pipelined_and_plain_streams_agree(K, task_nnz):
     check(C, R, f"K={K} S={task_nnz}")
 
 
+@pytest.mark.parametrize("K", [72, 128])
+def test_staged_and_unstaged_streams_agree(K):
+    """16-lane groups (K = 65..128) stage each task's column ids and values in LDS when every task
+    holds <= 256 entries.  Tasks here start at every offset mod 8 and hold up to 256 entries; one
+    row of 280 entries is split in two pieces by the default plan (staged) and kept whole with
+    piece_nnz = 300 (a 280-entry task: the plan falls back to the unstaged stream).  Both against
+    the oracle; every other row is summed in the same order, so bitwise equal."""
+    say("staged", K)
+    rng = np.random.default_rng(11)
+    m, n = 4000, 20000
+    degs = rng.integers(0, 40, size=m)
+    degs[rng.choice(m, 60, replace=False)] = rng.integers(100, 257, size=60)
+    degs[1234] = 280
+    cols = np.concatenate([np.sort(rng.choice(n, size=d, replace=False)) for d in degs]).astype(np.int32)
+    rowptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+    val = rng.uniform(-1, 1, size=len(cols)).astype(np.float16).astype(np.float32)
+    f = trspmm.build_format(rowptr, cols, val, skip_tc=True)
+    Bh = dense_B(n, K, seed=5)
+    R = osp.csr_spmm(rowptr, cols, val, Bh, m=m)
+    opts = dict(mfma_tc=False, mfma_sptc=False, task_nnz=128)
+    staged = trspmm.Plan.from_format(f, m, n, **opts)
+    whole = trspmm.Plan.from_format(f, m, n, piece_nnz=300, **opts)
+    assert staged.stats()["split_rows"] == 1 and whole.stats()["split_rows"] == 0
+    C1 = run_plan(staged, Bh)
+    C2 = run_plan(whole, Bh)
+    check(C1, R, f"staged K={K}")
+    check(C2, R, f"unstaged K={K}")
+    keep = np.arange(m) != 1234
+    assert np.array_equal(C1[keep], C2[keep])
+
+
 def test_leading_dimension_beyond_int32_is_refused():
     from trspmm import _native as nat
     import ctypes

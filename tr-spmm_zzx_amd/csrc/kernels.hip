@@ -201,6 +201,15 @@ struct Batch {
       }
     }
   }
+  // the same from a stream staged in LDS: entry q sits at sc[q - base], sv[q - base]
+  __device__ __forceinline__ void load_lds(const int32_t* sc, const uint16_t* sv, int base, int p, int end) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+      const int q = (p + i < end ? p + i : end - 1) - base;
+      cc[i] = sc[q];
+      vh[i] = sv[q];
+    }
+  }
   __device__ __forceinline__ void gather(const uint16_t* __restrict__ Bf, int64_t ldb) {
 #pragma unroll
     for (int i = 0; i < U; ++i) bb[i].load(Bf + row_offset(cc[i], ldb));
@@ -260,9 +269,50 @@ __device__ __forceinline__ void accumulate_row(const int32_t* __restrict__ col, 
 constexpr int kNtLoads = 1;
 constexpr int kNtStores = 2;
 
+// Staged A stream (LS): a lane group copies its task's column ids and values into LDS once, in
+// whole 16-byte chunks from an 8-entry-aligned base (every chunk read by one load instruction, all
+// loads issued before the first store; the plan's device block has 256 bytes of tail, so chunks
+// ending past an array stay inside it), and its batches then read them from LDS.  The loads are
+// non-temporal: each line is read exactly once, and the A stream then stays out of the caches that
+// hold B rows.  Tasks hold <= kStageMax entries (the launcher checks DevicePlan::task_max).
+constexpr int kStageMax = 256;
+constexpr int kStageSpan = kStageMax + 8;
+typedef int32_t int4_t __attribute__((ext_vector_type(4)));
+
+template <int LPG>
+__device__ __forceinline__ void stage_stream(const int32_t* __restrict__ col, const uint16_t* __restrict__ val,
+                                             int nz_begin, int nz_end, int li, int32_t* sc, uint16_t* sv) {
+  constexpr int CC = (kStageSpan / 4 + LPG - 1) / LPG;   // 4-entry column chunks per lane
+  constexpr int VC = (kStageSpan / 8 + LPG - 1) / LPG;   // 8-entry value chunks per lane
+  const int base = nz_begin & ~7;
+  const int span = nz_end - base;
+  const int clast = (span - 1) >> 2, vlast = (span - 1) >> 3;
+  int4_t c[CC], v[VC];
+#pragma unroll
+  for (int k = 0; k < CC; ++k) {   // chunks past the span repeat the last one (same data, same slot)
+    const int j = li + k * LPG <= clast ? li + k * LPG : clast;
+    c[k] = load_stream<true>(reinterpret_cast<const int4_t*>(col + base) + j);
+  }
+#pragma unroll
+  for (int k = 0; k < VC; ++k) {
+    const int j = li + k * LPG <= vlast ? li + k * LPG : vlast;
+    v[k] = load_stream<true>(reinterpret_cast<const int4_t*>(val + base) + j);
+  }
+#pragma unroll
+  for (int k = 0; k < CC; ++k) {
+    const int j = li + k * LPG <= clast ? li + k * LPG : clast;
+    reinterpret_cast<int4_t*>(sc)[j] = c[k];
+  }
+#pragma unroll
+  for (int k = 0; k < VC; ++k) {
+    const int j = li + k * LPG <= vlast ? li + k * LPG : vlast;
+    reinterpret_cast<int4_t*>(sv)[j] = v[k];
+  }
+}
+
 // PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
-// together with the row pointers, before the barrier.
-template <int VEC, int LPG, int U, int NT, bool PF>
+// together with the row pointers, before the barrier.  LS: staged stream (see stage_stream).
+template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                     int K, float* __restrict__ C, int64_t ldc,
                                                     float* __restrict__ partial) {
@@ -272,6 +322,9 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   // row pointers of each lane group's task, preloaded once so a row flush never waits on a
   // dependent global load (tasks carry at most kTaskRows rows)
   __shared__ int s_rp[4][GPW][kTaskRows + 1];
+  __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
+  __shared__ __align__(16) uint16_t s_val[LS ? 4 * GPW * kStageSpan : 8];
+  static_assert(!(LS && PF), "a staged stream is not pipelined");
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
@@ -288,6 +341,12 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   if constexpr (PF) {
     if (valid && t.nz_begin < t.nz_end) b.load_a(col, val, t.nz_begin, t.nz_end);
   }
+  int32_t* sc = s_col + (LS ? (wave * GPW + grp) * kStageSpan : 0);
+  uint16_t* sv = s_val + (LS ? (wave * GPW + grp) * kStageSpan : 0);
+  const int sbase = t.nz_begin & ~7;
+  if constexpr (LS) {
+    if (valid && t.nz_begin < t.nz_end) stage_stream<LPG>(col, val, t.nz_begin, t.nz_end, li, sc, sv);
+  }
   __syncthreads();
   if (!valid) return;
 
@@ -296,10 +355,19 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const uint16_t* __restrict__ Bf = B + (active ? f : 0);
   float acc[VEC];
   zero_acc(acc);
+  // one batch: column ids and values (from LDS when staged) and its B gathers
+  auto begin_batch = [&](int p, int end) {
+    if constexpr (LS) {
+      b.load_lds(sc, sv, sbase, p, end);
+      b.gather(Bf, ldb);
+    } else {
+      b.template step_begin<PF>(n, col, val, Bf, ldb, p, end);
+    }
+  };
 
   if (t.row_end < 0) {   // piece of a split row -> partial slot (re-read by the fixup: keep cached)
     for (int p = t.nz_begin; p < t.nz_end; p += U) {
-      b.template step_begin<PF>(n, col, val, Bf, ldb, p, t.nz_end);
+      begin_batch(p, t.nz_end);
 #pragma unroll
       for (int i = 0; i < U; ++i)
         if (p + i < t.nz_end) b.bb[i].fma(acc, h2f(b.vh[i]));
@@ -312,7 +380,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   int r = 0;                       // row index relative to row_begin
   int rend = rp[1];
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
-    b.template step_begin<PF>(n, col, val, Bf, ldb, p, t.nz_end);
+    begin_batch(p, t.nz_end);
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       if (p + i < t.nz_end) {
@@ -674,20 +742,28 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // pipelined stream for narrow groups with long tasks only (same-box A/B: R-MAT K=32/64
     // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks) +6%)
     const bool pf = lpg <= 8 && p.task_nnz >= 64;
-#define TRS_TASKS_NT(L, U, PF)                                                                            \
+    // staged A stream for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128: 1.118 ->
+    // 0.975 ms, non-temporal staging loads 1% better than plain ones; K=256 +4%, not staged).
+    // Its 27 KB of LDS per workgroup hold it at 5 waves per SIMD; that is not where the gain
+    // comes from (the unstaged kernel forced to 5 waves takes 1.27 ms), and staging 128 entries
+    // at a time to reach 8 waves measured 1.02 ms.
+    const bool ls = p.task_max <= kStageMax;
+#define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
     switch (p.streaming & 3) {                                                                            \
-      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3, PF>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
     constexpr int U = L >= 16 ? 2 : 8;                                                                    \
     if constexpr (L <= 8) {                                                                               \
-      if (pf) { TRS_TASKS_NT(L, U, true) } else { TRS_TASKS_NT(L, U, false) }                             \
+      if (pf) { TRS_TASKS_NT(L, U, true, false) } else { TRS_TASKS_NT(L, U, false, false) }               \
+    } else if constexpr (L == 16) {                                                                       \
+      if (ls) { TRS_TASKS_NT(L, U, false, true) } else { TRS_TASKS_NT(L, U, false, false) }               \
     } else {                                                                                              \
-      TRS_TASKS_NT(L, U, false)                                                                           \
+      TRS_TASKS_NT(L, U, false, false)                                                                    \
     }                                                                                                     \
     break;                                                                                                \
   }

@@ -50,6 +50,7 @@ struct DevicePlan {
   int32_t xcd_run = 1;         // consecutive workgroups per XCD run (1 = hardware round robin)
   int32_t sddmm_unroll = 0;    // SDDMM residual entries in flight per lane group (4, 8; 0 automatic)
   int32_t task_nnz = 0;        // entries per packed residual task
+  int32_t task_max = 0;        // most entries of any residual task (packed rows or a piece)
 };
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.

@@ -354,7 +354,8 @@ struct Blob {
     total = off + v.size() * sizeof(T);
     return off;
   }
-  size_t size() const { return std::max<size_t>(total, 256); }
+  // 256 bytes past the last array: kernels may read whole 16-byte chunks that end past an array
+  size_t size() const { return total + 256; }
 };
 
 struct Tasks {
@@ -624,6 +625,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
   d.task_nnz = T.task_nnz;
+  d.task_max = 0;
+  for (const trs::Task& t : tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   P->csr_only = false;
