@@ -173,6 +173,9 @@ typedef struct trs_plan_options {
                              0 = automatic */
   int32_t sddmm_unroll;   /* SDDMM residual entries in flight per lane group: 4 or 8; 0 = automatic
                              (8) */
+  int32_t stage;          /* a residual task's column ids (and values) are copied into LDS once
+                             before its gathers: 0 = automatic (16-lane groups, i.e. K = 65..128,
+                             and tasks of <= 256 entries), -1 = never */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

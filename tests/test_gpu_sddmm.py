@@ -42,6 +42,35 @@ def test_sddmm_long_rows_and_empty_rows():
     assert np.max(np.abs(out.cpu().numpy() - R)) < 1e-3
 
 
+@pytest.mark.parametrize("K", [72, 128, 256])
+def test_staged_and_unstaged_sddmm_agree(K):
+    """16-lane groups (K = 65..128) stage each task's column ids in LDS (16-byte chunks from an
+    8-entry-aligned base); K = 256 never stages.  Tasks here start at every offset mod 8 and hold
+    up to 256 entries (rows of 100-256 entries, split rows beyond): staged and unstaged
+    (stage = -1) plans against the closed form, and bitwise equal to each other (same summation
+    order)."""
+    print("sddmm staged", K, flush=True)
+    rng = np.random.default_rng(12)
+    m, n = 3000, 20000
+    degs = rng.integers(0, 40, size=m)
+    degs[rng.choice(m, 50, replace=False)] = rng.integers(100, 257, size=50)
+    degs[777] = 600
+    cols = np.concatenate([np.sort(rng.choice(n, size=d, replace=False)) for d in degs]).astype(np.int32)
+    rowptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+    vals = np.ones(len(cols), np.float16)
+    Xh = graphs.dense_operand(m, K, seed=6)
+    Yh = graphs.dense_operand(n, K, seed=7)
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    staged = trspmm.Plan.from_csr(rowptr, cols, vals, m, n, task_nnz=128).sddmm(X, Y)
+    plain = trspmm.Plan.from_csr(rowptr, cols, vals, m, n, task_nnz=128, stage=-1).sddmm(X, Y)
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(rowptr, cols, Xh, Yh)
+    tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))
+    got = staged.cpu().numpy()
+    assert np.max(np.abs(got - R)) <= tol
+    assert np.array_equal(got, plain.cpu().numpy())
+
+
 def test_sddmm_matches_torch_sampled_addmm():
     g = graphs.random_csr(200, 300, 0.05, seed=3)
     plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)

@@ -223,6 +223,9 @@ def test_staged_and_unstaged_streams_agree(K):
     check(C2, R, f"unstaged K={K}")
     keep = np.arange(m) != 1234
     assert np.array_equal(C1[keep], C2[keep])
+    # the same plan with staging switched off (stage = -1): every row bitwise equal
+    C3 = run_plan(trspmm.Plan.from_format(f, m, n, stage=-1, **opts), Bh)
+    assert np.array_equal(C1, C3)
 
 
 def test_leading_dimension_beyond_int32_is_refused():

@@ -310,6 +310,26 @@ __device__ __forceinline__ void stage_stream(const int32_t* __restrict__ col, co
   }
 }
 
+// Column ids only (SDDMM has no values): same chunking and clamping as stage_stream.
+template <int LPG>
+__device__ __forceinline__ void stage_cols(const int32_t* __restrict__ col, int nz_begin, int nz_end, int li,
+                                           int32_t* sc) {
+  constexpr int CC = (kStageSpan / 4 + LPG - 1) / LPG;
+  const int base = nz_begin & ~7;
+  const int clast = (nz_end - base - 1) >> 2;
+  int4_t c[CC];
+#pragma unroll
+  for (int k = 0; k < CC; ++k) {
+    const int j = li + k * LPG <= clast ? li + k * LPG : clast;
+    c[k] = load_stream<true>(reinterpret_cast<const int4_t*>(col + base) + j);
+  }
+#pragma unroll
+  for (int k = 0; k < CC; ++k) {
+    const int j = li + k * LPG <= clast ? li + k * LPG : clast;
+    reinterpret_cast<int4_t*>(sc)[j] = c[k];
+  }
+}
+
 // PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
 // together with the row pointers, before the barrier.  LS: staged stream (see stage_stream).
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
@@ -595,8 +615,10 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // Residual SDDMM: a lane group streams its task's entries U at a time (rows from the row pointers
 // preloaded into LDS, as in k_spmm_tasks); each lane forms partial dot products over its VEC
 // features of X[row] and Y[col] (X rows repeat across a row's entries and stay cached), and the
-// U sums are finished by reduce_scatter.  Pieces of long rows carry a single row.
-template <int VEC, int LPG, int U>
+// U sums are finished by reduce_scatter.  Pieces of long rows carry a single row.  LS: the task's
+// column ids are first staged in LDS (as in k_spmm_tasks), so batches do not re-read their cache
+// lines through L2.
+template <int VEC, int LPG, int U, bool LS>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
                                                      float* __restrict__ out) {
@@ -604,6 +626,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   constexpr int FPP = LPG * VEC;               // features per pass
   constexpr int UB = U < LPG ? U : LPG;        // entries per reduce_scatter batch
   __shared__ int s_rp[4][GPW][kTaskRows + 1];
+  __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
@@ -614,6 +637,11 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   const bool piece = t.row_end < 0;
   int* rp = s_rp[wave][grp];
   if (valid && !piece) preload_rowptr<LPG>(P.rowptr, t.row_begin, t.row_end - t.row_begin, li, rp);
+  int32_t* sc = s_col + (LS ? (wave * GPW + grp) * kStageSpan : 0);
+  const int sbase = t.nz_begin & ~7;
+  if constexpr (LS) {
+    if (valid && t.nz_begin < t.nz_end) stage_cols<LPG>(P.col, t.nz_begin, t.nz_end, li, sc);
+  }
   __syncthreads();
   if (!valid) return;
 
@@ -622,7 +650,10 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U], rr[U];
 #pragma unroll
-    for (int i = 0; i < U; ++i) cc[i] = P.col[p + i < t.nz_end ? p + i : t.nz_end - 1];   // unconditional loads
+    for (int i = 0; i < U; ++i) {   // unconditional loads (padded slots repeat the last entry)
+      const int q = p + i < t.nz_end ? p + i : t.nz_end - 1;
+      cc[i] = LS ? sc[q - sbase] : P.col[q];
+    }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
       const bool in = p + i < t.nz_end;
@@ -747,7 +778,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // Its 27 KB of LDS per workgroup hold it at 5 waves per SIMD; that is not where the gain
     // comes from (the unstaged kernel forced to 5 waves takes 1.27 ms), and staging 128 entries
     // at a time to reach 8 waves measured 1.02 ms.
-    const bool ls = p.task_max <= kStageMax;
+    const bool ls = p.task_max <= kStageMax && p.stage >= 0;
 #define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
     switch (p.streaming & 3) {                                                                            \
       case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
@@ -807,15 +838,25 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     const int lpg = lanes_for(K, VEC);
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb);
+    // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
+    // 1.140 -> 1.112 ms; K=256 +1%, not staged)
+    const bool ls = p.task_max <= kStageMax && p.stage >= 0;
+#define TRS_SD_U(L, U)                                                                                     \
+    if constexpr (L == 16) {                                                                               \
+      if (ls) { hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, true>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break; } \
+    }                                                                                                      \
+    hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, false>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
 #define TRS_SD(L)                                                                                          \
   case L:                                                                                                  \
-    if (p.sddmm_unroll == 4)                                                                               \
-      hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 4>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
-    else                                                                                                   \
-      hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, 8>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);    \
+    if (p.sddmm_unroll == 4) {                                                                             \
+      TRS_SD_U(L, 4)                                                                                       \
+    } else {                                                                                               \
+      TRS_SD_U(L, 8)                                                                                       \
+    }                                                                                                      \
     break;
     switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
 #undef TRS_SD
+#undef TRS_SD_U
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.ntiles > 0 && p.tile_pos) {

@@ -629,6 +629,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   for (const trs::Task& t : tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
+  d.stage = opt.stage < 0 ? -1 : 0;
   P->csr_only = false;
   trs_plan_stats& s = P->stats;
   s.m = m;
@@ -743,6 +744,10 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.streaming = 0;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.sddmm_unroll = opt.sddmm_unroll == 4 || opt.sddmm_unroll == 8 ? opt.sddmm_unroll : 0;
+  d.stage = opt.stage < 0 ? -1 : 0;
+  d.task_nnz = T.task_nnz;
+  d.task_max = 0;
+  for (const trs::Task& t : T.tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
   P->csr_only = true;
   trs_plan_stats& s = P->stats;
   s.m = m;
@@ -787,6 +792,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->window_row_cap = 0;
   o->xcd_run = 0;
   o->sddmm_unroll = 0;
+  o->stage = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }
