@@ -113,6 +113,30 @@ def test_hybrid_sddmm_matches_closed_form(name, gen, K, mfma):
     assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
 
 
+@pytest.mark.parametrize("K", [8, 40, 128, 136, 264, 36, 6])
+def test_sddmm_mfma_tiles_feature_widths(K):
+    """Dense-tile SDDMM: K % 8 == 0 takes the 16x16x32 MFMA kernel (one 16-byte load per lane and
+    32-feature step, up to 4 steps loaded ahead: K = 8 and 40 end inside a step, 136 and 264 run
+    a second chunk); other widths the 16x16x16 kernel (8-byte loads for K % 4 == 0, guarded
+    scalars otherwise).  Against the closed form, with most entries on tiles."""
+    print("sddmm mfma K", K, flush=True)
+    g = graphs.sbm(communities=512, seed=4, val_seed=5)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    st = plan.stats()
+    nnz = int(g.rowptr[g.m])
+    assert st["mfma_tiles"] > 0 and st["mfma_nnz"] > nnz // 4
+    Xh = graphs.dense_operand(g.m, K, seed=13)
+    Yh = graphs.dense_operand(g.n, K, seed=14)
+    out = torch.full((nnz,), float("nan"), device="cuda")
+    plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda(), out=out)
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[:nnz], Xh, Yh)
+    got = out.cpu().numpy()
+    assert not np.isnan(got).any()
+    assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
+
+
 def test_sddmm_zero_width_writes_zeros():
     g = graphs.random_csr(100, 90, 0.05, seed=6)
     plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)
