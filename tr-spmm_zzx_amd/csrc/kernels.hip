@@ -595,21 +595,49 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
 // Sum v[i] (i < U) over the LPG lanes of a group, U <= LPG (powers of two), with LPG - 1 shuffles
 // in total: log2(U) halving exchanges, after which lane li holds a partial sum of entry
 // e = li / (LPG / U), then log2(LPG / U) xor steps finish it.  Returns that entry's sum.
+// Two spellings of the same exchanges, chosen by the code the compiler makes of them (same-box
+// A/B on R-MAT, 8 entries per batch): the recursive one for groups of >= 8 lanes (K=128
+// 1.098 -> 1.032 ms, K=64 0.582 -> 0.549), the loop for 4-lane groups (K=32 0.476 -> 0.463).
+// Exchanges over DPP row permutes instead of shuffles measured no faster (K=128 1.090 ms).
+template <int LPG, int U, int OFF, int W>
+__device__ __forceinline__ void rs_halve(float (&v)[U], int li) {
+  if constexpr (W >= 1) {
+    const bool upper = (li & OFF) != 0;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+      const float send = upper ? v[i] : v[i + W];
+      const float keep = upper ? v[i + W] : v[i];
+      v[i] = keep + __shfl_xor(send, OFF, 64);
+    }
+    rs_halve<LPG, U, OFF / 2, W / 2>(v, li);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float rs_finish(float v) {
+  if constexpr (OFF >= 1) return rs_finish<OFF / 2>(v + __shfl_xor(v, OFF, 64));
+  else return v;
+}
+
 template <int LPG, int U>
 __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
+  if constexpr (LPG >= 8) {
+    rs_halve<LPG, U, LPG / 2, U / 2>(v, li);
+    return rs_finish<LPG / (2 * U)>(v[0]);
+  } else {
 #pragma unroll
-  for (int w = U / 2, off = LPG / 2; w >= 1; w >>= 1, off >>= 1) {
-    const bool upper = (li & off) != 0;
+    for (int w = U / 2, off = LPG / 2; w >= 1; w >>= 1, off >>= 1) {
+      const bool upper = (li & off) != 0;
 #pragma unroll
-    for (int i = 0; i < w; ++i) {
-      const float send = upper ? v[i] : v[i + w];
-      const float keep = upper ? v[i + w] : v[i];
-      v[i] = keep + __shfl_xor(send, off, 64);
+      for (int i = 0; i < w; ++i) {
+        const float send = upper ? v[i] : v[i + w];
+        const float keep = upper ? v[i + w] : v[i];
+        v[i] = keep + __shfl_xor(send, off, 64);
+      }
     }
-  }
 #pragma unroll
-  for (int off = LPG / (2 * U); off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
-  return v[0];
+    for (int off = LPG / (2 * U); off >= 1; off >>= 1) v[0] += __shfl_xor(v[0], off, 64);
+    return v[0];
+  }
 }
 
 // Residual SDDMM: a lane group streams its task's entries U at a time (rows from the row pointers
@@ -647,6 +675,12 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
 
   int r = 0;
   int rend = piece ? t.nz_end : rp[1];
+  // with a single feature pass, the X fragment of the last row used carries over to the next
+  // batch, so X is fetched once per row instead of once per batch
+  const bool carry = K <= FPP;
+  BFrag<VEC> xc;
+  xc.zero();
+  int xrow = -1;
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U], rr[U];
 #pragma unroll
@@ -677,16 +711,21 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const uint16_t* __restrict__ Yf = Y + (f < K ? f : 0);
 #pragma unroll
       for (int i = 0; i < U; ++i) y[i].load(Yf + row_offset(cc[i], ldy));
+      const bool reuse = carry && rr[0] == xrow;
 #pragma unroll
       for (int i = 0; i < U; ++i) {
-        if (f < K && p + i < t.nz_end && (i == 0 || rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
+        if (f < K && p + i < t.nz_end && (i == 0 ? !reuse : rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
         else x[i].zero();
       }
-      BFrag<VEC> xe = x[0];
+      BFrag<VEC> xe = reuse ? xc : x[0];
 #pragma unroll
       for (int i = 0; i < U; ++i) {
         if (i > 0 && rr[i] != rr[i - 1]) xe = x[i];
         s[i] += xe.dot(y[i]);
+      }
+      if (carry) {
+        xc = xe;
+        xrow = rr[U - 1];
       }
     }
 #pragma unroll
