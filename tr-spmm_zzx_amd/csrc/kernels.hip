@@ -802,7 +802,7 @@ __global__ __launch_bounds__(256) void k_sddmm_mfma32(DevicePlan P, const uint16
   const int row = P.tile_row0[t] + (lane & 15);
   const int col = P.tile_cols[t * 16 + (lane & 15)];
   // rows past m and empty column slots read row 0: they only feed D rows / columns never stored
-  const uint16_t* xp = X + row_offset(row < P.m ? row : 0, ldx);
+  const uint16_t* xp = X + (int64_t)(row < P.m ? row : 0) * ldx;   // ldx may exceed 2^31 (ldy may not)
   const uint16_t* yp = Y + row_offset(col >= 0 ? col : 0, ldy);
   const int fq = 8 * (lane >> 4);
   float4_t acc{0.f, 0.f, 0.f, 0.f};
@@ -958,7 +958,6 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
   if (ev) (void)hipEventRecord(ev[2], s);
   return hipGetLastError();
 }
-
 
 __global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
