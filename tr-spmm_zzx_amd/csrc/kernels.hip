@@ -498,10 +498,10 @@ __global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, fl
 //   A: A[l % 16][4 * (l / 16) + j]      B: B[4 * (l / 16) + j][l % 16]
 //   D: D[4 * (l / 16) + j][l % 16]
 // Here A = the 16x16 tile (window row x tile column), B = gathered B rows (tile column x feature).
-// Occupancy floor for KC <= 128: the register budget of 6 waves per SIMD (measured: 5 waves cost
-// 6% on SBM K=128).
+// Occupancy floor: the register budget of 6 waves per SIMD (the compiler settles at 5 otherwise;
+// measured: 5 waves cost 6% on SBM K=128 and 4% at K=256, 0.963 vs 0.924 ms).
 template <int VEC, int NTILE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NTILE >= 4 ? 1 : 6)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
 void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, int K, float* __restrict__ C,
                      int64_t ldc, int KC) {
   extern __shared__ __align__(16) unsigned char smem[];
