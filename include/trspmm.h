@@ -176,6 +176,10 @@ typedef struct trs_plan_options {
   int32_t stage;          /* a residual task's column ids (and values) are copied into LDS once
                              before its gathers: 0 = automatic (16-lane groups, i.e. K = 65..128,
                              and tasks of <= 256 entries), -1 = never */
+  int32_t occupancy;      /* waves per SIMD the residual SpMM task kernel may hold (2..8; values
+                             outside are clamped): fewer concurrent tasks keep fewer gathered rows
+                             in flight.  0 = automatic (2 for K <= 64, uncapped above), -1 =
+                             uncapped (as many as registers and LDS allow) */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

@@ -228,6 +228,22 @@ def test_staged_and_unstaged_streams_agree(K):
     assert np.array_equal(C1, C3)
 
 
+@pytest.mark.parametrize("K", [16, 32, 64, 128])
+def test_occupancy_cap_does_not_change_results(K):
+    """The residual task kernel's occupancy cap (dynamic LDS that limits workgroups per CU; 2 waves
+    per SIMD by default for K <= 64) only changes how many tasks run at once: every output is
+    bitwise the same with the cap at 2, 5 or off, and matches the oracle."""
+    say("occupancy", K)
+    g = graphs.rmat(scale=12, edge_factor=16, seed=9)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, K, seed=4)
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m)
+    outs = [run_plan(trspmm.Plan.from_format(f, g.m, g.n, occupancy=o), Bh) for o in (0, 2, 5, -1)]
+    check(outs[0], R, f"occupancy K={K}")
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
+
+
 def test_leading_dimension_beyond_int32_is_refused():
     from trspmm import _native as nat
     import ctypes

@@ -832,6 +832,32 @@ __global__ __launch_bounds__(256) void k_sddmm_mfma32(DevicePlan P, const uint16
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+// LDS of one CU on gfx950.  The residual task kernel can be held to fewer workgroups per CU than
+// its registers allow by giving each workgroup unused dynamic LDS.
+constexpr int kLdsPerCu = 160 * 1024;
+
+// Dynamic LDS that lets at most `waves` 256-thread workgroups (= waves per SIMD) share a CU, given
+// the kernel's static LDS; 0 = uncapped.  waves >= 2 keeps a workgroup's LDS under the 64 KB
+// limit.  The 256-byte margin absorbs alignment of the static arrays.
+inline size_t occupancy_pad(size_t lds_static, int waves) {
+  if (waves <= 0) return 0;
+  const size_t want = (size_t)kLdsPerCu / (size_t)(waves + 1) + 256;
+  return want > lds_static ? want - lds_static : 0;
+}
+
+// Static LDS of k_spmm_tasks<.., LPG, .., LS>: the row-pointer slices and, when staged, the column
+// id and value slices (the arrays it declares).
+constexpr size_t tasks_static_lds(int lpg, bool ls) {
+  return (size_t)4 * (64 / lpg) * (kTaskRows + 1) * 4 + (ls ? (size_t)4 * (64 / lpg) * kStageSpan * 6 : 32);
+}
+
+template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
+void launch_tasks(dim3 grid, int waves, hipStream_t s, const DevicePlan& p, const uint16_t* B, int64_t ldb, int K,
+                  float* C, int64_t ldc, float* partial) {
+  hipLaunchKernelGGL((k_spmm_tasks<VEC, LPG, U, NT, PF, LS>), grid, dim3(256),
+                     occupancy_pad(tasks_static_lds(LPG, LS), waves), s, p, B, ldb, K, C, ldc, partial);
+}
+
 int lanes_for(int K, int vec) {
   const int need = (K + vec - 1) / vec;
   int l = 1;
@@ -864,12 +890,18 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // comes from (the unstaged kernel forced to 5 waves takes 1.27 ms), and staging 128 entries
     // at a time to reach 8 waves measured 1.02 ms.
     const bool ls = p.task_max <= kStageMax && p.stage >= 0;
+    // occupancy: lane groups of <= 8 lanes (K <= 64) run 8 entries per batch and are held to 2 waves
+    // per SIMD (same-box A/B at 7/6/5/4/3/2 waves: grid+hubs K=32 0.426 ... 0.395 / 0.389 ms,
+    // R-MAT K=32 0.495 -> 0.420, K=64 0.579 -> 0.519, K=16 0.456 -> 0.400); wider groups run 2
+    // entries per batch and are not capped (R-MAT K=128 at 5 / 4 / 3 waves: 0.970 / 0.985 / 1.147
+    // ms; K=256 at 8 / 3 waves: 2.24 / 3.49)
+    const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0 : (lpg <= 8 ? 2 : 0);
 #define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
     switch (p.streaming & 3) {                                                                            \
-      case 0: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 0, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 1: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 1, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      case 2: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 2, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
-      default: hipLaunchKernelGGL((k_spmm_tasks<VEC, L, U, 3, PF, LS>), grid, dim3(256), 0, s, p, B, ldb, K, C, ldc, partial); break; \
+      case 0: launch_tasks<VEC, L, U, 0, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      case 1: launch_tasks<VEC, L, U, 1, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      case 2: launch_tasks<VEC, L, U, 2, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      default: launch_tasks<VEC, L, U, 3, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;  \
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \

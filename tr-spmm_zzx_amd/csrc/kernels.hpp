@@ -49,6 +49,7 @@ struct DevicePlan {
   int32_t streaming = 0;       // bit 0: non-temporal A-stream loads, bit 1: non-temporal C stores
   int32_t xcd_run = 1;         // consecutive workgroups per XCD run (1 = hardware round robin)
   int32_t stage = 0;           // staged task streams: 0 automatic, -1 never
+  int32_t occupancy = 0;       // waves per SIMD for the residual task kernel: 2..8, 0 automatic, -1 uncapped
   int32_t sddmm_unroll = 0;    // SDDMM residual entries in flight per lane group (4, 8; 0 automatic)
   int32_t task_nnz = 0;        // entries per packed residual task
   int32_t task_max = 0;        // most entries of any residual task (packed rows or a piece)

@@ -630,6 +630,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.stage = opt.stage < 0 ? -1 : 0;
+  d.occupancy = opt.occupancy < 0 ? -1 : opt.occupancy == 0 ? 0 : std::min(8, std::max(2, opt.occupancy));
   P->csr_only = false;
   trs_plan_stats& s = P->stats;
   s.m = m;
@@ -745,6 +746,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.sddmm_unroll = opt.sddmm_unroll == 4 || opt.sddmm_unroll == 8 ? opt.sddmm_unroll : 0;
   d.stage = opt.stage < 0 ? -1 : 0;
+  d.occupancy = opt.occupancy < 0 ? -1 : opt.occupancy == 0 ? 0 : std::min(8, std::max(2, opt.occupancy));
   d.task_nnz = T.task_nnz;
   d.task_max = 0;
   for (const trs::Task& t : T.tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
@@ -793,6 +795,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->xcd_run = 0;
   o->sddmm_unroll = 0;
   o->stage = 0;
+  o->occupancy = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }

@@ -221,12 +221,12 @@ class Plan:
                     sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                     feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
-                    stage: Optional[int] = None) -> "Plan":
+                    stage: Optional[int] = None, occupancy: Optional[int] = None) -> "Plan":
         """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap,
-                     xcd_run=xcd_run, stage=stage)
+                     xcd_run=xcd_run, stage=stage, occupancy=occupancy)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
         return cls(h.value)
@@ -248,12 +248,13 @@ class Plan:
     @classmethod
     def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                  feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
-                 xcd_run: Optional[int] = None, stage: Optional[int] = None) -> "Plan":
+                 xcd_run: Optional[int] = None, stage: Optional[int] = None,
+                 occupancy: Optional[int] = None) -> "Plan":
         rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
         col = np.ascontiguousarray(col, dtype=np.int32)
         val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
         o = _options(False, False, 1.0, task_nnz, piece_nnz=piece_nnz, feature_lanes=feature_lanes,
-                     streaming=streaming, xcd_run=xcd_run, stage=stage)
+                     streaming=streaming, xcd_run=xcd_run, stage=stage, occupancy=occupancy)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_csr(_ptr(rowptr), _ptr(col), _ptr(val), m, n, ctypes.byref(o),
                                                 ctypes.byref(h)), "trs_plan_create_csr")
