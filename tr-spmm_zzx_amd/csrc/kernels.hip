@@ -330,6 +330,12 @@ __device__ __forceinline__ void stage_cols(const int32_t* __restrict__ col, int 
   }
 }
 
+// Static LDS of k_spmm_tasks<.., LPG, .., LS>: the row-pointer slices and, when staged, the column
+// id and value slices (the arrays it declares; checked there).
+constexpr size_t tasks_static_lds(int lpg, bool ls) {
+  return (size_t)4 * (64 / lpg) * (kTaskRows + 1) * 4 + (ls ? (size_t)4 * (64 / lpg) * kStageSpan * 6 : 32);
+}
+
 // PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
 // together with the row pointers, before the barrier.  LS: staged stream (see stage_stream).
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
@@ -345,6 +351,8 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
   __shared__ __align__(16) uint16_t s_val[LS ? 4 * GPW * kStageSpan : 8];
   static_assert(!(LS && PF), "a staged stream is not pipelined");
+  static_assert(sizeof(s_rp) + sizeof(s_col) + sizeof(s_val) == tasks_static_lds(LPG, LS),
+                "tasks_static_lds must describe this kernel's LDS (the occupancy cap depends on it)");
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
@@ -843,12 +851,6 @@ inline size_t occupancy_pad(size_t lds_static, int waves) {
   if (waves <= 0) return 0;
   const size_t want = (size_t)kLdsPerCu / (size_t)(waves + 1) + 256;
   return want > lds_static ? want - lds_static : 0;
-}
-
-// Static LDS of k_spmm_tasks<.., LPG, .., LS>: the row-pointer slices and, when staged, the column
-// id and value slices (the arrays it declares).
-constexpr size_t tasks_static_lds(int lpg, bool ls) {
-  return (size_t)4 * (64 / lpg) * (kTaskRows + 1) * 4 + (ls ? (size_t)4 * (64 / lpg) * kStageSpan * 6 : 32);
 }
 
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
