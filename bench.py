@@ -437,6 +437,8 @@ def main():
             "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
             "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if roof["traffic"]:   # measured HBM bytes of the same kernel over its live time, against the peak
+        roof["traffic_frac"] = round(roof["traffic"] / (kms[dom] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     log(f"[bench] kernels {kms}, roofline {roof}")
     ms_cold = cold_ms(lambda: plan.spmm(B, out=C, workspace=ws), max(5, min(args.steps, 10)))
     log(f"[bench] cold (L2 + MALL flushed) {ms_cold:.4f} ms/step")
