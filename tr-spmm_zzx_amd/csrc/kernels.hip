@@ -56,6 +56,24 @@ struct BFrag<8> {
   }
 };
 template <>
+struct BFrag<4> {
+  half4_t v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const half4_t*>(p); }
+  __device__ __forceinline__ void zero() { v = half4_t{0, 0, 0, 0}; }
+  __device__ __forceinline__ void fma(float (&acc)[4], float a) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(a, (float)v[i], acc[i]);
+  }
+  __device__ __forceinline__ float dot(const BFrag& o) const {
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      s = __builtin_amdgcn_fdot2(half2_t{v[2 * i], v[2 * i + 1]}, half2_t{o.v[2 * i], o.v[2 * i + 1]}, s, false);
+    return s;
+  }
+};
+template <>
 struct BFrag<1> {
   _Float16 v;
   __device__ __forceinline__ void load(const uint16_t* p) { v = __builtin_bit_cast(_Float16, *p); }
@@ -76,6 +94,10 @@ __device__ __forceinline__ void store_vec(float* dst, const float (&acc)[VEC]) {
       reinterpret_cast<float4_t*>(dst)[0] = lo;
       reinterpret_cast<float4_t*>(dst)[1] = hi;
     }
+  } else if constexpr (VEC == 4) {
+    const float4_t v{acc[0], acc[1], acc[2], acc[3]};
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(dst));
+    else reinterpret_cast<float4_t*>(dst)[0] = v;
   } else {
     if constexpr (NT) __builtin_nontemporal_store(acc[0], dst);
     else dst[0] = acc[0];
@@ -542,6 +564,7 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
       b.load(B + row_offset(c >= 0 ? c : 0, ldb) + (fbase + ff < K ? fbase + ff : K - VEC));
       if (!in) b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
+      else if constexpr (VEC == 4) *reinterpret_cast<half4_t*>(bst + k * KCB + ff) = b.v;
       else bst[k * KCB + ff] = b.v;
     }
     __syncthreads();
@@ -591,6 +614,9 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
       const float4_t hi = reinterpret_cast<const float4_t*>(src)[1];
       racc[0] += lo[0]; racc[1] += lo[1]; racc[2] += lo[2]; racc[3] += lo[3];
       racc[4] += hi[0]; racc[5] += hi[1]; racc[6] += hi[2]; racc[7] += hi[3];
+    } else if constexpr (VEC == 4) {
+      const float4_t v = reinterpret_cast<const float4_t*>(src)[0];
+      racc[0] += v[0]; racc[1] += v[1]; racc[2] += v[2]; racc[3] += v[3];
     } else {
       racc[0] += src[0];
     }
@@ -1010,14 +1036,22 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
                        float* partial, hipStream_t stream, hipEvent_t* ev) {
   const bool v8 = K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
                   (partial == nullptr || aligned16(partial));
+  // 8-byte loads when rows are only 8-byte aligned (K % 4 == 0): R-MAT K=100 3.22 ms with 2-byte
+  // loads
+  const bool v4 = K % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(B) & 7) == 0 &&
+                  aligned16(C) && (partial == nullptr || aligned16(partial));
   return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, stream, ev)
+       : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, stream, ev)
             : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, stream, ev);
 }
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                         int K, float* out, hipStream_t stream, hipEvent_t* ev) {
   const bool v8 = K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
+  const bool v4 = K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
+                  (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
   return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
+       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, stream, ev)
             : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream, ev);
 }
 
