@@ -923,7 +923,9 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // R-MAT K=32 0.495 -> 0.420, K=64 0.579 -> 0.519, K=16 0.456 -> 0.400); wider groups run 2
     // entries per batch and are not capped (R-MAT K=128 at 5 / 4 / 3 waves: 0.970 / 0.985 / 1.147
     // ms; K=256 at 8 / 3 waves: 2.24 / 3.49)
-    const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0 : (lpg <= 8 ? 2 : 0);
+    // (2-byte loads, used for K <= 8 and odd widths, stay uncapped: R-MAT K=8 0.293 ms uncapped,
+    // 0.326 at 2 waves)
+    const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0 : (lpg <= 8 && VEC >= 4 ? 2 : 0);
 #define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
     switch (p.streaming & 3) {                                                                            \
       case 0: launch_tasks<VEC, L, U, 0, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
@@ -1034,11 +1036,14 @@ hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
 
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                        float* partial, hipStream_t stream, hipEvent_t* ev) {
-  const bool v8 = K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
+  // wide loads only where they leave several lanes per group: with K <= 8 one or two lanes would
+  // stream a task alone (R-MAT K=8: 0.545 ms with one 16-byte load per entry, 0.348 with two
+  // lanes of 8-byte loads, 0.283 with eight lanes of 2-byte loads; K=4 0.515 -> 0.220)
+  const bool v8 = K >= 16 && K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
                   (partial == nullptr || aligned16(partial));
   // 8-byte loads when rows are only 8-byte aligned (K % 4 == 0): R-MAT K=100 3.22 ms with 2-byte
   // loads
-  const bool v4 = K % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(B) & 7) == 0 &&
+  const bool v4 = K > 8 && K % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(B) & 7) == 0 &&
                   aligned16(C) && (partial == nullptr || aligned16(partial));
   return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, stream, ev)
        : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, stream, ev)
