@@ -717,10 +717,25 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   int xrow = -1;
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U], rr[U];
+    if constexpr ((LPG == 2 || LPG == 4) && U % LPG == 0 && !LS) {
+      // quad-shared column loads: lane j of the group loads entries p + j, p + j + LPG, ... and
+      // the group exchanges them by DPP broadcasts, so a load instruction carries LPG times fewer
+      // requests
+      constexpr int R = U / LPG;
+      int c[R];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {   // unconditional loads (padded slots repeat the last entry)
-      const int q = p + i < t.nz_end ? p + i : t.nz_end - 1;
-      cc[i] = LS ? sc[q - sbase] : P.col[q];
+      for (int k = 0; k < R; ++k) {
+        const int q = p + k * LPG + li < t.nz_end ? p + k * LPG + li : t.nz_end - 1;
+        c[k] = P.col[q];
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) cc[i] = group_bcast<LPG>(c[i / LPG], i % LPG);
+    } else {
+#pragma unroll
+      for (int i = 0; i < U; ++i) {   // unconditional loads (padded slots repeat the last entry)
+        const int q = p + i < t.nz_end ? p + i : t.nz_end - 1;
+        cc[i] = LS ? sc[q - sbase] : P.col[q];
+      }
     }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -1036,10 +1051,12 @@ hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
 
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                        float* partial, hipStream_t stream, hipEvent_t* ev) {
-  // wide loads only where they leave several lanes per group: with K <= 8 one or two lanes would
-  // stream a task alone (R-MAT K=8: 0.545 ms with one 16-byte load per entry, 0.348 with two
-  // lanes of 8-byte loads, 0.283 with eight lanes of 2-byte loads; K=4 0.515 -> 0.220)
-  const bool v8 = K >= 16 && K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
+  // wide loads only where they leave at least 4 lanes per group (whose column/value loads are
+  // shared): with K <= 8 one or two lanes would stream a task alone (R-MAT K=8: 0.545 ms with one
+  // 16-byte load per entry, 0.348 with two lanes of 8-byte loads, 0.283 with eight lanes of 2-byte
+  // loads; K=4 0.515 -> 0.220), and K=16 runs best as 4 lanes of 8-byte loads (R-MAT 0.436 ms with
+  // 2 lanes of 16-byte loads, 0.324; grid+hubs 0.368 -> 0.307)
+  const bool v8 = K > 16 && K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
                   (partial == nullptr || aligned16(partial));
   // 8-byte loads when rows are only 8-byte aligned (K % 4 == 0): R-MAT K=100 3.22 ms with 2-byte
   // loads
@@ -1052,8 +1069,10 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                         int K, float* out, hipStream_t stream, hipEvent_t* ev) {
-  const bool v8 = K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
-  const bool v4 = K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
+  // as for the SpMM: K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms
+  // with one lane of 16-byte loads per task, 0.331), K=16 8-byte loads (0.514 -> 0.413 ms)
+  const bool v8 = K > 16 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
+  const bool v4 = K > 8 && K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
                   (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
   return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
        : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, stream, ev)
