@@ -10,7 +10,7 @@ import trspmm
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("K", [1, 4, 7, 12, 32, 36, 64, 100, 128, 256, 600])
+@pytest.mark.parametrize("K", [1, 4, 7, 8, 12, 16, 24, 32, 36, 64, 100, 128, 256, 600])
 def test_sddmm_matches_closed_form(K):
     print("sddmm K", K, flush=True)
     g = graphs.rmat(scale=12, edge_factor=16, seed=4)

@@ -84,7 +84,7 @@ def test_mfma_and_residual_routes_agree(mfma_tc, mfma_sptc, fill):
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), "routes")
 
 
-@pytest.mark.parametrize("K", [1, 3, 4, 8, 12, 16, 24, 36, 40, 100, 200, 256, 260, 520, 1030])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 8, 12, 16, 20, 24, 36, 40, 100, 200, 256, 260, 520, 1030])
 def test_feature_widths(K):
     say("K", K)
     g = graphs.sbm(communities=128, seed=1, val_seed=2)
