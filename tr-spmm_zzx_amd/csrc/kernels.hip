@@ -1069,9 +1069,11 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                         int K, float* out, hipStream_t stream, hipEvent_t* ev) {
-  // as for the SpMM: K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms
-  // with one lane of 16-byte loads per task, 0.331), K=16 8-byte loads (0.514 -> 0.413 ms)
-  const bool v8 = K > 16 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
+  // K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms with one lane of
+  // 16-byte loads per task, 0.331), and up to K=64 8-byte loads are faster than 16-byte ones
+  // (same-box A/B on R-MAT: K=16 0.514 -> 0.413 ms, K=32 0.468 -> 0.430, K=64 0.550 -> 0.503;
+  // K=128 1.038 vs 1.080 with 8-byte loads, so 16-byte loads from K=72 on)
+  const bool v8 = K > 64 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
   const bool v4 = K > 8 && K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
                   (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
   return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
