@@ -3,9 +3,10 @@
 // Three SpMM kernels, all writing every output element exactly once (no atomics, no zero-fill):
 //   k_spmm_tasks    residual CSR.  A "lane group" of LPG lanes owns one task: a run of whole rows
 //                   (the entries streamed flat, rows flushed as their end is crossed) or one piece
-//                   of a long row.  Each lane holds VEC=8 consecutive features, so one B row of
-//                   K fp16 is fetched by K/8 lanes with 16-byte loads; U nonzeros are in flight per
-//                   lane.  fp32 accumulation.  Replaces the reference residual kernels
+//                   of a long row.  Each lane holds VEC consecutive features (8, 4 or 1: 16-, 8- or
+//                   2-byte loads, by K and alignment), so one B row of K fp16 is fetched by K/VEC
+//                   lanes; U nonzeros are in flight per lane; narrow groups are held to 2 waves per
+//                   SIMD by dynamic LDS.  fp32 accumulation.  Replaces the reference residual kernels
 //                   (TR-source/SpMM/mGCNkernel.cu:976-1171, spmm_utils/compute.h:27-240), which
 //                   accumulate in fp16 and only handle K = 128.
 //   k_spmm_fixup    sums the pieces of split rows in a fixed order (deterministic).
@@ -18,9 +19,11 @@
 // SDDMM (no reference counterpart):
 //   k_sddmm_tasks   residual entries: one lane group per task, per-entry dot products reduced
 //                   across the group.
-//   k_sddmm_mfma    one wave per dense 16x16 tile: D = X[16 window rows] . Y[16 tile columns]^T
-//                   accumulated over K with v_mfma_f32_16x16x16_f16 (both operands contiguous in
-//                   K, loaded straight from global), sampled at the tile's stored entries.
+//   k_sddmm_mfma32  one wave per dense 16x16 tile: D = X[16 window rows] . Y[16 tile columns]^T
+//                   accumulated over K with gfx950's v_mfma_f32_16x16x32_f16 (both operands
+//                   contiguous in K, 16-byte loads straight from global), sampled at the tile's
+//                   stored entries; k_sddmm_mfma is the same with v_mfma_f32_16x16x16_f16 for K
+//                   that is not a multiple of 8.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
