@@ -606,10 +606,11 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
     if (row >= P.m) break;
     float racc[VEC];
     zero_acc(racc);
-    // pipelined residual rows pay for the widest windows only (same-box A/B on SBM: K=256
-    // 1.05 -> 1.01 ms; K=128 0.520 -> 0.544, K=64 0.286 -> 0.304)
-    accumulate_row<VEC, 8, false, (NTILE >= 4)>(P.col, P.val, B + (f < K ? f : 0), ldb, P.rowptr[row],
-                                                 P.rowptr[row + 1], racc);
+    // pipelined batches of 4 entries (same-box A/B on SBM against 8 unpipelined / 8 pipelined /
+    // 4 unpipelined: K=64 0.230 vs 0.246 / 0.257 / 0.248 ms, K=128 0.430 vs 0.462 / 0.479 /
+    // 0.468, K=256 0.909 vs 0.938 / 0.922 / 1.037)
+    accumulate_row<VEC, 4, false, true>(P.col, P.val, B + (f < K ? f : 0), ldb, P.rowptr[row], P.rowptr[row + 1],
+                                        racc);
     if (f >= K) continue;
     const float* src = otile + rl * KCP + ff;
     if constexpr (VEC == 8) {
