@@ -684,7 +684,7 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // U sums are finished by reduce_scatter.  Pieces of long rows carry a single row.  LS: the task's
 // column ids are first staged in LDS (as in k_spmm_tasks), so batches do not re-read their cache
 // lines through L2.
-template <int VEC, int LPG, int U, bool LS>
+template <int VEC, int LPG, int U, bool LS, bool SPF = false>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
                                                      float* __restrict__ out) {
@@ -719,8 +719,8 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   BFrag<VEC> xc;
   xc.zero();
   int xrow = -1;
-  for (int p = t.nz_begin; p < t.nz_end; p += U) {
-    int cc[U], rr[U];
+  // column ids of the batch at p (unconditional loads: padded slots repeat the last entry)
+  auto load_cols = [&](int p, int (&cc)[U]) {
     if constexpr ((LPG == 2 || LPG == 4) && U % LPG == 0 && !LS) {
       // quad-shared column loads: lane j of the group loads entries p + j, p + j + LPG, ... and
       // the group exchanges them by DPP broadcasts, so a load instruction carries LPG times fewer
@@ -736,10 +736,23 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       for (int i = 0; i < U; ++i) cc[i] = group_bcast<LPG>(c[i / LPG], i % LPG);
     } else {
 #pragma unroll
-      for (int i = 0; i < U; ++i) {   // unconditional loads (padded slots repeat the last entry)
+      for (int i = 0; i < U; ++i) {
         const int q = p + i < t.nz_end ? p + i : t.nz_end - 1;
         cc[i] = LS ? sc[q - sbase] : P.col[q];
       }
+    }
+  };
+  // PF: the next batch's column ids are loaded while this batch's gathers are in flight
+  constexpr bool PFC = SPF && !LS;
+  int cn[U];
+  if constexpr (PFC) load_cols(t.nz_begin, cn);
+  for (int p = t.nz_begin; p < t.nz_end; p += U) {
+    int cc[U], rr[U];
+    if constexpr (PFC) {
+#pragma unroll
+      for (int i = 0; i < U; ++i) cc[i] = cn[i];
+    } else {
+      load_cols(p, cc);
     }
 #pragma unroll
     for (int i = 0; i < U; ++i) {
@@ -764,6 +777,9 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const uint16_t* __restrict__ Yf = Y + (f < K ? f : 0);
 #pragma unroll
       for (int i = 0; i < U; ++i) y[i].load(Yf + row_offset(cc[i], ldy));
+      if constexpr (PFC) {
+        if (f0 == 0 && p + U < t.nz_end) load_cols(p + U, cn);
+      }
       const bool reuse = carry && rr[0] == xrow;
 #pragma unroll
       for (int i = 0; i < U; ++i) {
@@ -1005,13 +1021,15 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb);
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
-    // 1.140 -> 1.112 ms; K=256 +1%, not staged)
+    // 1.140 -> 1.112 ms; K=256 +1%, not staged); groups of <= 8 lanes load the next batch's
+    // column ids while the current batch's gathers are in flight (K=32 0.429 -> 0.416 ms, K=8
+    // -1%; 32-lane groups +1%, not pipelined)
     const bool ls = p.task_max <= kStageMax && p.stage >= 0;
 #define TRS_SD_U(L, U)                                                                                     \
     if constexpr (L == 16) {                                                                               \
       if (ls) { hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, true>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break; } \
     }                                                                                                      \
-    hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, false>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
+    hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, false, (L <= 8)>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
 #define TRS_SD(L)                                                                                          \
   case L:                                                                                                  \
     if (p.sddmm_unroll == 4) {                                                                             \
