@@ -944,9 +944,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
     // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
     // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
-    // pipelined stream for narrow groups with long tasks only (same-box A/B: R-MAT K=32/64
-    // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks) +6%)
-    const bool pf = lpg <= 8 && p.task_nnz >= 64;
+    // pipelined stream for narrow groups with long tasks (same-box A/B: R-MAT K=32/64
+    // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks, 4 lanes) +6%), and for 8-lane groups
+    // whatever the task length (grid+hubs K=64 0.620 -> 0.582 ms, K=8 0.251 -> 0.238)
+    const bool pf = lpg <= 8 && (p.task_nnz >= 64 || lpg == 8);
     // staged A stream for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128: 1.118 ->
     // 0.975 ms, non-temporal staging loads 1% better than plain ones; K=256 +4%, not staged).
     // Its 27 KB of LDS per workgroup hold it at 5 waves per SIMD; that is not where the gain
