@@ -164,8 +164,9 @@ typedef struct trs_plan_options {
   int32_t feature_lanes;  /* lanes per lane group (power of two <= 64; each lane holds 8 features):
                              fewer lanes = several feature passes with a smaller B working set
                              per pass (0 = automatic) */
-  int32_t streaming;      /* non-temporal hints, bit 0: A-stream loads, bit 1: C stores (keeps
-                             them from evicting gathered B rows); 0 plain; -1 automatic (C stores) */
+  int32_t streaming;      /* non-temporal hints, bit 0: A-stream loads, bit 1: C stores and
+                             residual SDDMM outputs (keeps them from evicting gathered B / Y
+                             rows); 0 plain; -1 automatic (bit 1) */
   int32_t window_row_cap; /* longest residual row an MFMA window may carry before its tiles go
                              back to the residual path (0 = automatic) */
   int32_t xcd_run;        /* workgroups are remapped so each of the 8 XCDs (own L2) runs this many

@@ -71,6 +71,31 @@ def test_staged_and_unstaged_sddmm_agree(K):
     assert np.array_equal(got, plain.cpu().numpy())
 
 
+@pytest.mark.parametrize("K", [4, 8, 16, 32, 72, 256])
+def test_streaming_and_plain_sddmm_stores_agree(K):
+    """Residual outputs go out with non-temporal stores where a lane group writes 8 consecutive
+    sums (groups of >= 8 lanes), plain stores otherwise and when the plan asks (streaming = 0):
+    bitwise equal, and on a hybrid plan whose residual outputs are scattered by res_pos."""
+    print("sddmm streaming", K, flush=True)
+    g = graphs.sbm(communities=512, seed=8, val_seed=9)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    nnz = int(g.rowptr[g.m])
+    X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=15)).cuda()
+    Y = torch.from_numpy(graphs.dense_operand(g.n, K, seed=16)).cuda()
+    outs = []
+    for streaming in (None, 0):
+        plan = trspmm.Plan.for_sddmm(f, g.m, g.n, streaming=streaming)
+        out = torch.full((nnz,), float("nan"), device="cuda")
+        plan.sddmm(X, Y, out=out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    a, b = (o.cpu().numpy() for o in outs)
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[:nnz], X.cpu().numpy(), Y.cpu().numpy())
+    assert not np.isnan(a).any()
+    assert np.max(np.abs(a - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
+    assert np.array_equal(a, b)
+
+
 def test_sddmm_matches_torch_sampled_addmm():
     g = graphs.random_csr(200, 300, 0.05, seed=3)
     plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)

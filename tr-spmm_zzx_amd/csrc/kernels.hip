@@ -683,8 +683,9 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // features of X[row] and Y[col] (X rows repeat across a row's entries and stay cached), and the
 // U sums are finished by reduce_scatter.  Pieces of long rows carry a single row.  LS: the task's
 // column ids are first staged in LDS (as in k_spmm_tasks), so batches do not re-read their cache
-// lines through L2.
-template <int VEC, int LPG, int U, bool LS, bool SPF = false>
+// lines through L2.  SPF: the next batch's column ids are loaded under the current gathers.  NTO:
+// outputs are written with non-temporal stores, so they do not evict gathered Y rows from L2.
+template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
                                                      float* __restrict__ out) {
@@ -804,7 +805,11 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       for (int i = 0; i < UB; ++i) v[i] = s[b + i];
       const float sum = reduce_scatter<LPG, UB>(v, li);
       const int e = b + li / (LPG / UB);
-      if (li % (LPG / UB) == 0 && p + e < t.nz_end) out[P.res_pos ? P.res_pos[p + e] : p + e] = sum;
+      if (li % (LPG / UB) == 0 && p + e < t.nz_end) {
+        float* o = &out[P.res_pos ? P.res_pos[p + e] : p + e];
+        if constexpr (NTO) __builtin_nontemporal_store(sum, o);
+        else *o = sum;
+      }
     }
   }
 }
@@ -1024,13 +1029,24 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
     // 1.140 -> 1.112 ms; K=256 +1%, not staged); groups of <= 8 lanes load the next batch's
     // column ids while the current batch's gathers are in flight (K=32 0.429 -> 0.416 ms, K=8
-    // -1%; 32-lane groups +1%, not pipelined)
+    // -1%; 32-lane groups +1%, not pipelined); outputs written with non-temporal stores unless
+    // the plan asks for plain ones, where a group writes 8 consecutive sums (32 bytes) per store
+    // (same-box A/B on R-MAT: K=8 0.329 -> 0.264 ms, K=32 0.423 -> 0.394, K=64 -1.5%, K=128 -1%;
+    // 16-byte runs, as 4-lane groups write at K=16, lose: 0.418 -> 0.469)
     const bool ls = p.task_max <= kStageMax && p.stage >= 0;
+    const bool nto = (p.streaming & 2) != 0;
+#define TRS_SD_LAUNCH(...) hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out)
 #define TRS_SD_U(L, U)                                                                                     \
+    constexpr bool nt_ok = (U < L ? U : L) >= 8;                                                           \
     if constexpr (L == 16) {                                                                               \
-      if (ls) { hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, true>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out); break; } \
+      if (ls) {                                                                                            \
+        if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, true, false, nt_ok);                                    \
+        else TRS_SD_LAUNCH(VEC, L, U, true);                                                               \
+        break;                                                                                             \
+      }                                                                                                    \
     }                                                                                                      \
-    hipLaunchKernelGGL((k_sddmm_tasks<VEC, L, U, false, (L <= 8)>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out);
+    if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, false, (L <= 8), nt_ok);                                    \
+    else TRS_SD_LAUNCH(VEC, L, U, false, (L <= 8));
 #define TRS_SD(L)                                                                                          \
   case L:                                                                                                  \
     if (p.sddmm_unroll == 4) {                                                                             \
@@ -1042,6 +1058,7 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     switch (lpg) { TRS_SD(1) TRS_SD(2) TRS_SD(4) TRS_SD(8) TRS_SD(16) TRS_SD(32) TRS_SD(64) }
 #undef TRS_SD
 #undef TRS_SD_U
+#undef TRS_SD_LAUNCH
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.ntiles > 0 && p.tile_pos) {

@@ -742,7 +742,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.tile_pos = tile_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tpos);
   d.ntiles = tile_pos.empty() ? 0 : (int32_t)L.tiles.size();
   d.feature_lanes = opt.feature_lanes;
-  d.streaming = 0;
+  d.streaming = opt.streaming < 0 ? 2 : (opt.streaming & 2);
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.sddmm_unroll = opt.sddmm_unroll == 4 || opt.sddmm_unroll == 8 ? opt.sddmm_unroll : 0;
   d.stage = opt.stage < 0 ? -1 : 0;

@@ -235,11 +235,14 @@ class Plan:
     def for_sddmm(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
                   sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
-                  sddmm_unroll: Optional[int] = None, stage: Optional[int] = None) -> "Plan":
+                  sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
+                  streaming: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
-        ``sddmm`` outputs follow the input CSR order."""
+        ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
+        residual outputs with non-temporal stores."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
-                     feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage)
+                     feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
+                     streaming=streaming)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
                   "trs_plan_create_sddmm")
