@@ -624,7 +624,7 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
     } else {
       racc[0] += src[0];
     }
-    if (P.streaming & 2) store_vec<VEC, true>(C + (int64_t)row * ldc + f, racc);
+    if ((P.streaming & 2) && K >= 8) store_vec<VEC, true>(C + (int64_t)row * ldc + f, racc);
     else store_vec<VEC, false>(C + (int64_t)row * ldc + f, racc);
   }
 }
@@ -967,8 +967,12 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // (2-byte loads, used for K <= 8 and odd widths, stay uncapped: R-MAT K=8 0.293 ms uncapped,
     // 0.326 at 2 waves)
     const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0 : (lpg <= 8 && VEC >= 4 ? 2 : 0);
+    // non-temporal C stores only where a row is at least 32 bytes (K >= 8): shorter rows lose
+    // the L2's write combining (same-box A/B on grid+hubs: K=4 0.226 ms plain vs 0.246 streamed,
+    // K=1 0.201 vs 0.208; K=8 0.292 plain vs 0.242 streamed, R-MAT K=16 0.341 vs 0.320)
+    const int streaming = K >= 8 ? (p.streaming & 3) : (p.streaming & 1);
 #define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
-    switch (p.streaming & 3) {                                                                            \
+    switch (streaming) {                                                                                  \
       case 0: launch_tasks<VEC, L, U, 0, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
       case 1: launch_tasks<VEC, L, U, 1, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
       case 2: launch_tasks<VEC, L, U, 2, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
