@@ -10,7 +10,7 @@ import trspmm
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("K", [1, 4, 7, 8, 12, 16, 24, 32, 36, 64, 100, 128, 256, 600])
+@pytest.mark.parametrize("K", [1, 4, 7, 8, 10, 12, 14, 16, 18, 24, 30, 32, 36, 64, 66, 100, 128, 130, 256, 600])
 def test_sddmm_matches_closed_form(K):
     print("sddmm K", K, flush=True)
     g = graphs.rmat(scale=12, edge_factor=16, seed=4)
@@ -25,6 +25,27 @@ def test_sddmm_matches_closed_form(K):
     # per-entry dot of K fp16 products, fp32 accumulation
     tol = 1e-5 * np.sqrt(K) * 4 + 1e-6
     assert np.max(np.abs(got - R)) <= tol * max(1.0, np.max(np.abs(R))), np.max(np.abs(got - R))
+
+
+@pytest.mark.parametrize("K,pad", [(14, 2), (14, 1), (16, 1), (12, 2), (40, 2)])
+def test_sddmm_strided_operands(K, pad):
+    """X and Y as column slices of wider arrays (leading dimension K + pad): an even leading
+    dimension keeps 4-byte loads (K = 9..16 and even widths not divisible by 4), an odd one falls
+    back to 2-byte loads; both against the closed form."""
+    print("sddmm strided", K, pad, flush=True)
+    g = graphs.rmat(scale=11, edge_factor=8, seed=10)
+    plan = trspmm.Plan.from_csr(g.rowptr, g.col, g.val.astype(np.float16), g.m, g.n)
+    Xh = graphs.dense_operand(g.m, K, seed=21)
+    Yh = graphs.dense_operand(g.n, K, seed=22)
+    Xw = torch.zeros((g.m, K + pad), dtype=torch.float16, device="cuda")
+    Yw = torch.zeros((g.n, K + pad), dtype=torch.float16, device="cuda")
+    Xw[:, :K] = torch.from_numpy(Xh).cuda()
+    Yw[:, :K] = torch.from_numpy(Yh).cuda()
+    out = plan.sddmm(Xw[:, :K], Yw[:, :K])
+    torch.cuda.synchronize()
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))
+    assert np.max(np.abs(out.cpu().numpy() - R)) <= tol
 
 
 def test_sddmm_long_rows_and_empty_rows():

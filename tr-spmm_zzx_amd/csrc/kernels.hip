@@ -18,7 +18,7 @@
 //                   (mGCNkernel_online.cu:54-241, 812-933) and the add kernel (:1314-1324).
 // SDDMM (no reference counterpart):
 //   k_sddmm_tasks   residual entries: one lane group per task, per-entry dot products reduced
-//                   across the group.
+//                   across the group; 16-, 8-, 4- or 2-byte loads of X and Y by K and alignment.
 //   k_sddmm_mfma32  one wave per dense 16x16 tile: D = X[16 window rows] . Y[16 tile columns]^T
 //                   accumulated over K with gfx950's v_mfma_f32_16x16x32_f16 (both operands
 //                   contiguous in K, 16-byte loads straight from global), sampled at the tile's
@@ -31,6 +31,7 @@
 namespace trs {
 namespace {
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -50,7 +51,6 @@ struct BFrag<8> {
   }
   // v_dot2_f32_f16: two fp16 products (exact in fp32) added to an fp32 accumulator per instruction
   __device__ __forceinline__ float dot(const BFrag& o) const {
-    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -68,13 +68,23 @@ struct BFrag<4> {
     for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(a, (float)v[i], acc[i]);
   }
   __device__ __forceinline__ float dot(const BFrag& o) const {
-    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       s = __builtin_amdgcn_fdot2(half2_t{v[2 * i], v[2 * i + 1]}, half2_t{o.v[2 * i], o.v[2 * i + 1]}, s, false);
     return s;
   }
+};
+template <>
+struct BFrag<2> {
+  half2_t v;
+  __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const half2_t*>(p); }
+  __device__ __forceinline__ void zero() { v = half2_t{0, 0}; }
+  __device__ __forceinline__ void fma(float (&acc)[2], float a) const {
+    acc[0] = __builtin_fmaf(a, (float)v[0], acc[0]);
+    acc[1] = __builtin_fmaf(a, (float)v[1], acc[1]);
+  }
+  __device__ __forceinline__ float dot(const BFrag& o) const { return __builtin_amdgcn_fdot2(v, o.v, 0.f, false); }
 };
 template <>
 struct BFrag<1> {
@@ -1115,11 +1125,17 @@ hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, con
                         int K, float* out, hipStream_t stream, hipEvent_t* ev) {
   // K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms with one lane of
   // 16-byte loads per task, 0.331), and up to K=64 8-byte loads are faster than 16-byte ones
-  // (same-box A/B on R-MAT: K=16 0.514 -> 0.413 ms, K=32 0.468 -> 0.430, K=64 0.550 -> 0.503;
-  // K=128 1.038 vs 1.080 with 8-byte loads, so 16-byte loads from K=72 on)
+  // (same-box A/B on R-MAT: K=32 0.468 -> 0.430 ms, K=64 0.550 -> 0.503; K=128 1.038 vs 1.080
+  // with 8-byte loads, so 16-byte loads from K=72 on)
   const bool v8 = K > 64 && K % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(X) && aligned16(Y);
   const bool v4 = K > 8 && K % 4 == 0 && ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 7) == 0 &&
                   (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
+  // 4-byte loads for K = 9..16 (8-lane groups, whose outputs go out in 32-byte runs; R-MAT K=16
+  // 0.418 -> 0.334 ms, K=12 0.408 -> 0.287) and for other even widths that 8-byte loads cannot
+  // serve (K=18 0.743 -> 0.431 ms, K=66 1.866 -> 1.479, K=130 2.350 -> 1.993 with 2-byte loads)
+  const bool v2 = K > 8 && (K <= 16 || !(v8 || v4)) && K % 2 == 0 && ldx % 2 == 0 && ldy % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(X) & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 3) == 0;
+  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, stream, ev);
   return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
        : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, stream, ev)
             : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream, ev);
