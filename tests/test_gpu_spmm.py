@@ -84,7 +84,8 @@ def test_mfma_and_residual_routes_agree(mfma_tc, mfma_sptc, fill):
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), "routes")
 
 
-@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 8, 12, 16, 20, 24, 36, 40, 100, 200, 256, 260, 520, 1030])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 8, 10, 12, 14, 16, 18, 20, 24, 30, 36, 40, 66, 98, 100, 130, 200,
+                               256, 260, 520, 1030])
 def test_feature_widths(K):
     say("K", K)
     g = graphs.sbm(communities=128, seed=1, val_seed=2)
@@ -109,26 +110,28 @@ def test_strided_operands_and_output():
     assert torch.all(out_full[:, :4] == 7.0) and torch.all(out_full[:, 68:] == 7.0)
 
 
-@pytest.mark.parametrize("K,vec", [(100, 4), (36, 4), (132, 4), (98, 1)])
-def test_eight_byte_path_long_rows_and_offsets(K, vec):
-    """K % 4 == 0 but K % 8 != 0 takes 8-byte B loads (rows only 8-byte aligned): split rows and
-    their fixups, the MFMA window kernel, and a B view starting 4 halves into its buffer; other K
-    take 2-byte loads."""
-    say("vec", K, vec)
+@pytest.mark.parametrize("K,off,vec", [(100, 4, 4), (36, 4, 4), (132, 4, 4), (98, 4, 2), (18, 4, 2),
+                                       (66, 4, 2), (100, 2, 2), (98, 1, 1)])
+def test_narrow_load_paths_long_rows_and_offsets(K, off, vec):
+    """B as a view starting `off` halves into its buffer: K % 4 == 0 with rows 8-byte aligned takes
+    8-byte loads, even K with rows 4-byte aligned 4-byte loads, the rest 2-byte loads (`vec`
+    features per load).  Split rows and their fixups, and the MFMA window kernel."""
+    say("vec", K, off, vec)
     g = graphs.rmat(scale=12, edge_factor=16, seed=12)
     f = trspmm.build_format(g.rowptr, g.col, g.val)
     plan = trspmm.Plan.from_format(f, g.m, g.n, piece_nnz=64)
     assert plan.stats()["split_rows"] > 0
     Bfull = torch.from_numpy(dense_B(g.n + 1, K, seed=K).reshape(-1)[: (g.n + 1) * K]).cuda()
-    B = Bfull[4: 4 + g.n * K].view(g.n, K)            # 8-byte aligned, not 16
-    assert B.data_ptr() % 16 == 8
+    B = Bfull[off: off + g.n * K].view(g.n, K)
+    assert B.data_ptr() % 16 == 2 * off
     C = plan.spmm(B)
     torch.cuda.synchronize()
     check(C.cpu().numpy(), osp.csr_spmm(g.rowptr, g.col, g.val, B.cpu().numpy(), m=g.m), f"K={K}")
     s = graphs.sbm(communities=128, seed=5, val_seed=6)
     sp = trspmm.Plan.from_format(trspmm.build_format(s.rowptr, s.col, s.val), s.m, s.n)
     assert sp.stats()["mfma_tiles"] > 0
-    Bs = torch.from_numpy(dense_B(s.n, K, seed=K + 1)).cuda()
+    Bsf = torch.from_numpy(dense_B(s.n + 1, K, seed=K + 1).reshape(-1)[: (s.n + 1) * K]).cuda()
+    Bs = Bsf[off: off + s.n * K].view(s.n, K)
     Cs = sp.spmm(Bs)
     torch.cuda.synchronize()
     check(Cs.cpu().numpy(), osp.csr_spmm(s.rowptr, s.col, s.val, Bs.cpu().numpy(), m=s.m), f"sbm K={K}")

@@ -3,10 +3,10 @@
 // Three SpMM kernels, all writing every output element exactly once (no atomics, no zero-fill):
 //   k_spmm_tasks    residual CSR.  A "lane group" of LPG lanes owns one task: a run of whole rows
 //                   (the entries streamed flat, rows flushed as their end is crossed) or one piece
-//                   of a long row.  Each lane holds VEC consecutive features (8, 4 or 1: 16-, 8- or
-//                   2-byte loads, by K and alignment), so one B row of K fp16 is fetched by K/VEC
-//                   lanes; U nonzeros are in flight per lane; narrow groups are held to 2 waves per
-//                   SIMD by dynamic LDS.  fp32 accumulation.  Replaces the reference residual kernels
+//                   of a long row.  Each lane holds VEC consecutive features (8, 4, 2 or 1:
+//                   16-, 8-, 4- or 2-byte loads, by K and alignment), so one B row of K fp16 is
+//                   fetched by K/VEC lanes; U nonzeros are in flight per lane; narrow groups are
+//                   held to 2 or 4 waves per SIMD by dynamic LDS.  fp32 accumulation.  Replaces the reference residual kernels
 //                   (TR-source/SpMM/mGCNkernel.cu:976-1171, spmm_utils/compute.h:27-240), which
 //                   accumulate in fp16 and only handle K = 128.
 //   k_spmm_fixup    sums the pieces of split rows in a fixed order (deterministic).
@@ -34,6 +34,7 @@ namespace {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -111,6 +112,10 @@ __device__ __forceinline__ void store_vec(float* dst, const float (&acc)[VEC]) {
     const float4_t v{acc[0], acc[1], acc[2], acc[3]};
     if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<float4_t*>(dst));
     else reinterpret_cast<float4_t*>(dst)[0] = v;
+  } else if constexpr (VEC == 2) {
+    const float2_t v{acc[0], acc[1]};
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<float2_t*>(dst));
+    else reinterpret_cast<float2_t*>(dst)[0] = v;
   } else {
     if constexpr (NT) __builtin_nontemporal_store(acc[0], dst);
     else dst[0] = acc[0];
@@ -578,6 +583,7 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
       if (!in) b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
       else if constexpr (VEC == 4) *reinterpret_cast<half4_t*>(bst + k * KCB + ff) = b.v;
+      else if constexpr (VEC == 2) *reinterpret_cast<half2_t*>(bst + k * KCB + ff) = b.v;
       else bst[k * KCB + ff] = b.v;
     }
     __syncthreads();
@@ -631,6 +637,9 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
     } else if constexpr (VEC == 4) {
       const float4_t v = reinterpret_cast<const float4_t*>(src)[0];
       racc[0] += v[0]; racc[1] += v[1]; racc[2] += v[2]; racc[3] += v[3];
+    } else if constexpr (VEC == 2) {
+      const float2_t v = reinterpret_cast<const float2_t*>(src)[0];
+      racc[0] += v[0]; racc[1] += v[1];
     } else {
       racc[0] += src[0];
     }
@@ -976,7 +985,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // ms; K=256 at 8 / 3 waves: 2.24 / 3.49)
     // (2-byte loads, used for K <= 8 and odd widths, stay uncapped: R-MAT K=8 0.293 ms uncapped,
     // 0.326 at 2 waves)
-    const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0 : (lpg <= 8 && VEC >= 4 ? 2 : 0);
+    // (4-byte loads in 8-lane groups, K = 10 and 14: 4 waves; R-MAT K=10 0.358 ms uncapped, 0.346
+    // at 4 waves, 0.396 at 2)
+    const int waves = p.occupancy > 0 ? p.occupancy : p.occupancy < 0 ? 0
+                    : lpg <= 8 ? (VEC >= 4 ? 2 : VEC == 2 ? 4 : 0) : 0;
     // non-temporal C stores only where a row is at least 32 bytes (K >= 8): shorter rows lose
     // the L2's write combining (same-box A/B on grid+hubs: K=4 0.226 ms plain vs 0.246 streamed,
     // K=1 0.201 vs 0.208; K=8 0.292 plain vs 0.242 streamed, R-MAT K=16 0.341 vs 0.320)
@@ -1116,6 +1128,14 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
   // loads
   const bool v4 = K > 8 && K % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(B) & 7) == 0 &&
                   aligned16(C) && (partial == nullptr || aligned16(partial));
+  // 4-byte loads for even widths that 8-byte loads cannot serve (same-box A/B against 2-byte
+  // loads, R-MAT: K=10 0.438 -> 0.346 ms, K=18 0.776 -> 0.612, K=30 0.828 -> 0.641, K=98 3.245 ->
+  // 2.313; SBM K=18 0.295 -> 0.208).  K=12 and 16 stay on 8-byte loads in 4-lane groups (R-MAT
+  // K=16 0.318 vs 0.333 ms with 4-byte loads in 8-lane groups)
+  const bool v2 = K > 8 && !(v8 || v4) && K % 2 == 0 && ldb % 2 == 0 && ldc % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(B) & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0 &&
+                  (partial == nullptr || aligned16(partial));
+  if (v2) return launch_spmm_vec<2>(p, B, ldb, K, C, ldc, partial, stream, ev);
   return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, stream, ev)
        : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, stream, ev)
             : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, stream, ev);
