@@ -327,7 +327,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 100 untimed steps by default: after the seconds of host-side graph and plan building the GPU
+    # clocks need tens of milliseconds of work to ramp up (SDDMM K=64: 0.592 ms per step after 5
+    # warm-up steps, 0.499 after 200; R-MAT SpMM K=128 unchanged at 0.969)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--k", type=int, default=0, help="override the configuration's feature width")
