@@ -239,10 +239,12 @@ def bench_sddmm(args, workload, g, K):
     achieved = bytes_k / (kms[dom] * 1e-3) / 1e9
     alg_total = 8 * g.nnz + 4 * (M + 1) + 2 * M * K + 2 * N * K
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(names[dom], workload),
             "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
             "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if roof["traffic"]:
+        roof["traffic_frac"] = round(roof["traffic"] / (kms[dom] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     outj = {"metric": f"SDDMM GFLOP/s (2·nnz·K) + % HBM roofline, R-MAT 2^20 pattern K={K} fp16", "value": round(gflops, 2),
             "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
@@ -314,8 +316,10 @@ def ceiling_probe():
         del plan, B, C, f
 
 
-def load_traffic(workload: str):
-    path = os.path.join(ROOT, "profiles", f"spmm_tasks_{workload}_pmc.json")
+def load_traffic(kernel: str, workload: str):
+    """Measured HBM bytes per launch of `kernel` on `workload` (FETCH_SIZE and WRITE_SIZE runs,
+    scaled by a device copy of known size), or None where no counter run is recorded."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -436,7 +440,7 @@ def main():
     achieved = bytes_k / (kms[dom] * 1e-3) / 1e9
     alg_total = 6 * g.nnz + 4 * (M + 1) + 2 * N * K + 4 * M * K
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(names[dom], workload),
             "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
             "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
             "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
