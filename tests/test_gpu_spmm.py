@@ -84,8 +84,8 @@ def test_mfma_and_residual_routes_agree(mfma_tc, mfma_sptc, fill):
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), "routes")
 
 
-@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 8, 10, 12, 14, 16, 18, 20, 24, 30, 36, 40, 66, 98, 100, 130, 200,
-                               256, 260, 520, 1030])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 8, 10, 12, 14, 16, 18, 20, 24, 30, 33, 36, 40, 65, 66, 81, 97, 98, 100,
+                               130, 200, 256, 260, 520, 1030])
 def test_feature_widths(K):
     say("K", K)
     g = graphs.sbm(communities=128, seed=1, val_seed=2)
