@@ -952,6 +952,19 @@ int lanes_for(int K, int vec) {
   return l;
 }
 
+// Narrow loads of a width just past a power of two leave most lanes of a wide group idle: the
+// group width (>= 16 lanes) with the fewest lane slots over all feature passes (ties to fewer
+// passes), taken when it saves at least a fifth of the slots of `lpg` lanes.
+int fewer_lane_slots(int K, int vec, int lpg) {
+  const int slots0 = (K + lpg * vec - 1) / (lpg * vec) * lpg;
+  int best = lpg, best_slots = slots0;
+  for (int l = lpg / 2; l >= 16; l >>= 1) {
+    const int slots = (K + l * vec - 1) / (l * vec) * l;
+    if (slots < best_slots) best = l, best_slots = slots;
+  }
+  return best_slots * 5 <= slots0 * 4 ? best : lpg;
+}
+
 template <int VEC>
 hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
                            float* partial, hipStream_t s, hipEvent_t* ev) {
@@ -960,21 +973,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   // a plan may ask for fewer lanes per group: several feature passes, each gathering a narrower
   // slice of B (smaller working set per pass)
   while (p.feature_lanes > 0 && lpg > p.feature_lanes && lpg > 1) lpg >>= 1;
-  if (p.feature_lanes <= 0 && VEC <= 2) {
-    // narrow loads of a width just past a power of two leave most lanes of a wide group idle:
-    // the group width (>= 16 lanes) with the fewest lane slots over all feature passes (ties to
-    // fewer passes) is taken when it saves at least a fifth of the slots.  Same-box A/B on R-MAT:
-    // K=66 2.25 ms in one pass of 64 lanes -> 1.93 in three of 16, K=130 4.59 -> 3.21, K=65 3.14
-    // -> 2.42, K=81 3.20 -> 2.78, K=33 1.47 -> 1.35; grid+hubs K=66 1.99 -> 2.07, K=33 1.41 ->
-    // 1.46.  K=97 (an eighth fewer slots in seven passes) measured 3.25 -> 3.33 and keeps 64 lanes
-    const int slots0 = (K + lpg * VEC - 1) / (lpg * VEC) * lpg;
-    int best = lpg, best_slots = slots0;
-    for (int l = lpg / 2; l >= 16; l >>= 1) {
-      const int slots = (K + l * VEC - 1) / (l * VEC) * l;
-      if (slots < best_slots) best = l, best_slots = slots;
-    }
-    if (best_slots * 5 <= slots0 * 4) lpg = best;
-  }
+  // (same-box A/B on R-MAT: K=66 2.25 ms in one pass of 64 lanes -> 1.93 in three of 16, K=130
+  // 4.59 -> 3.21, K=65 3.14 -> 2.42, K=81 3.20 -> 2.78, K=33 1.47 -> 1.35; grid+hubs K=66 1.99 ->
+  // 2.07, K=33 1.41 -> 1.46.  K=97, an eighth fewer slots in seven passes: 3.25 -> 3.33)
+  if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
   const int fpp = lpg * VEC;
   const int passes = (K + fpp - 1) / fpp;
   if (p.ntasks > 0) {
@@ -1064,7 +1066,13 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
                             int K, float* out, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
   if (p.ntasks > 0) {
-    const int lpg = lanes_for(K, VEC);
+    int lpg = lanes_for(K, VEC);
+    // fewer lanes than features: the kernel loops over feature chunks per batch (no second walk
+    // of the entries), so narrow loads take the group width with the fewest lane slots (same-box
+    // A/B on R-MAT: K=66 1.49 ms with 64 lanes -> 0.91 with 16, K=82 1.50 -> 0.99, K=130 2.00 ->
+    // 1.72, K=33 1.40 -> 0.73, K=65 1.87 -> 1.20)
+    while (p.feature_lanes > 0 && lpg > p.feature_lanes && lpg > 1) lpg >>= 1;
+    if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb);
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
