@@ -1073,6 +1073,10 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // 1.72, K=33 1.40 -> 0.73, K=65 1.87 -> 1.20)
     while (p.feature_lanes > 0 && lpg > p.feature_lanes && lpg > 1) lpg >>= 1;
     if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
+    // at least 8 lanes, so that a group writes 8 consecutive sums (32 bytes) per store and the
+    // outputs stream; lanes past K add zeros (R-MAT K=4 0.329 -> 0.258 ms, K=2 0.327 -> 0.259,
+    // K=1 0.467 -> 0.260)
+    if (p.feature_lanes <= 0 && lpg < 8) lpg = 8;
     const int gpb = 4 * (64 / lpg);
     dim3 grid((p.ntasks + gpb - 1) / gpb);
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
