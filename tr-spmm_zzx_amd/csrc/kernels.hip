@@ -977,6 +977,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   // 4.59 -> 3.21, K=65 3.14 -> 2.42, K=81 3.20 -> 2.78, K=33 1.47 -> 1.35; grid+hubs K=66 1.99 ->
   // 2.07, K=33 1.41 -> 1.46.  K=97, an eighth fewer slots in seven passes: 3.25 -> 3.33)
   if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
+  // at least 4 lanes, whose column/value loads are shared, also where K < 4 leaves lanes idle
+  // (same-box A/B: R-MAT K=1 0.316 -> 0.183 ms, K=2 0.255 -> 0.201; grid+hubs K=1 0.201 -> 0.122,
+  // K=2 0.237 -> 0.175; 8 lanes at K=3: R-MAT 0.214 -> 0.258)
+  if (p.feature_lanes <= 0 && lpg < 4) lpg = 4;
   const int fpp = lpg * VEC;
   const int passes = (K + fpp - 1) / fpp;
   if (p.ntasks > 0) {
