@@ -1163,7 +1163,10 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
   // loads, R-MAT: K=10 0.438 -> 0.346 ms, K=18 0.776 -> 0.612, K=30 0.828 -> 0.641, K=98 3.245 ->
   // 2.313; SBM K=18 0.295 -> 0.208).  K=12 and 16 stay on 8-byte loads in 4-lane groups (R-MAT
   // K=16 0.318 vs 0.333 ms with 4-byte loads in 8-lane groups)
-  const bool v2 = K > 8 && !(v8 || v4) && K % 2 == 0 && ldb % 2 == 0 && ldc % 2 == 0 &&
+  // K = 6 and 8 too, in groups of 4 lanes (R-MAT K=6 0.297 -> 0.253 ms, K=8 0.283 -> 0.273; SBM,
+  // whose window kernel stages B rows with the same loads, K=6 0.189 -> 0.144, K=8 0.180 ->
+  // 0.145; grid+hubs K=8 0.241 -> 0.245).  K=4 stays on 2-byte loads (R-MAT 0.219 vs 0.233)
+  const bool v2 = (K > 8 || K == 6 || K == 8) && !(v8 || v4) && K % 2 == 0 && ldb % 2 == 0 && ldc % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(B) & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0 &&
                   (partial == nullptr || aligned16(partial));
   if (v2) return launch_spmm_vec<2>(p, B, ldb, K, C, ldc, partial, stream, ev);
