@@ -350,7 +350,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}): this build has no multi-GPU path; "
-              "row windows would shard across GPUs with one all-gather of B (see DESIGN.md)", file=sys.stderr)
+              "row windows would shard across GPUs, with B all-gathered once per SpMM", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

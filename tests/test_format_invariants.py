@@ -1,5 +1,5 @@
-"""Structural invariants of the builder output (SURVEY §8(c) list; rules of
-TR-source/Block/block_online.cpp), checked on synthetic graphs larger than the golden fixtures and
+"""Structural invariants of the builder output (rules of TR-source/Block/block_online.cpp:
+partition of the input, offsets, bit counts, tile counts, packing, atomic flags), checked on synthetic graphs larger than the golden fixtures and
 with varied parameters.  The fixtures pin bit-exactness on their inputs; these pin the array
 relations everywhere else."""
 import numpy as np
