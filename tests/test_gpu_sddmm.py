@@ -136,6 +136,26 @@ def test_sddmm_feature_lanes_option(K, lanes):
     assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
 
 
+@pytest.mark.parametrize("K", [2, 4, 16, 32, 72, 128, 256])
+def test_sddmm_four_entries_per_batch(K):
+    """Plan option sddmm_unroll = 4: batches of 4 entries per lane group (4 sums per
+    reduce-scatter, written with plain stores), on tasks with long and empty rows.  Against the
+    closed form."""
+    print("sddmm unroll4", K, flush=True)
+    g = graphs.grid_hubs(side=64, hubs=2, hub_degree=2000, seed=3, val_seed=4)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.for_sddmm(f, g.m, g.n, sddmm_unroll=4)
+    Xh = graphs.dense_operand(g.m, K, seed=25)
+    Yh = graphs.dense_operand(g.n, K, seed=26)
+    out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda())
+    torch.cuda.synchronize()
+    nnz = int(g.rowptr[g.m])
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[:nnz], Xh, Yh)
+    got = out.cpu().numpy()
+    assert not np.isnan(got).any()
+    assert np.max(np.abs(got - R)) <= 1e-4 * np.sqrt(K) * max(1.0, np.abs(R).max())
+
+
 def test_sddmm_matches_torch_sampled_addmm():
     g = graphs.random_csr(200, 300, 0.05, seed=3)
     plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)
