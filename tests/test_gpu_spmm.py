@@ -177,6 +177,45 @@ def test_rows_beyond_m_are_dropped_like_reference():
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=40), "m<rows")
 
 
+@pytest.mark.parametrize("K", [4, 32, 128])
+def test_streaming_hints_do_not_change_results(K):
+    """Plan option `streaming`: bit 0 streams the column/value loads, bit 1 the C stores (the
+    default; plain below 8 features).  Cache hints only: all four settings bitwise equal, on a
+    plan with MFMA windows, residual tasks and split rows."""
+    say("streaming", K)
+    g = graphs.sbm(communities=200, seed=21, val_seed=22)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, K, seed=7)
+    outs = [run_plan(trspmm.Plan.from_format(f, g.m, g.n, streaming=st, piece_nnz=32), Bh) for st in (0, 1, 2, 3)]
+    check(outs[0], osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"streaming K={K}")
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("K,lanes", [(128, 4), (64, 2), (40, 8), (66, 16)])
+def test_feature_lanes_option(K, lanes):
+    """Plan option feature_lanes: fewer lanes per group than the width needs, the features split
+    into passes over the tasks (grid dimension y).  Against the oracle."""
+    say("lanes", K, lanes)
+    g = graphs.rmat(scale=12, edge_factor=16, seed=14)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, K, seed=8)
+    C = run_plan(trspmm.Plan.from_format(f, g.m, g.n, feature_lanes=lanes, piece_nnz=64), Bh)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"lanes K={K}")
+
+
+@pytest.mark.parametrize("cap", [1, 8])
+def test_window_row_cap_option(cap):
+    """Plan option window_row_cap: windows whose residual rows are longer than the cap hand their
+    tiles back to the residual path.  Against the oracle, with a dense-block graph."""
+    say("cap", cap)
+    g = graphs.sbm(communities=200, seed=23, val_seed=24)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, 64, seed=9)
+    C = run_plan(trspmm.Plan.from_format(f, g.m, g.n, window_row_cap=cap), Bh)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"cap={cap}")
+
+
 @pytest.mark.parametrize("xcd_run", [1, 3, 16, 64])
 @pytest.mark.parametrize("m", [997, 40000])
 def test_xcd_remap_covers_every_work_item(xcd_run, m):
