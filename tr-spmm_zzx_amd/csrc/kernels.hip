@@ -471,12 +471,12 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
 
 // C[row] = sum of a split row's partial slots, in slot order (deterministic), 4 slots in flight.
 template <int VEC, int LPG>
-__global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
-                                                    const float* __restrict__ partial) {
+__device__ __forceinline__ void fixup_narrow(const DevicePlan& P, int block, int K, float* __restrict__ C,
+                                             int64_t ldc, const float* __restrict__ partial) {
   constexpr int GPW = 64 / LPG;
   constexpr int SU = 4;
   const int lane = threadIdx.x & 63;
-  const int id = (blockIdx.x * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
+  const int id = (block * 4 + (threadIdx.x >> 6)) * GPW + lane / LPG;
   if (id >= P.nfixups) return;
   const int f = blockIdx.y * (LPG * VEC) + (lane % LPG) * VEC;
   if (f >= K) return;
@@ -506,14 +506,14 @@ __global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* 
 // Split rows with many slots: one workgroup per row.  Lane group g sums slots g, g + G, ... (in
 // order), then the G group sums are combined by a fixed binary tree in LDS (deterministic).
 template <int VEC, int LPG>
-__global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
-                                                         const float* __restrict__ partial) {
+__device__ __forceinline__ void fixup_wide(const DevicePlan& P, int block, int K, float* __restrict__ C,
+                                           int64_t ldc, const float* __restrict__ partial) {
   constexpr int G = 256 / LPG;
   __shared__ float red[G][LPG * VEC];
   const int g = threadIdx.x / LPG;
   const int li = threadIdx.x % LPG;
   const int f = blockIdx.y * (LPG * VEC) + li * VEC;
-  const Fixup x = P.wfixups[blockIdx.x];
+  const Fixup x = P.wfixups[block];
   float acc[VEC];
   zero_acc(acc);
   if (f < K) {
@@ -537,6 +537,16 @@ __global__ __launch_bounds__(256) void k_spmm_fixup_wide(DevicePlan P, int K, fl
     for (int i = 0; i < VEC; ++i) acc[i] = red[0][li * VEC + i];
     store_vec<VEC>(C + (int64_t)x.row * ldc + f, acc);
   }
+}
+
+// Both kinds of split rows in one launch: blocks [0, nwfixups) take one wide row each, the rest
+// the narrow rows, 4 waves x 64 / LPG lane groups per block (one launch instead of two: the
+// narrow and wide sets write disjoint rows and run side by side).
+template <int VEC, int LPG>
+__global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* __restrict__ C, int64_t ldc,
+                                                    const float* __restrict__ partial) {
+  if ((int)blockIdx.x < P.nwfixups) fixup_wide<VEC, LPG>(P, blockIdx.x, K, C, ldc, partial);
+  else fixup_narrow<VEC, LPG>(P, (int)blockIdx.x - P.nwfixups, K, C, ldc, partial);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1048,18 +1058,12 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 4>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
-  if (p.nfixups > 0) {
+  if (p.nfixups > 0 || p.nwfixups > 0) {
     const int gpb = 4 * (64 / lpg);
-    dim3 grid((p.nfixups + gpb - 1) / gpb, passes);
+    dim3 grid(p.nwfixups + (p.nfixups + gpb - 1) / gpb, passes);
 #define TRS_FIX(L) case L: hipLaunchKernelGGL((k_spmm_fixup<VEC, L>), grid, dim3(256), 0, s, p, K, C, ldc, partial); break;
     switch (lpg) { TRS_FIX(1) TRS_FIX(2) TRS_FIX(4) TRS_FIX(8) TRS_FIX(16) TRS_FIX(32) TRS_FIX(64) }
 #undef TRS_FIX
-  }
-  if (p.nwfixups > 0) {
-    dim3 grid(p.nwfixups, passes);
-#define TRS_WFIX(L) case L: hipLaunchKernelGGL((k_spmm_fixup_wide<VEC, L>), grid, dim3(256), 0, s, p, K, C, ldc, partial); break;
-    switch (lpg) { TRS_WFIX(1) TRS_WFIX(2) TRS_WFIX(4) TRS_WFIX(8) TRS_WFIX(16) TRS_WFIX(32) TRS_WFIX(64) }
-#undef TRS_WFIX
   }
   if (ev) (void)hipEventRecord(ev[3], s);
   return hipGetLastError();
