@@ -1155,8 +1155,9 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
   // wide loads only where they leave at least 4 lanes per group (whose column/value loads are
   // shared): with K <= 8 one or two lanes would stream a task alone (R-MAT K=8: 0.545 ms with one
   // 16-byte load per entry, 0.348 with two lanes of 8-byte loads, 0.283 with eight lanes of 2-byte
-  // loads; K=4 0.515 -> 0.220), and K=16 runs best as 4 lanes of 8-byte loads (R-MAT 0.436 ms with
-  // 2 lanes of 16-byte loads, 0.324; grid+hubs 0.368 -> 0.307)
+  // loads, 0.273 with four lanes of 4-byte loads (below); K=4 0.515 -> 0.220), and K=16 runs best
+  // as 4 lanes of 8-byte loads (R-MAT 0.436 ms with 2 lanes of 16-byte loads, 0.324; grid+hubs
+  // 0.368 -> 0.307)
   const bool v8 = K > 16 && K % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned16(B) && aligned16(C) &&
                   (partial == nullptr || aligned16(partial));
   // 8-byte loads when rows are only 8-byte aligned (K % 4 == 0): R-MAT K=100 3.22 ms with 2-byte
