@@ -2,12 +2,14 @@
 
     python bench.py [--steps K] [--warmup W] [--config 2|3|5|4] [--no-cpu-baseline]
                     [--scramble SEED] [--reorder tca]
-    python bench.py --ceiling-probe      # practical copy / random-gather rates of the box
 
 A step is one SpMM C = A B over the whole graph with A (device plan) and B already resident in
 HBM.  Prints one JSON line with GFLOP/s (2 nnz K / t), the roofline object of the dominant kernel
-(algorithmic bytes per launch / its HIP-event duration on the launch stream), and the CPU baseline
-(torch.sparse.mm CSR fp32 on the host cores, the oracle's CPU SpMM) timed on a bounded sample.
+(compulsory bytes of the share it computes -- A's entries and row pointers, B once, C once -- per
+launch / its HIP-event duration on the launch stream; the bytes its data layout adds on top, task
+descriptors, partial slots and dense tile padding, are reported apart as `impl_bytes`), and the
+CPU baseline (torch.sparse.mm CSR fp32 on the host cores, the oracle's CPU SpMM) timed on a bounded
+sample.
 """
 from __future__ import annotations
 
@@ -15,7 +17,6 @@ import argparse
 import ctypes
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -230,21 +231,18 @@ def bench_sddmm(args, workload, g, K):
     names = ["sddmm_tasks", "sddmm_mfma"]
     dom = int(np.argmax(kms))
     M, N = g.m, g.n
-    if dom == 0:   # column ids, output index when tiles exist, outputs, row pointers, tasks, X and Y once
+    # compulsory bytes (column id + fp32 output per entry, row pointers, X and Y once) of the share
+    # the dominant kernel computes; the layout's extra bytes are reported apart
+    if dom == 0:
         nr = st["csr_nnz"]
-        bytes_k = (4 + 4 + (4 if st["mfma_tiles"] else 0)) * nr + 4 * (M + 1) + 16 * st["tasks"] \
-            + 2 * M * K + 2 * N * K
-    else:          # per tile: 16 column ids + 256 output slots; X and Y rows once; outputs
-        bytes_k = st["mfma_tiles"] * (64 + 1024) + 4 * st["mfma_nnz"] + 2 * M * K + 2 * N * K
-    achieved = bytes_k / (kms[dom] * 1e-3) / 1e9
-    alg_total = 8 * g.nnz + 4 * (M + 1) + 2 * M * K + 2 * N * K
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(names[dom], workload),
-            "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
-            "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
-            "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    if roof["traffic"]:
-        roof["traffic_frac"] = round(roof["traffic"] / (kms[dom] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        bytes_k = 8 * nr + 4 * (M + 1) + 2 * M * K + 2 * N * K
+        impl = (4 * nr if st["mfma_tiles"] else 0) + 16 * st["tasks"]   # output index, task descriptors
+    else:
+        bytes_k = 8 * st["mfma_nnz"] + 2 * M * K + 2 * N * K
+        impl = st["mfma_tiles"] * (64 + 1024) - 4 * st["mfma_nnz"]      # column ids, dense output slots
+    roof = roofline(bytes_k, impl, kms[dom], names[dom], names, kms, workload)
+    roof["whole_step_frac"] = round((8 * g.nnz + 4 * (M + 1) + 2 * M * K + 2 * N * K) / (ms_step * 1e-3) / 1e9
+                                    / HBM_PEAK_GBS, 4)
     outj = {"metric": f"SDDMM GFLOP/s (2·nnz·K) + % HBM roofline, R-MAT 2^20 pattern K={K} fp16", "value": round(gflops, 2),
             "unit": "GFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
@@ -258,73 +256,31 @@ def bench_sddmm(args, workload, g, K):
     print(json.dumps(outj), flush=True)
 
 
-def ceiling_probe():
-    """Reference points for the roofline fractions: streaming read / write / copy kernels
-    (./bench_stream_probe, built by __graft_entry__.build(), run first in a child process of its
-    own), a 2 GiB torch device copy, and uniform-random row gathers through the residual SpMM
-    kernel (1M rows x d random columns, no column reuse) for several operand sizes and row widths.
-    One JSON line per probe."""
-    probe = os.path.join(ROOT, "bench_stream_probe")
-    if not os.path.exists(probe):
-        sys.exit(f"{probe} is not built: run __graft_entry__.build()")
-    r = subprocess.run([probe], capture_output=True, text=True, timeout=300)
-    sys.stdout.write(r.stdout)
-    sys.stdout.flush()
-    if r.returncode != 0:
-        sys.exit(f"bench_stream_probe failed ({r.returncode}): {r.stderr[-500:]}")
-    import numpy as np
-    import torch
-    import trspmm
-    from trspmm import graphs
-
-    def timeit(fn, n=10):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(n):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n
-
-    src = torch.ones(512 << 20, dtype=torch.float32, device="cuda")   # 2 GiB
-    dst = torch.empty_like(src)
-    ms = timeit(lambda: dst.copy_(src))
-    print(json.dumps({"probe": "device copy 2 GiB fp32", "ms": round(ms, 4),
-                      "TB/s read+write": round(4 * 2**30 / ms / 1e9, 3)}), flush=True)
-    del src, dst
-    rng = np.random.default_rng(0)
-    m = 1 << 20
-    for n, K, d in [(8 << 20, 128, 32), (2 << 20, 128, 32), (1 << 20, 128, 32), (8 << 20, 64, 32),
-                    (1 << 20, 64, 32), (8 << 20, 32, 32), (1 << 20, 32, 32), (4 << 20, 32, 32)]:
-        keys = np.unique(rng.integers(0, m * n, size=m * d, dtype=np.int64))
-        rowptr, col = graphs.csr_from_keys(keys, m, n, m)
-        g = graphs.Graph("probe", m, n, rowptr, col, np.ones(len(keys), np.float32))
-        f = trspmm.build_format(g.rowptr, g.col, g.val, skip_tc=True)
-        plan = trspmm.Plan.from_format(f, m, n, mfma_tc=False, mfma_sptc=False)
-        B = torch.ones(n, K, dtype=torch.float16, device="cuda")
-        C = torch.empty(m, K, device="cuda")
-        ms = timeit(lambda: plan.spmm(B, out=C))
-        gathered = len(keys) * K * 2
-        print(json.dumps({"probe": f"random row gather: B {n >> 20}M x {K} fp16 ({n * K * 2 / 1e6:.0f} MB), "
-                                   f"{len(keys) / m:.1f} random columns per row", "ms": round(ms, 4),
-                          "gathered TB/s": round(gathered / ms / 1e9, 3),
-                          "C write TB/s": round(m * K * 4 / ms / 1e9, 3)}), flush=True)
-        del plan, B, C, f
-
-
 def load_traffic(kernel: str, workload: str):
-    """Measured HBM bytes per launch of `kernel` on `workload` (FETCH_SIZE and WRITE_SIZE runs,
-    scaled by a device copy of known size), or None where no counter run is recorded."""
+    """HBM bytes per launch of `kernel` on `workload` measured in an earlier rocprofv3 --pmc run
+    (FETCH_SIZE and WRITE_SIZE, scaled by a device copy of known size) and the file they come from,
+    or (None, None) where no counter run is recorded.  Never this run's measurement."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_pmc.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         d = json.load(f)
-    return d.get("hbm_bytes_per_launch")
+    src = f"profiles/{os.path.basename(path)[:-5]}.md ({d.get('measured', 'earlier run')}; a separate " \
+          "rocprofv3 --pmc run, not this one)"
+    return d.get("hbm_bytes_per_launch"), src
+
+
+def roofline(bytes_k: int, impl: int, ms: float, kernel: str, names, kms, workload: str) -> dict:
+    """Roofline object of the dominant kernel: `achieved` = its compulsory bytes per launch over
+    its HIP-event duration, `impl_bytes` = what its data layout reads or writes on top (not counted
+    as achieved), `traffic` = measured HBM bytes per launch from the stored counter run named in
+    `traffic_source` (null where none is recorded)."""
+    achieved = bytes_k / (ms * 1e-3) / 1e9
+    traffic, source = load_traffic(kernel, workload)
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+            "alg_bytes": int(bytes_k), "impl_bytes": int(impl), "kernel": kernel, "kernel_ms": round(ms, 4),
+            "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)}}
 
 
 def main():
@@ -343,8 +299,6 @@ def main():
     ap.add_argument("--reorder", choices=["none", "tca", "tca-aligned"], default="none",
                     help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
                          "tca-aligned keeps clusters inside 16-row windows")
-    ap.add_argument("--ceiling-probe", action="store_true",
-                    help="print the box's copy and random-gather rates (one JSON line each) and exit")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -360,9 +314,6 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.ceiling_probe:
-        ceiling_probe()
-        return
     t0 = time.time()
     workload, g, K, bseed = make_workload(args.config)
     if args.k:
@@ -428,24 +379,22 @@ def main():
     M, N = g.m, g.n
     rows_w = min(M, 16 * st["mfma_windows"])
     nnz_w = st["window_csr_nnz"]
-    if dom == 0:    # residual tasks: its entries, row pointers, one pass over B, its output rows
+    # compulsory bytes (fp16 value + int32 column per entry, int32 row pointers, B once, C once) of
+    # the share the dominant kernel computes; bytes its data layout adds are reported apart
+    if dom == 0:    # residual tasks: entries and rows outside MFMA windows
         nnz_k = st["csr_nnz"] - nnz_w
         rows_k = M - rows_w
-        bytes_k = 6 * nnz_k + 4 * (rows_k + 1) + 16 * st["tasks"] + 2 * N * K + 4 * rows_k * K \
-            + 4 * st["partial_slots"] * K
-    elif dom == 1:  # MFMA windows: dense 16x16 fp16 tiles + 16 column ids, window residual, B once, C
-        bytes_k = st["mfma_tiles"] * (512 + 64) + 6 * nnz_w + 2 * N * K + 4 * rows_w * K
-    else:           # fixup: read partial slots, write split rows
-        bytes_k = 4 * st["partial_slots"] * K + 4 * st["split_rows"] * K
-    achieved = bytes_k / (kms[dom] * 1e-3) / 1e9
-    alg_total = 6 * g.nnz + 4 * (M + 1) + 2 * N * K + 4 * M * K
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(names[dom], workload),
-            "kernel": names[dom], "kernel_ms": round(kms[dom], 4),
-            "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)},
-            "whole_step_frac": round(alg_total / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    if roof["traffic"]:   # measured HBM bytes of the same kernel over its live time, against the peak
-        roof["traffic_frac"] = round(roof["traffic"] / (kms[dom] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        bytes_k = 6 * nnz_k + 4 * (rows_k + 1) + 2 * N * K + 4 * rows_k * K
+        impl = 16 * st["tasks"] + 4 * K * st["partial_slots"]          # task descriptors, partial slots
+    elif dom == 1:  # MFMA windows: tile entries + the windows' residual entries, their rows
+        bytes_k = 6 * (st["mfma_nnz"] + nnz_w) + 4 * (rows_w + 1) + 2 * N * K + 4 * rows_w * K
+        impl = st["mfma_tiles"] * (512 + 64) - 6 * st["mfma_nnz"]      # dense 16x16 tiles + column ids
+    else:           # fixup: the split rows it writes
+        bytes_k = 4 * st["split_rows"] * K
+        impl = 4 * K * st["partial_slots"]
+    roof = roofline(bytes_k, impl, kms[dom], names[dom], names, kms, workload)
+    roof["whole_step_frac"] = round((6 * g.nnz + 4 * (M + 1) + 2 * N * K + 4 * M * K) / (ms_step * 1e-3) / 1e9
+                                    / HBM_PEAK_GBS, 4)
     log(f"[bench] kernels {kms}, roofline {roof}")
     ms_cold = cold_ms(lambda: plan.spmm(B, out=C, workspace=ws), max(5, min(args.steps, 10)))
     log(f"[bench] cold (L2 + MALL flushed) {ms_cold:.4f} ms/step")

@@ -7,9 +7,18 @@
 Each fixture holds `rowptr`, `col`, `val`, the builder parameters and `out_<slot>` for slots 0..28
 (slot 29, the build time, is not deterministic and is not stored).  The reference prints per-window
 diagnostics on stdout; they are discarded.
+
+    python tests/golden/make_golden.py digests
+
+writes tests/golden/builder_digests.json instead: for the full-size BASELINE configurations 1
+(Erdos-Renyi 4096) and 3 (SBM, 1M rows, 17.0M entries) and for R-MAT 2^18 (7.6M entries), too large
+to commit as arrays, the SHA-256 of the input CSR and of each of the reference's 29 output arrays
+(dtype, shape and bytes; see `array_digest`).  About two minutes of reference time in all.
 """
 from __future__ import annotations
 
+import hashlib
+import json
 import os
 import sys
 
@@ -81,10 +90,49 @@ def run_reference(mod, rowptr, col, val, p):
     return [t.numpy().copy() for t in out]
 
 
+def array_digest(a) -> str:
+    """SHA-256 of an array's dtype, shape and little-endian bytes (C order)."""
+    a = np.ascontiguousarray(a)
+    h = hashlib.sha256()
+    h.update(f"{a.dtype.str}|{tuple(int(x) for x in a.shape)}|".encode())
+    h.update(a.tobytes())
+    return h.hexdigest()
+
+
+def csr_digest(rowptr, col, val) -> str:
+    return hashlib.sha256("|".join(array_digest(a) for a in (rowptr, col, val)).encode()).hexdigest()
+
+
+def digest_cases():
+    """(name, graph generator) of the full-size cases; the test regenerates the same graphs."""
+    return [("er4096_config1", lambda: graphs.erdos_renyi_gcn()),
+            ("sbm1m_config3", lambda: graphs.sbm()),
+            ("rmat18", lambda: graphs.rmat(scale=18, edge_factor=16, seed=31))]
+
+
+def write_digests(mod):
+    import time
+    out = {}
+    for name, gen in digest_cases():
+        g = gen()
+        t0 = time.time()
+        arrs = run_reference(mod, g.rowptr, g.col, g.val, DEFAULT)
+        out[name] = {"m": g.m, "nnz": g.nnz, "input": csr_digest(g.rowptr, g.col, g.val),
+                     "slots": [array_digest(arrs[i]) for i in range(29)],
+                     "shapes": [list(arrs[i].shape) for i in range(29)]}
+        print(name, "nnz", g.nnz, f"reference {time.time() - t0:.1f}s", flush=True)
+    with open(os.path.join(HERE, "builder_digests.json"), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+
+
 def main():
     mod = ob.reference_module()
     if mod is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref, needs /root/reference)")
+    if sys.argv[1:] == ["digests"]:
+        write_digests(mod)
+        return
     for name, rowptr, col, val, over, env in cases():
         p = dict(DEFAULT, **over)
         old = {k: os.environ.get(k) for k in env}

@@ -67,3 +67,21 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.trs_spmm_f16(None, None, 0, 1, None, 0, None, 0, None) == 1
     assert lib.trs_spmm_workspace_bytes(None, 8) == 0
     assert lib.trs_format_slot(None, 0, None, None) == 1
+
+
+def test_plan_from_csr_refuses_short_arrays():
+    """Plan.from_csr checks the array lengths the C entry point reads (rowptr[0..m], col / val up
+    to rowptr[m]) before calling it, so no host read goes out of bounds; no GPU needed."""
+    import numpy as np
+    import trspmm
+    rowptr = np.array([0, 2, 3, 5], np.int32)
+    col = np.array([0, 1, 1, 0, 2], np.int32)
+    val = np.ones(5, np.float16)
+    with pytest.raises(ValueError, match="rowptr"):
+        trspmm.Plan.from_csr(rowptr[:-1], col, val, 3, 3)          # shorter than m + 1
+    with pytest.raises(ValueError, match="rowptr"):
+        trspmm.Plan.from_csr(rowptr, col, val, 2, 3)               # longer than m + 1
+    with pytest.raises(ValueError, match="col and val"):
+        trspmm.Plan.from_csr(rowptr, col[:4], val, 3, 3)
+    with pytest.raises(ValueError, match="col and val"):
+        trspmm.Plan.from_csr(rowptr, col, val[:3], 3, 3)

@@ -31,11 +31,12 @@ class ParallelArrays(ctypes.Structure):
            ("m", I32), ("n", I32)])
 
 
-def _fixture():
-    g = graphs.sbm(communities=64, seed=3, val_seed=4)   # TC blocks, 2:4 groups and short residual parts
+def _fixture(g=None):
+    default = g is None
+    g = g or graphs.sbm(communities=64, seed=3, val_seed=4)   # TC blocks, 2:4 groups, short residual parts
     f = trspmm.build_format(g.rowptr, g.col, g.val)
     arrs = [np.ascontiguousarray(a) for a in f.arrays()]
-    assert arrs[1].size > 1 and arrs[17].shape[0] > 0 and arrs[15].size > 0
+    assert not default or (arrs[1].size > 1 and arrs[17].shape[0] > 0 and arrs[15].size > 0)
     for i in (3, 11, 16):   # t / c values reach the operator as fp16
         arrs[i] = arrs[i].astype(np.float16).view(np.uint16)
     return g, arrs
@@ -111,6 +112,7 @@ CASES = [
     ("2:4 position outside 0..3", lambda a: a[20].__setitem__((0, 0, 0), 7), (1,)),
     ("s_offsets out of range", lambda a: a[22].__setitem__(-1, a[22][-1] + 9), (1,)),
     ("tile offsets out of range", lambda a: a[28].__setitem__(-1, a[28][-1] + 9), (1,)),
+    ("short residual values shorter than columns", lambda a: a.__setitem__(16, a[16][:-1].copy()), (1,)),
 ]
 
 
@@ -128,3 +130,20 @@ def test_malformed_arrays_are_refused_before_upload(what, mutate, codes, packed)
     if what == "tile offsets out of range" and not packed:
         pytest.skip("the group plan reads s_offsets, not s_window_tile_offset")
     assert rc in codes, (what, rc, msg)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_long_residual_values_shorter_than_columns_are_refused(packed):
+    # the SBM fixture has no long residual part: give it one of four entries, with a value short
+    g, arrs = _fixture()
+    arrs = [a.copy() for a in arrs]
+    arrs[7] = np.array([0, 4], np.int32)                    # c_row_offsets
+    arrs[8] = np.array([0], np.int32)                       # c_row
+    arrs[9] = np.array([0], np.int32)                       # c_atomic
+    arrs[10] = np.array([0, 1, 2, 3], np.int32)             # c_column
+    arrs[11] = np.ones(4, np.float16).view(np.uint16)       # c_value
+    rc, msg = _create(arrs, g, packed)
+    assert rc in (0, 3), msg                                # well-formed so far
+    arrs[11] = arrs[11][:3].copy()
+    rc, msg = _create(arrs, g, packed)
+    assert rc == 1 and "value" in msg, (rc, msg)

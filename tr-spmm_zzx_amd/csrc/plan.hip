@@ -863,6 +863,9 @@ int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_option
   }
   if (a->n_c_row_offsets < a->n_c_row + 1 || a->n_cs_row_offsets < a->n_cs_row + 1)
     return report(fail(TRS_EINVAL, "residual offsets shorter than part lists"));
+  // lower_residual reads a value for every column entry a part covers
+  if (a->n_c_value < a->n_c_column || a->n_cs_value < a->n_cs_column)
+    return report(fail(TRS_EINVAL, "residual value arrays shorter than their column arrays"));
   Lowering L;
   L.m = a->m;
   L.n = a->n;

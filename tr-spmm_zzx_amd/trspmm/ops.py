@@ -196,9 +196,19 @@ def _options(mfma_tc: bool, mfma_sptc: bool, sptc_min_fill: float, task_nnz: int
     return o
 
 
+def _launch_stream(stream):
+    return stream if stream is not None else torch.cuda.current_stream()
+
+
 def _stream_ptr(stream) -> int:
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return int(s.cuda_stream)
+    return int(_launch_stream(stream).cuda_stream)
+
+
+def _on_current_device(name: str, t: torch.Tensor) -> None:
+    """Plans are bound to the device they were created on, which the C ABI requires to be the
+    current one (TRS_EDEVICE otherwise); operands on another GPU are refused here."""
+    if t.device.index != torch.cuda.current_device():
+        raise ValueError(f"{name} is on {t.device}, not on the current device cuda:{torch.cuda.current_device()}")
 
 
 class Plan:
@@ -256,6 +266,13 @@ class Plan:
         rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
         col = np.ascontiguousarray(col, dtype=np.int32)
         val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
+        # trs_plan_create_csr reads rowptr[0..m] and col / val up to rowptr[m]: refuse short arrays here
+        if m < 0 or rowptr.ndim != 1 or rowptr.shape[0] != m + 1:
+            raise ValueError(f"rowptr must hold m + 1 = {m + 1} entries (got {rowptr.shape})")
+        nnz = int(rowptr[-1])
+        if col.shape[0] < nnz or val.shape[0] < nnz:
+            raise ValueError(f"col and val must hold at least rowptr[-1] = {nnz} entries "
+                             f"(got {col.shape[0]} and {val.shape[0]})")
         o = _options(False, False, 1.0, task_nnz, piece_nnz=piece_nnz, feature_lanes=feature_lanes,
                      streaming=streaming, xcd_run=xcd_run, stage=stage, occupancy=occupancy)
         h = ctypes.c_void_p()
@@ -277,37 +294,53 @@ class Plan:
 
     def spmm(self, B: torch.Tensor, out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
              stream=None) -> torch.Tensor:
-        """C = A B for B [n, K] fp16 on the GPU; returns float32 [m, K]."""
+        """C = A B for B [n, K] fp16 on the GPU; returns float32 [m, K].  Temporaries (a defaulted
+        ``out`` or workspace) are allocated on the launch stream, so the caching allocator does not
+        hand them to other work while the kernels on ``stream`` still use them."""
         st = self.stats()
         if not (B.is_cuda and B.dtype == torch.float16 and B.dim() == 2 and B.shape[0] == st["n"]):
             raise ValueError(f"B must be a CUDA fp16 tensor of shape [{st['n']}, K]")
+        _on_current_device("B", B)
         if B.stride(1) != 1:
             B = B.contiguous()
         K = B.shape[1]
-        if out is None:
-            out = torch.empty((st["m"], K), dtype=torch.float32, device=B.device)
+        need = self.workspace_bytes(K)
+        with torch.cuda.stream(_launch_stream(stream)):
+            if out is None:
+                out = torch.empty((st["m"], K), dtype=torch.float32, device=B.device)
+            if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+                workspace = torch.empty(need, dtype=torch.uint8, device=B.device)
         if not (out.is_cuda and out.dtype == torch.float32 and tuple(out.shape) == (st["m"], K) and out.stride(1) == 1):
             raise ValueError("out must be a CUDA float32 tensor [m, K] with unit column stride")
-        need = self.workspace_bytes(K)
-        if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-            workspace = torch.empty(need, dtype=torch.uint8, device=B.device)
+        _on_current_device("out", out)
+        if need:
+            if not (workspace.is_cuda and workspace.is_contiguous()):
+                raise ValueError("workspace must be a contiguous CUDA tensor")
+            _on_current_device("workspace", workspace)
         ws_ptr = workspace.data_ptr() if need else 0
         nat.check(nat.lib().trs_spmm_f16(self._h, B.data_ptr(), B.stride(0), K, out.data_ptr(), out.stride(0),
                                          ws_ptr, need, _stream_ptr(stream)), "trs_spmm_f16")
         return out
 
     def sddmm(self, X: torch.Tensor, Y: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-        """out[e] = X[row_e] . Y[col_e] for every stored entry (CSR order); float32 [nnz]."""
+        """out[e] = X[row_e] . Y[col_e] for every stored entry (CSR order); float32 [nnz].  A given
+        ``out`` must be a contiguous float32 CUDA tensor of at least ``stats()['nnz']`` elements."""
         st = self.stats()
         for name, t, rows in (("X", X, st["m"]), ("Y", Y, st["n"])):
             if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 2 and t.shape[0] == rows):
                 raise ValueError(f"{name} must be a CUDA fp16 tensor with {rows} rows")
+            _on_current_device(name, t)
         if X.shape[1] != Y.shape[1]:
             raise ValueError("X and Y need the same feature width")
         X = X if X.stride(1) == 1 else X.contiguous()
         Y = Y if Y.stride(1) == 1 else Y.contiguous()
         if out is None:
-            out = torch.empty(st["nnz"], dtype=torch.float32, device=X.device)
+            with torch.cuda.stream(_launch_stream(stream)):
+                out = torch.empty(st["nnz"], dtype=torch.float32, device=X.device)
+        if not (isinstance(out, torch.Tensor) and out.is_cuda and out.dtype == torch.float32 and out.is_contiguous()
+                and out.numel() >= st["nnz"]):
+            raise ValueError(f"out must be a contiguous CUDA float32 tensor of at least {st['nnz']} elements")
+        _on_current_device("out", out)
         nat.check(nat.lib().trs_sddmm_f16(self._h, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), X.shape[1],
                                           out.data_ptr(), _stream_ptr(stream)), "trs_sddmm_f16")
         return out
