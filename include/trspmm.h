@@ -276,6 +276,17 @@ int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K);
 int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
+/* trs_spmm_f16 without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  The partial slots come from a static device array of TRS_NOALLOC_SCRATCH_BYTES,
+ * which every GPU the library runs on holds until the process ends; the call allocates nothing.
+ * Plans whose trs_spmm_workspace_bytes(p, K) exceeds that size are refused with TRS_EINVAL.  All
+ * calls on one GPU share its array: calls that overlap on one GPU race (serialise them).  Same
+ * kernels and arguments as trs_spmm_f16, so the output is bitwise equal to it. */
+#define TRS_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)
+int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
+                         void* stream);
+
 /* out[e] = sum_k X[row_e, k] * Y[col_e, k] for every stored entry e of the plan (order: see the
  * plan constructor).  X [m, K], Y [n, K] fp16; out float32 [nnz].  Only SDDMM plans
  * (trs_plan_create_sddmm, trs_plan_create_csr) are accepted.  ldy < 2^31 (TRS_ERANGE otherwise).

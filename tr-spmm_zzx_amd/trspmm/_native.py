@@ -82,6 +82,7 @@ PROTOTYPES = {
     "trs_plan_free": (None, [c_p]),
     "trs_spmm_workspace_bytes": (c_i64, [c_p, c_i32]),
     "trs_spmm_f16": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p]),
+    "trs_spmm_f16_noalloc": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p]),
     "trs_sddmm_f16": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p]),
     "trs_spmm_f16_timed": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_i32, c_i32,
                                    ctypes.POINTER(c_f32)]),
