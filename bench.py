@@ -200,7 +200,7 @@ def bench_sddmm(args, workload, g, K):
     from trspmm import _native as nat, graphs
     t0 = time.time()
     fmt = trspmm.build_format(g.rowptr, g.col, g.val)
-    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n)
+    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split)
     st = plan.stats()
     del fmt
     log(f"[bench] sddmm plan {st} ({time.time() - t0:.1f}s)")
@@ -299,6 +299,9 @@ def main():
     ap.add_argument("--reorder", choices=["none", "tca", "tca-aligned"], default="none",
                     help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
                          "tca-aligned keeps clusters inside 16-row windows")
+    ap.add_argument("--xcd-split", type=int, default=None,
+                    help="plan option xcd_split (rows of >= N residual entries cut by XCD column ranges; "
+                         "-1 off; default: the library's)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -336,7 +339,7 @@ def main():
     log(f"[bench] format built in {fmt.elapsed:.2f}s")
     pre["build_s"] = round(fmt.elapsed, 3)
     t1 = time.time()
-    plan = trspmm.Plan.from_format(fmt, g.m, g.n)
+    plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split)
     pre["plan_s"] = round(time.time() - t1, 3)
     if "reorder_s" in pre:
         pre["reorder_s"] = round(pre["reorder_s"], 3)

@@ -181,6 +181,12 @@ typedef struct trs_plan_options {
                              outside are clamped): fewer concurrent tasks keep fewer gathered rows
                              in flight.  0 = automatic (2 for K <= 64, uncapped above), -1 =
                              uncapped (as many as registers and LDS allow) */
+  int32_t xcd_split;      /* XCD column split: the columns are divided among the 8 XCDs (hashed for
+                             SpMM, contiguous ranges for SDDMM) and residual rows with at least this
+                             many entries are cut into one sub-row per XCD, run by that XCD's
+                             workgroups (workgroup i runs on XCD i mod 8), so each XCD's L2 holds B
+                             rows of an eighth of the columns; an SpMM sub-row costs a partial slot.
+                             0 = automatic (SpMM 256, SDDMM off), -1 = off */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);
@@ -283,7 +289,7 @@ int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, f
  * Plans whose trs_spmm_workspace_bytes(p, K) exceeds that size are refused with TRS_EINVAL.  All
  * calls on one GPU share its array: calls that overlap on one GPU race (serialise them).  Same
  * kernels and arguments as trs_spmm_f16, so the output is bitwise equal to it. */
-#define TRS_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)
+#define TRS_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
 int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
                          void* stream);
 

@@ -243,3 +243,21 @@ def test_sddmm_nonfinite_Y_reaches_only_entries_that_use_it():
     Yh[hub, 5] = np.float16(np.nan)
     out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()).cpu().numpy()
     assert np.array_equal(~np.isfinite(out), g.col[: g.nnz] == hub)
+
+
+def test_sddmm_xcd_column_split_is_bitwise_equal():
+    """The XCD column split only reorders the residual tasks (pieces of long rows by column range);
+    every output is the same dot product, bitwise."""
+    print("sddmm xcd split", flush=True)
+    g = graphs.rmat(scale=13, edge_factor=16, seed=8)
+    Xh = graphs.dense_operand(g.m, 128, seed=3)
+    Yh = graphs.dense_operand(g.n, 128, seed=4)
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    outs = []
+    for xs in (-1, 8, 64):
+        plan = trspmm.Plan.from_csr(g.rowptr, g.col, g.val.astype(np.float16), g.m, g.n, xcd_split=xs)
+        outs.append(plan.sddmm(X, Y))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    assert np.max(np.abs(outs[1].cpu().numpy() - R)) <= (1e-5 * np.sqrt(128) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))

@@ -281,7 +281,7 @@ def test_staged_and_unstaged_streams_agree(K):
     f = trspmm.build_format(rowptr, cols, val, skip_tc=True)
     Bh = dense_B(n, K, seed=5)
     R = osp.csr_spmm(rowptr, cols, val, Bh, m=m)
-    opts = dict(mfma_tc=False, mfma_sptc=False, task_nnz=128)
+    opts = dict(mfma_tc=False, mfma_sptc=False, task_nnz=128, xcd_split=-1)
     staged = trspmm.Plan.from_format(f, m, n, **opts)
     whole = trspmm.Plan.from_format(f, m, n, piece_nnz=300, **opts)
     assert staged.stats()["split_rows"] == 1 and whole.stats()["split_rows"] == 0
@@ -355,3 +355,25 @@ def test_nonfinite_B_reaches_only_rows_that_use_it(K):
         assert np.array_equal(bad[:, K - 1], uses_hub), "NaN column"
         assert np.array_equal(bad[:, 0], uses_lone), "Inf column"
         assert not bad[:, 1:K - 1].any(), "non-finite values leaked into other features"
+
+
+@pytest.mark.parametrize("K", [32, 128])
+def test_xcd_column_split_matches_oracle_and_unsplit_rows(K):
+    """Rows of >= xcd_split residual entries cut by 8 column ranges (one queue per XCD): against
+    the oracle, deterministic from call to call, and every row left whole bitwise equal to the
+    plan without the split (same entries, same order)."""
+    say("xcd split", K)
+    g = graphs.rmat(scale=14, edge_factor=16, seed=12)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Bh = dense_B(g.n, K, seed=13)
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m)
+    split = trspmm.Plan.from_format(f, g.m, g.n, xcd_split=48)
+    whole = trspmm.Plan.from_format(f, g.m, g.n, xcd_split=-1)
+    assert split.stats()["split_rows"] > whole.stats()["split_rows"]
+    C1 = run_plan(split, Bh)
+    C2 = run_plan(whole, Bh)
+    check(C1, R, f"xcd split K={K}")
+    assert np.array_equal(C1, run_plan(split, Bh))
+    deg = np.diff(g.rowptr[: g.m + 1])
+    keep = deg < 48
+    assert keep.sum() > g.m // 2 and np.array_equal(C1[keep], C2[keep])

@@ -149,6 +149,30 @@ __device__ __forceinline__ int xcd_remap(int i, int n, int run) {
   return (j / run) * span + x * run + (j % run);
 }
 
+// Residual task of lane group `grp` of wave `wave` (GPW lane groups per wave, 4 waves per
+// workgroup).  With per-XCD queues, workgroup i runs on XCD i mod kXcds and takes its tasks, in
+// order, from that XCD's queue; otherwise the tasks form one list spread by xcd_remap.
+__device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int grp, int gpw, bool& valid) {
+  if (P.xcd_queues) {
+    const int x = (int)(blockIdx.x % kXcds), k = (int)(blockIdx.x / kXcds);
+    const int id = P.xq[x] + (k * 4 + wave) * gpw + grp;
+    valid = id < P.xq[x + 1];
+    return id;
+  }
+  const int id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + wave) * gpw + grp;
+  valid = id < P.ntasks;
+  return id;
+}
+
+// Workgroups of 4 waves x gpw lane groups that cover the plan's residual tasks.
+inline int residual_grid(const DevicePlan& P, int gpw) {
+  const int gpb = 4 * gpw;
+  if (!P.xcd_queues) return (P.ntasks + gpb - 1) / gpb;
+  int most = 0;
+  for (int x = 0; x < kXcds; ++x) most = std::max(most, (P.xq[x + 1] - P.xq[x] + gpb - 1) / gpb);
+  return most * kXcds;
+}
+
 // Row pointers rowptr[row_begin .. row_end] of a multi-row task into the lane group's LDS slice:
 // all loads are issued before the first store (indices clamped to the task's last pointer), so
 // the preload costs one memory round trip instead of one per pointer each lane handles.
@@ -397,9 +421,8 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
   const int li = lane % LPG;
-  const int wg = xcd_remap(blockIdx.x, gridDim.x, P.xcd_run);
-  const int task_id = (wg * 4 + wave) * GPW + grp;
-  const bool valid = task_id < P.ntasks;
+  bool valid;
+  const int task_id = residual_task(P, wave, grp, GPW, valid);
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   const int32_t* __restrict__ col = P.col;
   const uint16_t* __restrict__ val = P.val;
@@ -490,7 +513,7 @@ __device__ __forceinline__ void fixup_narrow(const DevicePlan& P, int block, int
 #pragma unroll
       for (int i = 0; i < VEC; ++i) v[u][i] = 0.f;
       if (s + u < x.slots) {
-        const float* src = partial + (int64_t)(x.slot_begin + s + u) * K + f;
+        const float* src = partial + (int64_t)P.slot_list[x.slot_begin + s + u] * K + f;
 #pragma unroll
         for (int i = 0; i < VEC; ++i) v[u][i] = src[i];
       }
@@ -518,7 +541,7 @@ __device__ __forceinline__ void fixup_wide(const DevicePlan& P, int block, int K
   zero_acc(acc);
   if (f < K) {
     for (int s = g; s < x.slots; s += G) {
-      const float* src = partial + (int64_t)(x.slot_begin + s) * K + f;
+      const float* src = partial + (int64_t)P.slot_list[x.slot_begin + s] * K + f;
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[i] += src[i];
     }
@@ -727,8 +750,8 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
   const int li = lane % LPG;
-  const int task_id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + wave) * GPW + grp;
-  const bool valid = task_id < P.ntasks;
+  bool valid;
+  const int task_id = residual_task(P, wave, grp, GPW, valid);
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   const bool piece = t.row_end < 0;
   int* rp = s_rp[wave][grp];
@@ -795,6 +818,9 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       }
       rr[i] = t.row_begin + r;
     }
+    int dsub[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) dsub[i] = P.sub_delta ? P.sub_delta[rr[i]] : 0;
     float s[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) s[i] = 0.f;
@@ -813,7 +839,8 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const bool reuse = carry && rr[0] == xrow;
 #pragma unroll
       for (int i = 0; i < U; ++i) {
-        if (f < K && p + i < t.nz_end && (i == 0 ? !reuse : rr[i] != rr[i - 1])) x[i].load(X + (int64_t)rr[i] * ldx + f);
+        if (f < K && p + i < t.nz_end && (i == 0 ? !reuse : rr[i] != rr[i - 1]))
+          x[i].load(X + (int64_t)(P.sub_row ? P.sub_row[rr[i]] : rr[i]) * ldx + f);
         else x[i].zero();
       }
       BFrag<VEC> xe = reuse ? xc : x[0];
@@ -835,7 +862,13 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const float sum = reduce_scatter<LPG, UB>(v, li);
       const int e = b + li / (LPG / UB);
       if (li % (LPG / UB) == 0 && p + e < t.nz_end) {
-        float* o = &out[P.res_pos ? P.res_pos[p + e] : p + e];
+        // split part: output index = entry index + sub_delta of the entry's sub-row
+        const int q = p + e;
+        int od = 0;   // split part: output index - entry index of entry e's sub-row (selected, not indexed)
+#pragma unroll
+        for (int i = 0; i < UB; ++i)
+          if (i == e - b) od = dsub[b + i];
+        float* o = &out[P.sub_delta ? q + od : P.res_pos ? P.res_pos[q] : q];
         if constexpr (NTO) __builtin_nontemporal_store(sum, o);
         else *o = sum;
       }
@@ -948,6 +981,21 @@ inline size_t occupancy_pad(size_t lds_static, int waves) {
   return want > lds_static ? want - lds_static : 0;
 }
 
+// The plan as the residual kernels see its split part: sub-rows for rows, the per-XCD queues for
+// tasks (workgroup i takes queue i mod kXcds).
+DevicePlan split_view(const DevicePlan& p) {
+  DevicePlan v = p;
+  v.rowptr = p.x_rowptr;
+  v.tasks = p.x_tasks;
+  v.ntasks = p.x_ntasks;
+  v.task_max = p.x_task_max;
+  v.xcd_queues = 1;
+  v.sub_delta = p.x_sub_delta;
+  v.sub_row = p.x_sub_row;
+  v.res_pos = nullptr;
+  return v;
+}
+
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
 void launch_tasks(dim3 grid, int waves, hipStream_t s, const DevicePlan& p, const uint16_t* B, int64_t ldb, int K,
                   float* C, int64_t ldc, float* partial) {
@@ -993,9 +1041,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   if (p.feature_lanes <= 0 && lpg < 4) lpg = 4;
   const int fpp = lpg * VEC;
   const int passes = (K + fpp - 1) / fpp;
-  if (p.ntasks > 0) {
-    const int gpb = 4 * (64 / lpg);
-    dim3 grid((p.ntasks + gpb - 1) / gpb, passes);
+  // the main part writes C; the split part (XCD column split) writes sub-row j to partial slot j
+  auto run_tasks = [&](const DevicePlan& p, float* C, int64_t ldc) {
+    if (p.ntasks <= 0) return;
+    dim3 grid(residual_grid(p, 64 / lpg), passes);
     // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
     // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
     // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
@@ -1046,7 +1095,9 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     switch (lpg) { TRS_TASKS(1) TRS_TASKS(2) TRS_TASKS(4) TRS_TASKS(8) TRS_TASKS(16) TRS_TASKS(32) TRS_TASKS(64) }
 #undef TRS_TASKS
 #undef TRS_TASKS_NT
-  }
+  };
+  run_tasks(p, C, ldc);
+  if (p.x_ntasks > 0) run_tasks(split_view(p), partial, K);
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {
     const int kc16 = ((K + 15) / 16) * 16;
@@ -1073,7 +1124,7 @@ template <int VEC>
 hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                             int K, float* out, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
-  if (p.ntasks > 0) {
+  {
     int lpg = lanes_for(K, VEC);
     // fewer lanes than features: the kernel loops over feature chunks per batch (no second walk
     // of the entries), so narrow loads take the group width with the fewest lane slots (same-box
@@ -1085,8 +1136,10 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // outputs stream; lanes past K add zeros (R-MAT K=4 0.329 -> 0.258 ms, K=2 0.327 -> 0.259,
     // K=1 0.467 -> 0.260)
     if (p.feature_lanes <= 0 && lpg < 8) lpg = 8;
-    const int gpb = 4 * (64 / lpg);
-    dim3 grid((p.ntasks + gpb - 1) / gpb);
+    // the main part, then the split part (XCD column split) through its view
+    auto run_tasks = [&](const DevicePlan& p) {
+    if (p.ntasks <= 0) return;
+    dim3 grid(residual_grid(p, 64 / lpg));
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
     // 1.140 -> 1.112 ms; K=256 +1%, not staged); groups of <= 8 lanes load the next batch's
     // column ids while the current batch's gathers are in flight (K=32 0.429 -> 0.416 ms, K=8
@@ -1120,6 +1173,9 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #undef TRS_SD
 #undef TRS_SD_U
 #undef TRS_SD_LAUNCH
+    };
+    run_tasks(p);
+    if (p.x_ntasks > 0) run_tasks(split_view(p));
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.ntiles > 0 && p.tile_pos) {

@@ -10,13 +10,21 @@ namespace trs {
 // ~row_end (a split row, finished by the fixup kernel).
 struct Task { int32_t row_begin, row_end, nz_begin, nz_end; };
 
-// A split row: C[row] = sum of partial slots [slot_begin, slot_begin + slots) in order.
+// A split row: C[row] = sum of partial slots slot_list[slot_begin .. slot_begin + slots) in order.
 struct Fixup { int32_t row, slot_begin, slots, pad; };
 
 // Rows per multi-row residual task (the task kernel preloads their row pointers into LDS).
 constexpr int kTaskRows = 32;
 // Split rows with more slots than this are summed by one workgroup each.
+// (A Fixup's slot_begin indexes DevicePlan::slot_list, which names the row's partial slots in
+// summation order.)
 constexpr int kWideFixupSlots = 16;
+
+// XCDs of an MI355X: workgroup i of a launch runs on XCD i mod kXcds (each XCD has its own L2).
+constexpr int kXcds = 8;
+// XCD whose L2 serves column c's B row in the SpMM column split: a multiplicative hash spreads hot
+// and cold columns evenly over the XCDs.
+inline int xcd_of_column(int32_t c) { return (int)(((uint32_t)c * 2654435761u) >> 29); }
 
 // A window handled by the MFMA window kernel: 16 output rows starting at row0 (rows >= m are
 // dropped), dense 16x16 fp16 tiles [tile_begin, tile_end), plus that window's residual rows.
@@ -53,6 +61,22 @@ struct DevicePlan {
   int32_t sddmm_unroll = 0;    // SDDMM residual entries in flight per lane group (4, 8; 0 automatic)
   int32_t task_nnz = 0;        // entries per packed residual task
   int32_t task_max = 0;        // most entries of any residual task (packed rows or a piece)
+  const int32_t* slot_list = nullptr;   // partial slots of the split rows, in summation order
+  // XCD column split: sub-rows (pieces of long rows by column range, laid out range-major in
+  // col / val after the main part) with their own tasks, queue x = x_tasks [xq[x], xq[x + 1]) for
+  // XCD x; SpMM sub-row j sums into partial slot j
+  const Task* x_tasks = nullptr;
+  int32_t x_ntasks = 0;
+  int32_t x_task_max = 0;
+  const int32_t* x_rowptr = nullptr;
+  const int32_t* x_sub_delta = nullptr; // SDDMM: output index - entry index on sub-row j
+  const int32_t* x_sub_row = nullptr;   // SDDMM: the row of sub-row j
+  int32_t xq[kXcds + 1] = {};
+  // set in the view the launcher builds for the split part (see split_view): tasks come from the
+  // per-XCD queues, workgroup i taking queue i mod kXcds; rows are sub-rows
+  int32_t xcd_queues = 0;
+  const int32_t* sub_delta = nullptr;
+  const int32_t* sub_row = nullptr;
 };
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.

@@ -57,6 +57,16 @@ struct Status {
 
 Status fail(int code, const std::string& m) { return Status{code, m}; }
 
+// Default XCD column split threshold of SpMM plans (rows with at least this many residual
+// entries; R-MAT 2^20 step at K = 32 / 64 / 128 / 256: -16% / -6% / -18% / -19% against no split,
+// 128 and 512 entries measured slower at K = 128).  SDDMM plans do not split by default: with
+// contiguous column ranges (its outputs must stay in runs) R-MAT K = 128 measured 0.98 ms unsplit,
+// 1.03 - 1.18 ms split at 256 - 32 entries.
+constexpr int32_t kSpmmSplitMin = 256;
+constexpr int32_t kSddmmSplitMin = 0;
+// SDDMM column ranges: weight of a distinct column, in entries, when balancing the XCDs
+constexpr int64_t kSddmmColumnWeight = 48;
+
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
   const unsigned h = std::thread::hardware_concurrency();
@@ -358,21 +368,47 @@ struct Blob {
   size_t size() const { return total + 256; }
 };
 
+// Residual work items of a plan.
+//
+// Main part: tasks over the rows of `rowptr` that no MFMA window owns (owned: per 16-row block,
+// empty = none), spread over the chip by xcd_remap: runs of whole rows (<= S entries, <= kTaskRows
+// rows) and equal pieces of rows longer than piece_max.  SpMM pieces sum into partial slots that
+// the fixup kernel adds up in a fixed order; SDDMM pieces write their own outputs.
+//
+// XCD column split (split part): workgroup i runs on XCD i mod 8 (measured on MI355X for every
+// grid size and workload), and each XCD has its own 4 MB L2.  The columns are divided among the 8
+// XCDs and rows with at least split_min entries are cut into sub-rows, one per XCD, laid out
+// XCD-major after the main part; XCD x's sub-rows are packed into tasks like ordinary rows and
+// queued for XCD x, so each L2 caches B rows of one eighth of the columns only.  An SpMM sub-row's
+// sum goes to a partial slot (sub-row j -> slot j; pieces of long sub-rows get slots of their own
+// after those), and the fixup adds a split row's slots in XCD order, so the result is
+// deterministic.  SDDMM sub-rows are copies of the split rows' column ids over contiguous column
+// ranges, whose outputs go to the entries' own positions (sub_delta[j] = output index - entry
+// index on sub-row j).
 struct Tasks {
-  std::vector<trs::Task> tasks;
-  std::vector<trs::Fixup> fix, wfix;
+  std::vector<trs::Task> tasks;      // main part
+  std::vector<trs::Task> xtasks;     // split part: queue x = xtasks [xq[x], xq[x + 1])
+  int32_t xq[trs::kXcds + 1] = {};
+  std::vector<int32_t> xrowptr;      // sub-row j: entries [xrowptr[j], xrowptr[j + 1]) of col / val
+  std::vector<int32_t> sub_delta;    // SDDMM: output index - entry index on sub-row j
+  std::vector<int32_t> sub_row;      // SDDMM: the row sub-row j belongs to
+  std::vector<trs::Fixup> fix, wfix; // SpMM: {row, first index into slot_list, slots}
+  std::vector<int32_t> slot_list;
   int32_t slots = 0;
   int64_t split_rows = 0;
-  int32_t task_nnz = 0;   // entries per packed task (S)
+  int32_t task_nnz = 0;              // entries per packed task (S)
+  int32_t task_max = 0, xtask_max = 0;
   Status st;
 };
 
-// Residual work items over the rows of `rowptr` that no MFMA window owns (owned: per 16-row block,
-// empty = none).  with_fixup: long rows become pieces summed into partial slots (SpMM); otherwise
-// each piece writes its own outputs (SDDMM, whose outputs are per entry).
-Tasks build_tasks(const std::vector<int32_t>& rowptr, int32_t m, int64_t nent, const std::vector<uint8_t>& owned,
-                  bool with_fixup, const trs_plan_options& opt) {
+// rowptr / col / val: the residual CSR (val null for SDDMM).  SpMM moves the split rows' entries
+// out of the main part (their main rows become empty) into the sub-rows; SDDMM keeps the main part
+// whole (outputs follow its order) and appends copies of the split rows' column ids.
+Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::vector<uint16_t>* val, int32_t m,
+                  int32_t n, const std::vector<uint8_t>& owned, bool with_fixup, int32_t split_min,
+                  const trs_plan_options& opt) {
   Tasks T;
+  const int64_t nent = rowptr[m];
   // Entries per packed task: short rows want small tasks (more lane groups in flight, fewer row
   // flushes per group), long rows want larger ones.  Measured on MI355X: 32 for a degree-4 mesh,
   // 128 for R-MAT (mean non-empty row ~49) -- about four mean rows per task.
@@ -387,43 +423,231 @@ Tasks build_tasks(const std::vector<int32_t>& rowptr, int32_t m, int64_t nent, c
   const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
   const int rows_cap = trs::kTaskRows;
   auto is_owned = [&](int32_t r) { return !owned.empty() && owned[r / 16]; };
-  std::vector<trs::Task> pieces, packed;
-  int32_t r = 0;
-  while (r < m) {
-    if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
-    const int32_t deg = rowptr[r + 1] - rowptr[r];
-    if (deg > piece_max) {
-      const int np = (deg + piece_max - 1) / piece_max;
-      const int32_t base = T.slots;
-      for (int q = 0; q < np; ++q) {
-        const int32_t b = rowptr[r] + (int32_t)((int64_t)deg * q / np);
-        const int32_t e = rowptr[r] + (int32_t)((int64_t)deg * (q + 1) / np);
-        pieces.push_back({r, with_fixup ? ~T.slots : -1, b, e});
-        if (with_fixup) ++T.slots;
+
+  // split rows and the column cut points of the XCD ranges, balanced by the split rows' entries
+  std::vector<uint8_t> split((size_t)m, 0);
+  int64_t split_entries = 0;
+  if (split_min > 0 && n > 0)
+    for (int32_t r = 0; r < m; ++r)
+      if (!is_owned(r) && rowptr[r + 1] - rowptr[r] >= split_min) {
+        split[r] = 1;
+        split_entries += rowptr[r + 1] - rowptr[r];
       }
-      if (with_fixup) {
-        (np > trs::kWideFixupSlots ? T.wfix : T.fix).push_back({r, base, np, 0});
-        ++T.split_rows;
+  struct Sub { int32_t row, b, e; };   // SDDMM: entries [b, e) of the residual CSR
+  std::vector<Sub> subs;                 // XCD-major
+  int32_t xfirst[trs::kXcds + 1] = {};
+  if (split_entries > 0) {
+    std::vector<int32_t> rows_split;
+    for (int32_t r = 0; r < m; ++r)
+      if (split[r]) rows_split.push_back(r);
+    const size_t ns = rows_split.size();
+    if (with_fixup) {
+      // SpMM: a column's XCD is a hash of its index, so every XCD gets an even share of hot and
+      // cold columns (contiguous ranges leave the XCD of the rarely used columns with most of the
+      // misses: measured on R-MAT, the other XCDs then wait for it).  Sub-rows are copies, so the
+      // scattered entries cost nothing more.
+      std::vector<int32_t> cnt(ns * trs::kXcds, 0);
+      for (size_t i = 0; i < ns; ++i)
+        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e)
+          cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
+      std::vector<int32_t> rp2((size_t)m + 1), col2((size_t)nent);
+      std::vector<uint16_t> val2((size_t)nent);
+      int64_t w = 0;
+      for (int32_t r = 0; r < m; ++r) {
+        rp2[r] = (int32_t)w;
+        if (split[r]) continue;
+        for (int32_t e = rowptr[r]; e < rowptr[r + 1]; ++e, ++w) {
+          col2[w] = col[e];
+          val2[w] = (*val)[e];
+        }
       }
-      ++r;
-      continue;
+      rp2[m] = (int32_t)w;
+      // sub-row starts, XCD-major; cnt becomes each (row, XCD) write cursor
+      for (int y = 0; y < trs::kXcds; ++y) {
+        xfirst[y] = (int32_t)subs.size();
+        for (size_t i = 0; i < ns; ++i) {
+          int32_t& c = cnt[i * trs::kXcds + y];
+          if (c == 0) { c = -1; continue; }
+          subs.push_back({rows_split[i], 0, 0});
+          T.xrowptr.push_back((int32_t)w);
+          const int32_t len = c;
+          c = (int32_t)w;
+          w += len;
+        }
+      }
+      xfirst[trs::kXcds] = (int32_t)subs.size();
+      T.xrowptr.push_back((int32_t)w);
+      for (size_t i = 0; i < ns; ++i)
+        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e) {
+          const int32_t q = cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
+          col2[q] = col[e];
+          val2[q] = (*val)[e];
+        }
+      rowptr.swap(rp2);
+      col.swap(col2);
+      val->swap(val2);
+    } else {
+      // SDDMM: outputs must stay in runs, so contiguous column ranges, balanced by entries plus a
+      // fixed weight per distinct column (the first use of a column misses whatever its degree,
+      // so ranges of rarely used columns get fewer entries)
+      std::vector<int64_t> cnt((size_t)n, 0);
+      for (int32_t r : rows_split)
+        for (int32_t e = rowptr[r]; e < rowptr[r + 1]; ++e) cnt[col[e]]++;
+      int64_t tot = 0;
+      for (int32_t c = 0; c < n; ++c)
+        if (cnt[c]) tot += cnt[c] += kSddmmColumnWeight;
+      int32_t cut[trs::kXcds + 1];
+      cut[0] = 0;
+      int x = 1;
+      int64_t acc = 0;
+      for (int32_t c = 0; c < n && x < trs::kXcds; ++c) {
+        acc += cnt[c];
+        while (x < trs::kXcds && acc * trs::kXcds >= tot * x) cut[x++] = c + 1;
+      }
+      for (; x <= trs::kXcds; ++x) cut[x] = n;
+      // each split row's columns are sorted: a range is a contiguous run of its entries
+      std::vector<int32_t> bnd(ns * (trs::kXcds + 1));
+      for (size_t i = 0; i < ns; ++i) {
+        const int32_t r = rows_split[i];
+        int32_t* bd = &bnd[i * (trs::kXcds + 1)];
+        bd[0] = rowptr[r];
+        for (int y = 1; y < trs::kXcds; ++y)
+          bd[y] = (int32_t)(std::lower_bound(col.begin() + rowptr[r], col.begin() + rowptr[r + 1], cut[y]) - col.begin());
+        bd[trs::kXcds] = rowptr[r + 1];
+      }
+      for (int y = 0; y < trs::kXcds; ++y) {
+        xfirst[y] = (int32_t)subs.size();
+        for (size_t i = 0; i < ns; ++i) {
+          const int32_t* bd = &bnd[i * (trs::kXcds + 1)];
+          if (bd[y + 1] > bd[y]) subs.push_back({rows_split[i], bd[y], bd[y + 1]});
+        }
+      }
+      xfirst[trs::kXcds] = (int32_t)subs.size();
+      // the main part stays whole (outputs follow its order); the sub-rows are copies of its
+      // column ids after it
+      T.xrowptr.resize(subs.size() + 1);
+      T.sub_delta.resize(subs.size());
+      T.sub_row.resize(subs.size());
+      int64_t w = nent;
+      col.resize((size_t)nent + (size_t)split_entries);
+      for (size_t j = 0; j < subs.size(); ++j) {
+        T.xrowptr[j] = (int32_t)w;
+        T.sub_delta[j] = subs[j].b - (int32_t)w;
+        T.sub_row[j] = subs[j].row;
+        for (int32_t e = subs[j].b; e < subs[j].e; ++e, ++w) col[w] = col[e];
+      }
+      T.xrowptr[subs.size()] = (int32_t)w;
     }
-    // pack whole rows while the entry count stays within S (a single long row forms its own task)
+  }
+  const int32_t J = (int32_t)subs.size();
+  if (with_fixup) T.slots = J;   // sub-row j sums into slot j; piece slots follow
+
+  // equal pieces of at most piece_max entries of [b, e) of (sub-)row r
+  auto cut_pieces = [&](int32_t r, int32_t b, int32_t e, std::vector<trs::Task>& outv, std::vector<int32_t>* slots_of) {
+    const int32_t d = e - b;
+    const int np = (d + piece_max - 1) / piece_max;
+    for (int q = 0; q < np; ++q) {
+      const int32_t pb = b + (int32_t)((int64_t)d * q / np), pe = b + (int32_t)((int64_t)d * (q + 1) / np);
+      outv.push_back({r, with_fixup ? ~T.slots : -1, pb, pe});
+      if (with_fixup) {
+        if (slots_of) slots_of->push_back(T.slots);
+        ++T.slots;
+      }
+    }
+  };
+  auto add_fixup = [&](int32_t r, const std::vector<int32_t>& sl) {
+    if (!with_fixup) return;
+    (sl.size() > (size_t)trs::kWideFixupSlots ? T.wfix : T.fix)
+        .push_back({r, (int32_t)T.slot_list.size(), (int32_t)sl.size(), 0});
+    T.slot_list.insert(T.slot_list.end(), sl.begin(), sl.end());
+    ++T.split_rows;
+  };
+  // runs of whole (sub-)rows [r, r1) of rp, row r1 - r <= rows_cap, entries <= S, none longer
+  // than piece_max; stop(r) ends a run before row r
+  auto pack = [&](const std::vector<int32_t>& rp, int32_t r, int32_t end, auto&& stop) {
     int32_t r1 = r + 1;
-    int32_t tot = deg;
-    while (r1 < m && r1 - r < rows_cap && !is_owned(r1)) {
-      const int32_t d = rowptr[r1 + 1] - rowptr[r1];
+    int32_t tot = rp[r + 1] - rp[r];
+    while (r1 < end && r1 - r < rows_cap && !stop(r1)) {
+      const int32_t d = rp[r1 + 1] - rp[r1];
       if (d > piece_max || tot + d > S) break;
       tot += d;
       ++r1;
     }
+    return r1;
+  };
+
+  // main part
+  std::vector<trs::Task> pieces, packed;
+  std::vector<int32_t> sl;
+  int32_t r = 0;
+  while (r < m) {
+    if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
+    if (split[r]) { ++r; continue; }
+    const int32_t deg = rowptr[r + 1] - rowptr[r];
+    if (deg > piece_max) {
+      sl.clear();
+      cut_pieces(r, rowptr[r], rowptr[r + 1], pieces, &sl);
+      add_fixup(r, sl);
+      ++r;
+      continue;
+    }
+    const int32_t r1 = pack(rowptr, r, m, [&](int32_t q) { return is_owned(q) || split[q] != 0; });
     packed.push_back({r, r1, rowptr[r], rowptr[r1]});
     r = r1;
   }
   T.tasks.reserve(pieces.size() + packed.size());
   T.tasks.insert(T.tasks.end(), pieces.begin(), pieces.end());
   T.tasks.insert(T.tasks.end(), packed.begin(), packed.end());
-  if (T.tasks.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
+  // longest tasks first: a workgroup's lane groups then carry tasks of similar length, so none
+  // idles while a longer one finishes (R-MAT K = 32 / 64 / 128: -9% / -11% / -5%)
+  std::stable_sort(T.tasks.begin(), T.tasks.end(),
+                   [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
+
+  // split part: per range, pieces of long sub-rows and runs of the others
+  if (J > 0) {
+    std::vector<std::vector<int32_t>> piece_slots((size_t)J);
+    for (int y = 0; y < trs::kXcds; ++y) {
+      T.xq[y] = (int32_t)T.xtasks.size();
+      int32_t j = xfirst[y];
+      while (j < xfirst[y + 1]) {
+        const int32_t d = T.xrowptr[j + 1] - T.xrowptr[j];
+        if (d > piece_max) {
+          cut_pieces(j, T.xrowptr[j], T.xrowptr[j + 1], T.xtasks, &piece_slots[j]);
+          ++j;
+          continue;
+        }
+        const int32_t j1 = pack(T.xrowptr, j, xfirst[y + 1], [&](int32_t q) { return false; });
+        T.xtasks.push_back({j, j1, T.xrowptr[j], T.xrowptr[j1]});
+        j = j1;
+      }
+    }
+    T.xq[trs::kXcds] = (int32_t)T.xtasks.size();
+    // longest tasks first in each queue: the lane groups of a workgroup then carry tasks of
+    // similar length, so none idles for long while a long piece finishes
+    for (int y = 0; y < trs::kXcds; ++y)
+      std::stable_sort(T.xtasks.begin() + T.xq[y], T.xtasks.begin() + T.xq[y + 1],
+                       [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
+    if (with_fixup) {
+      // a split row's slots in range order: sub-row j's own slot, or its pieces' slots
+      std::vector<int32_t> first((size_t)m, -1);
+      std::vector<std::vector<int32_t>> rs;
+      for (int32_t jj = 0; jj < J; ++jj) {
+        const int32_t row = subs[jj].row;
+        if (first[row] < 0) {
+          first[row] = (int32_t)rs.size();
+          rs.emplace_back();
+        }
+        auto& v = rs[first[row]];
+        if (piece_slots[jj].empty()) v.push_back(jj);
+        else v.insert(v.end(), piece_slots[jj].begin(), piece_slots[jj].end());
+      }
+      for (int32_t q = 0; q < m; ++q)
+        if (first[q] >= 0) add_fixup(q, rs[first[q]]);
+    }
+  }
+  for (const trs::Task& t : T.tasks) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
+  for (const trs::Task& t : T.xtasks) T.xtask_max = std::max(T.xtask_max, t.nz_end - t.nz_begin);
+  if (T.tasks.size() + T.xtasks.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
   return T;
 }
 
@@ -577,11 +801,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   }
 
   // residual tasks over rows not owned by an MFMA window
-  Tasks T = build_tasks(rowptr, m, nent, owned, true, opt);
+  // XCD column split for SpMM (each sub-row costs a partial slot of 4 K bytes written and read back)
+  const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSpmmSplitMin;
+  Tasks T = build_tasks(rowptr, col, &val, m, L.n, owned, true, split_min, opt);
   if (!T.st.ok()) return T.st;
-  std::vector<trs::Task>& tasks = T.tasks;
-  std::vector<trs::Fixup>& fix = T.fix;
-  std::vector<trs::Fixup>& wfix = T.wfix;
   const int32_t slots = T.slots;
   const int64_t split_rows = T.split_rows;
 
@@ -590,9 +813,12 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   const size_t o_rowptr = blob.add(rowptr);
   const size_t o_col = blob.add(col);
   const size_t o_val = blob.add(val);
-  const size_t o_tasks = blob.add(tasks);
-  const size_t o_fix = blob.add(fix);
-  const size_t o_wfix = blob.add(wfix);
+  const size_t o_tasks = blob.add(T.tasks);
+  const size_t o_xtasks = blob.add(T.xtasks);
+  const size_t o_xrowptr = blob.add(T.xrowptr);
+  const size_t o_fix = blob.add(T.fix);
+  const size_t o_wfix = blob.add(T.wfix);
+  const size_t o_slots = blob.add(T.slot_list);
   const size_t o_mwin = blob.add(mwin);
   const size_t o_tcol = blob.add(tile_cols);
   const size_t o_ta = blob.add(tile_a);
@@ -610,11 +836,17 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   d.col = reinterpret_cast<const int32_t*>(base + o_col);
   d.val = reinterpret_cast<const uint16_t*>(base + o_val);
   d.tasks = reinterpret_cast<const trs::Task*>(base + o_tasks);
-  d.ntasks = (int32_t)tasks.size();
+  d.ntasks = (int32_t)T.tasks.size();
+  d.x_tasks = reinterpret_cast<const trs::Task*>(base + o_xtasks);
+  d.x_ntasks = (int32_t)T.xtasks.size();
+  d.x_rowptr = reinterpret_cast<const int32_t*>(base + o_xrowptr);
+  std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
+  d.x_task_max = T.xtask_max;
   d.fixups = reinterpret_cast<const trs::Fixup*>(base + o_fix);
-  d.nfixups = (int32_t)fix.size();
+  d.nfixups = (int32_t)T.fix.size();
   d.wfixups = reinterpret_cast<const trs::Fixup*>(base + o_wfix);
-  d.nwfixups = (int32_t)wfix.size();
+  d.nwfixups = (int32_t)T.wfix.size();
+  d.slot_list = reinterpret_cast<const int32_t*>(base + o_slots);
   d.partial_slots = slots;
   d.mwin = reinterpret_cast<const trs::MfmaWindow*>(base + o_mwin);
   d.nmwin = (int32_t)mwin.size();
@@ -625,8 +857,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
   d.task_nnz = T.task_nnz;
-  d.task_max = 0;
-  for (const trs::Task& t : tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
+  d.task_max = T.task_max;
   d.streaming = opt.streaming < 0 ? 2 : opt.streaming;
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.stage = opt.stage < 0 ? -1 : 0;
@@ -639,7 +870,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   s.mfma_tiles = (int64_t)L.tiles.size();
   s.mfma_nnz = mfma_nnz;
   s.nnz = nent + mfma_nnz;
-  s.tasks = (int64_t)tasks.size();
+  s.tasks = (int64_t)(T.tasks.size() + T.xtasks.size());
   s.split_rows = split_rows;
   s.partial_slots = slots;
   s.device_bytes = (int64_t)blob.size();
@@ -711,13 +942,21 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
       tile_cols.insert(tile_cols.end(), t.cols, t.cols + 16);
     }
   }
-  Tasks T = build_tasks(rowptr, m, nent, {}, false, opt);
+  // SDDMM sub-rows write their own outputs (no partial slot)
+  const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSddmmSplitMin;
+  // the split part's outputs are contiguous runs of the residual order: only without tiles, whose
+  // merge interleaves output positions
+  Tasks T = build_tasks(rowptr, col, nullptr, m, L.n, {}, false, te.empty() ? split_min : 0, opt);
   if (!T.st.ok()) return T.st;
 
   Blob blob;
   const size_t o_rowptr = blob.add(rowptr);
   const size_t o_col = blob.add(col);
   const size_t o_tasks = blob.add(T.tasks);
+  const size_t o_xtasks = blob.add(T.xtasks);
+  const size_t o_xrowptr = blob.add(T.xrowptr);
+  const size_t o_spos = blob.add(T.sub_delta);
+  const size_t o_srow = blob.add(T.sub_row);
   const size_t o_rpos = blob.add(res_pos);
   const size_t o_trow = blob.add(tile_row0);
   const size_t o_tcol = blob.add(tile_cols);
@@ -736,6 +975,13 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.col = reinterpret_cast<const int32_t*>(base + o_col);
   d.tasks = reinterpret_cast<const trs::Task*>(base + o_tasks);
   d.ntasks = (int32_t)T.tasks.size();
+  d.x_tasks = reinterpret_cast<const trs::Task*>(base + o_xtasks);
+  d.x_ntasks = (int32_t)T.xtasks.size();
+  d.x_rowptr = reinterpret_cast<const int32_t*>(base + o_xrowptr);
+  d.x_sub_delta = reinterpret_cast<const int32_t*>(base + o_spos);
+  d.x_sub_row = reinterpret_cast<const int32_t*>(base + o_srow);
+  std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
+  d.x_task_max = T.xtask_max;
   d.res_pos = res_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_rpos);
   d.tile_row0 = tile_row0.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_trow);
   d.tile_cols = tile_cols.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tcol);
@@ -748,8 +994,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.stage = opt.stage < 0 ? -1 : 0;
   d.occupancy = opt.occupancy < 0 ? -1 : opt.occupancy == 0 ? 0 : std::min(8, std::max(2, opt.occupancy));
   d.task_nnz = T.task_nnz;
-  d.task_max = 0;
-  for (const trs::Task& t : T.tasks) d.task_max = std::max(d.task_max, t.nz_end - t.nz_begin);
+  d.task_max = T.task_max;
   P->csr_only = true;
   trs_plan_stats& s = P->stats;
   s.m = m;
@@ -758,7 +1003,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   s.mfma_tiles = d.ntiles;
   s.mfma_nnz = (int64_t)te.size();
   s.nnz = nent + (int64_t)te.size();
-  s.tasks = (int64_t)T.tasks.size();
+  s.tasks = (int64_t)(T.tasks.size() + T.xtasks.size());
   s.device_bytes = (int64_t)blob.size();
   *out = P;
   return Status{};
@@ -796,6 +1041,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->sddmm_unroll = 0;
   o->stage = 0;
   o->occupancy = 0;
+  o->xcd_split = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }

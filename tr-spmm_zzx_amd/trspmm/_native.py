@@ -31,7 +31,7 @@ class PlanOptions(ctypes.Structure):
     _fields_ = [("mfma_tc", c_i32), ("mfma_sptc", c_i32), ("sptc_min_fill", c_f32), ("task_nnz", c_i32),
                 ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
                 ("xcd_run", c_i32), ("sddmm_unroll", c_i32), ("stage", c_i32),
-                ("occupancy", c_i32)]
+                ("occupancy", c_i32), ("xcd_split", c_i32)]
 
 
 class PlanStats(ctypes.Structure):

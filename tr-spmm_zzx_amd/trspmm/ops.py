@@ -231,12 +231,13 @@ class Plan:
                     sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                     feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
-                    stage: Optional[int] = None, occupancy: Optional[int] = None) -> "Plan":
+                    stage: Optional[int] = None, occupancy: Optional[int] = None,
+                    xcd_split: Optional[int] = None) -> "Plan":
         """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap,
-                     xcd_run=xcd_run, stage=stage, occupancy=occupancy)
+                     xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
         return cls(h.value)
@@ -246,13 +247,13 @@ class Plan:
                   sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
-                  streaming: Optional[int] = None) -> "Plan":
+                  streaming: Optional[int] = None, xcd_split: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
         residual outputs with non-temporal stores."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
-                     streaming=streaming)
+                     streaming=streaming, xcd_split=xcd_split)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
                   "trs_plan_create_sddmm")
@@ -262,7 +263,7 @@ class Plan:
     def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                  feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                  xcd_run: Optional[int] = None, stage: Optional[int] = None,
-                 occupancy: Optional[int] = None) -> "Plan":
+                 occupancy: Optional[int] = None, xcd_split: Optional[int] = None) -> "Plan":
         rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
         col = np.ascontiguousarray(col, dtype=np.int32)
         val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
@@ -274,7 +275,8 @@ class Plan:
             raise ValueError(f"col and val must hold at least rowptr[-1] = {nnz} entries "
                              f"(got {col.shape[0]} and {val.shape[0]})")
         o = _options(False, False, 1.0, task_nnz, piece_nnz=piece_nnz, feature_lanes=feature_lanes,
-                     streaming=streaming, xcd_run=xcd_run, stage=stage, occupancy=occupancy)
+                     streaming=streaming, xcd_run=xcd_run, stage=stage, occupancy=occupancy,
+                     xcd_split=xcd_split)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_csr(_ptr(rowptr), _ptr(col), _ptr(val), m, n, ctypes.byref(o),
                                                 ctypes.byref(h)), "trs_plan_create_csr")
