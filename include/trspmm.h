@@ -181,12 +181,13 @@ typedef struct trs_plan_options {
                              outside are clamped): fewer concurrent tasks keep fewer gathered rows
                              in flight.  0 = automatic (2 for K <= 64, uncapped above), -1 =
                              uncapped (as many as registers and LDS allow) */
-  int32_t xcd_split;      /* XCD column split: the columns are divided among the 8 XCDs (hashed for
-                             SpMM, contiguous ranges for SDDMM) and residual rows with at least this
-                             many entries are cut into one sub-row per XCD, run by that XCD's
-                             workgroups (workgroup i runs on XCD i mod 8), so each XCD's L2 holds B
-                             rows of an eighth of the columns; an SpMM sub-row costs a partial slot.
-                             0 = automatic (SpMM 256, SDDMM off), -1 = off */
+  int32_t xcd_split;      /* XCD column split: the columns are divided among the 8 XCDs by a hash
+                             and residual rows with at least this many entries are cut into one
+                             sub-row per XCD, run by that XCD's workgroups (workgroup i runs on XCD
+                             i mod 8), so each XCD's L2 holds B (or Y) rows of an eighth of the
+                             columns; an SpMM sub-row costs a partial slot, an SDDMM sub-row entry
+                             an output index (SDDMM uses the split from K = 128 on).
+                             0 = automatic (SpMM 256, SDDMM 512), -1 = off */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

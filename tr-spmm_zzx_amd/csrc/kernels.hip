@@ -818,9 +818,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       }
       rr[i] = t.row_begin + r;
     }
-    int dsub[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) dsub[i] = P.sub_delta ? P.sub_delta[rr[i]] : 0;
+
     float s[U];
 #pragma unroll
     for (int i = 0; i < U; ++i) s[i] = 0.f;
@@ -862,13 +860,8 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const float sum = reduce_scatter<LPG, UB>(v, li);
       const int e = b + li / (LPG / UB);
       if (li % (LPG / UB) == 0 && p + e < t.nz_end) {
-        // split part: output index = entry index + sub_delta of the entry's sub-row
         const int q = p + e;
-        int od = 0;   // split part: output index - entry index of entry e's sub-row (selected, not indexed)
-#pragma unroll
-        for (int i = 0; i < UB; ++i)
-          if (i == e - b) od = dsub[b + i];
-        float* o = &out[P.sub_delta ? q + od : P.res_pos ? P.res_pos[q] : q];
+        float* o = &out[P.res_pos ? P.res_pos[q - P.res_off] : q];
         if constexpr (NTO) __builtin_nontemporal_store(sum, o);
         else *o = sum;
       }
@@ -990,9 +983,9 @@ DevicePlan split_view(const DevicePlan& p) {
   v.ntasks = p.x_ntasks;
   v.task_max = p.x_task_max;
   v.xcd_queues = 1;
-  v.sub_delta = p.x_sub_delta;
   v.sub_row = p.x_sub_row;
-  v.res_pos = nullptr;
+  v.res_pos = p.x_pos;          // SDDMM: the split entries' output indices (follow the main part)
+  v.res_off = (int32_t)p.nnz_csr;
   return v;
 }
 
@@ -1174,8 +1167,15 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #undef TRS_SD_U
 #undef TRS_SD_LAUNCH
     };
-    run_tasks(p);
-    if (p.x_ntasks > 0) run_tasks(split_view(p));
+    if (p.x_ntasks > 0 && K < kSddmmSplitMinK) {   // the unsplit layout of every row
+      DevicePlan v = p;
+      v.tasks = p.full_tasks;
+      v.ntasks = p.nfull_tasks;
+      run_tasks(v);
+    } else {
+      run_tasks(p);
+      if (p.x_ntasks > 0) run_tasks(split_view(p));
+    }
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.ntiles > 0 && p.tile_pos) {

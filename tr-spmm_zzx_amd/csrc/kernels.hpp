@@ -48,7 +48,7 @@ struct DevicePlan {
   const int32_t* tile_cols = nullptr;  // [tiles][16]
   const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16 (SpMM)
   int32_t ntiles = 0;
-  // SDDMM plans: output index of each residual entry (null = identity) and, per tile, its first
+  // SDDMM plans: output index of each residual entry (null = identity; see res_off) and, per tile, its first
   // row and the output index of each of its 256 (row, column) slots (-1 = not stored)
   const int32_t* res_pos = nullptr;
   const int32_t* tile_row0 = nullptr;
@@ -69,15 +69,23 @@ struct DevicePlan {
   int32_t x_ntasks = 0;
   int32_t x_task_max = 0;
   const int32_t* x_rowptr = nullptr;
-  const int32_t* x_sub_delta = nullptr; // SDDMM: output index - entry index on sub-row j
+  const int32_t* x_pos = nullptr;       // SDDMM: output index of the split part's entries
   const int32_t* x_sub_row = nullptr;   // SDDMM: the row of sub-row j
+  // SDDMM plans with a split part also keep the unsplit task list of all rows, used below
+  // kSddmmSplitMinK
+  const Task* full_tasks = nullptr;
+  int32_t nfull_tasks = 0;
   int32_t xq[kXcds + 1] = {};
   // set in the view the launcher builds for the split part (see split_view): tasks come from the
   // per-XCD queues, workgroup i taking queue i mod kXcds; rows are sub-rows
   int32_t xcd_queues = 0;
-  const int32_t* sub_delta = nullptr;
   const int32_t* sub_row = nullptr;
+  int32_t res_off = 0;   // res_pos[q - res_off] is entry q's output index
 };
+
+// SDDMM runs a plan's split part from this feature width on (narrower rows measured faster
+// unsplit).
+constexpr int kSddmmSplitMinK = 128;
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,

@@ -57,15 +57,12 @@ struct Status {
 
 Status fail(int code, const std::string& m) { return Status{code, m}; }
 
-// Default XCD column split threshold of SpMM plans (rows with at least this many residual
-// entries; R-MAT 2^20 step at K = 32 / 64 / 128 / 256: -16% / -6% / -18% / -19% against no split,
-// 128 and 512 entries measured slower at K = 128).  SDDMM plans do not split by default: with
-// contiguous column ranges (its outputs must stay in runs) R-MAT K = 128 measured 0.98 ms unsplit,
-// 1.03 - 1.18 ms split at 256 - 32 entries.
+// Default XCD column split thresholds (rows with at least this many residual entries).  SpMM, R-MAT
+// 2^20 step at K = 32 / 64 / 128 / 256: -16% / -6% / -18% / -19% against no split (128 and 512
+// entries measured slower at K = 128).  SDDMM, K = 128 / 256: -14% / -20% (its launcher keeps the
+// unsplit layout below K = 128, where the split measured slower: K = 32 / 64 / 96 +65% / +20% / +8%).
 constexpr int32_t kSpmmSplitMin = 256;
-constexpr int32_t kSddmmSplitMin = 0;
-// SDDMM column ranges: weight of a distinct column, in entries, when balancing the XCDs
-constexpr int64_t kSddmmColumnWeight = 48;
+constexpr int32_t kSddmmSplitMin = 512;
 
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
@@ -382,16 +379,17 @@ struct Blob {
 // queued for XCD x, so each L2 caches B rows of one eighth of the columns only.  An SpMM sub-row's
 // sum goes to a partial slot (sub-row j -> slot j; pieces of long sub-rows get slots of their own
 // after those), and the fixup adds a split row's slots in XCD order, so the result is
-// deterministic.  SDDMM sub-rows are copies of the split rows' column ids over contiguous column
-// ranges, whose outputs go to the entries' own positions (sub_delta[j] = output index - entry
-// index on sub-row j).
+// deterministic.  SDDMM sub-rows are copies of the split rows' column ids, with the output index
+// of each entry (x_pos); since the split only pays from K = 128 on, an SDDMM plan also keeps the
+// unsplit task list of all rows (full) for narrower widths.
 struct Tasks {
   std::vector<trs::Task> tasks;      // main part
   std::vector<trs::Task> xtasks;     // split part: queue x = xtasks [xq[x], xq[x + 1])
   int32_t xq[trs::kXcds + 1] = {};
   std::vector<int32_t> xrowptr;      // sub-row j: entries [xrowptr[j], xrowptr[j + 1]) of col / val
-  std::vector<int32_t> sub_delta;    // SDDMM: output index - entry index on sub-row j
+  std::vector<int32_t> x_pos;        // SDDMM: output index of each sub-row entry
   std::vector<int32_t> sub_row;      // SDDMM: the row sub-row j belongs to
+  std::vector<trs::Task> full;       // SDDMM with a split part: the unsplit layout of every row
   std::vector<trs::Fixup> fix, wfix; // SpMM: {row, first index into slot_list, slots}
   std::vector<int32_t> slot_list;
   int32_t slots = 0;
@@ -433,7 +431,7 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
         split[r] = 1;
         split_entries += rowptr[r + 1] - rowptr[r];
       }
-  struct Sub { int32_t row, b, e; };   // SDDMM: entries [b, e) of the residual CSR
+  struct Sub { int32_t row; };
   std::vector<Sub> subs;                 // XCD-major
   int32_t xfirst[trs::kXcds + 1] = {};
   if (split_entries > 0) {
@@ -468,7 +466,7 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
         for (size_t i = 0; i < ns; ++i) {
           int32_t& c = cnt[i * trs::kXcds + y];
           if (c == 0) { c = -1; continue; }
-          subs.push_back({rows_split[i], 0, 0});
+          subs.push_back({rows_split[i]});
           T.xrowptr.push_back((int32_t)w);
           const int32_t len = c;
           c = (int32_t)w;
@@ -487,56 +485,36 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
       col.swap(col2);
       val->swap(val2);
     } else {
-      // SDDMM: outputs must stay in runs, so contiguous column ranges, balanced by entries plus a
-      // fixed weight per distinct column (the first use of a column misses whatever its degree,
-      // so ranges of rarely used columns get fewer entries)
-      std::vector<int64_t> cnt((size_t)n, 0);
-      for (int32_t r : rows_split)
-        for (int32_t e = rowptr[r]; e < rowptr[r + 1]; ++e) cnt[col[e]]++;
-      int64_t tot = 0;
-      for (int32_t c = 0; c < n; ++c)
-        if (cnt[c]) tot += cnt[c] += kSddmmColumnWeight;
-      int32_t cut[trs::kXcds + 1];
-      cut[0] = 0;
-      int x = 1;
-      int64_t acc = 0;
-      for (int32_t c = 0; c < n && x < trs::kXcds; ++c) {
-        acc += cnt[c];
-        while (x < trs::kXcds && acc * trs::kXcds >= tot * x) cut[x++] = c + 1;
-      }
-      for (; x <= trs::kXcds; ++x) cut[x] = n;
-      // each split row's columns are sorted: a range is a contiguous run of its entries
-      std::vector<int32_t> bnd(ns * (trs::kXcds + 1));
-      for (size_t i = 0; i < ns; ++i) {
-        const int32_t r = rows_split[i];
-        int32_t* bd = &bnd[i * (trs::kXcds + 1)];
-        bd[0] = rowptr[r];
-        for (int y = 1; y < trs::kXcds; ++y)
-          bd[y] = (int32_t)(std::lower_bound(col.begin() + rowptr[r], col.begin() + rowptr[r + 1], cut[y]) - col.begin());
-        bd[trs::kXcds] = rowptr[r + 1];
-      }
+      // SDDMM: the same hashed split; the main part stays whole (its outputs are the identity) and
+      // the sub-rows are copies of the split rows' column ids, each with its output index
+      std::vector<int32_t> cnt(ns * trs::kXcds, 0);
+      for (size_t i = 0; i < ns; ++i)
+        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e)
+          cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
+      int64_t w = nent;
+      col.resize((size_t)nent + (size_t)split_entries);
+      T.x_pos.resize((size_t)split_entries);
       for (int y = 0; y < trs::kXcds; ++y) {
         xfirst[y] = (int32_t)subs.size();
         for (size_t i = 0; i < ns; ++i) {
-          const int32_t* bd = &bnd[i * (trs::kXcds + 1)];
-          if (bd[y + 1] > bd[y]) subs.push_back({rows_split[i], bd[y], bd[y + 1]});
+          int32_t& c = cnt[i * trs::kXcds + y];
+          if (c == 0) { c = -1; continue; }
+          subs.push_back({rows_split[i]});
+          T.xrowptr.push_back((int32_t)w);
+          T.sub_row.push_back(rows_split[i]);
+          const int32_t len = c;
+          c = (int32_t)w;
+          w += len;
         }
       }
       xfirst[trs::kXcds] = (int32_t)subs.size();
-      // the main part stays whole (outputs follow its order); the sub-rows are copies of its
-      // column ids after it
-      T.xrowptr.resize(subs.size() + 1);
-      T.sub_delta.resize(subs.size());
-      T.sub_row.resize(subs.size());
-      int64_t w = nent;
-      col.resize((size_t)nent + (size_t)split_entries);
-      for (size_t j = 0; j < subs.size(); ++j) {
-        T.xrowptr[j] = (int32_t)w;
-        T.sub_delta[j] = subs[j].b - (int32_t)w;
-        T.sub_row[j] = subs[j].row;
-        for (int32_t e = subs[j].b; e < subs[j].e; ++e, ++w) col[w] = col[e];
-      }
-      T.xrowptr[subs.size()] = (int32_t)w;
+      T.xrowptr.push_back((int32_t)w);
+      for (size_t i = 0; i < ns; ++i)
+        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e) {
+          const int32_t q = cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
+          col[q] = col[e];
+          T.x_pos[q - nent] = e;
+        }
     }
   }
   const int32_t J = (int32_t)subs.size();
@@ -576,32 +554,36 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
     return r1;
   };
 
-  // main part
-  std::vector<trs::Task> pieces, packed;
-  std::vector<int32_t> sl;
-  int32_t r = 0;
-  while (r < m) {
-    if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
-    if (split[r]) { ++r; continue; }
-    const int32_t deg = rowptr[r + 1] - rowptr[r];
-    if (deg > piece_max) {
-      sl.clear();
-      cut_pieces(r, rowptr[r], rowptr[r + 1], pieces, &sl);
-      add_fixup(r, sl);
-      ++r;
-      continue;
+  // main part (skip_split: without the split rows); longest tasks first, so that a workgroup's
+  // lane groups carry tasks of similar length and none idles while a longer one finishes (R-MAT
+  // K = 32 / 64 / 128: -9% / -11% / -5%)
+  auto build_main = [&](bool skip_split, std::vector<trs::Task>& outv) {
+    std::vector<trs::Task> pieces, packed;
+    std::vector<int32_t> sl;
+    int32_t r = 0;
+    while (r < m) {
+      if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
+      if (skip_split && split[r]) { ++r; continue; }
+      const int32_t deg = rowptr[r + 1] - rowptr[r];
+      if (deg > piece_max) {
+        sl.clear();
+        cut_pieces(r, rowptr[r], rowptr[r + 1], pieces, &sl);
+        add_fixup(r, sl);
+        ++r;
+        continue;
+      }
+      const int32_t r1 = pack(rowptr, r, m, [&](int32_t q) { return is_owned(q) || (skip_split && split[q] != 0); });
+      packed.push_back({r, r1, rowptr[r], rowptr[r1]});
+      r = r1;
     }
-    const int32_t r1 = pack(rowptr, r, m, [&](int32_t q) { return is_owned(q) || split[q] != 0; });
-    packed.push_back({r, r1, rowptr[r], rowptr[r1]});
-    r = r1;
-  }
-  T.tasks.reserve(pieces.size() + packed.size());
-  T.tasks.insert(T.tasks.end(), pieces.begin(), pieces.end());
-  T.tasks.insert(T.tasks.end(), packed.begin(), packed.end());
-  // longest tasks first: a workgroup's lane groups then carry tasks of similar length, so none
-  // idles while a longer one finishes (R-MAT K = 32 / 64 / 128: -9% / -11% / -5%)
-  std::stable_sort(T.tasks.begin(), T.tasks.end(),
-                   [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
+    outv.reserve(pieces.size() + packed.size());
+    outv.insert(outv.end(), pieces.begin(), pieces.end());
+    outv.insert(outv.end(), packed.begin(), packed.end());
+    std::stable_sort(outv.begin(), outv.end(),
+                     [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
+  };
+  build_main(true, T.tasks);
+  if (!with_fixup && J > 0) build_main(false, T.full);   // SDDMM: no slots, no fixups to repeat
 
   // split part: per range, pieces of long sub-rows and runs of the others
   if (J > 0) {
@@ -646,8 +628,9 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
     }
   }
   for (const trs::Task& t : T.tasks) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
+  for (const trs::Task& t : T.full) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
   for (const trs::Task& t : T.xtasks) T.xtask_max = std::max(T.xtask_max, t.nz_end - t.nz_begin);
-  if (T.tasks.size() + T.xtasks.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
+  if (T.tasks.size() + T.xtasks.size() + T.full.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
   return T;
 }
 
@@ -955,8 +938,9 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const size_t o_tasks = blob.add(T.tasks);
   const size_t o_xtasks = blob.add(T.xtasks);
   const size_t o_xrowptr = blob.add(T.xrowptr);
-  const size_t o_spos = blob.add(T.sub_delta);
+  const size_t o_xpos = blob.add(T.x_pos);
   const size_t o_srow = blob.add(T.sub_row);
+  const size_t o_full = blob.add(T.full);
   const size_t o_rpos = blob.add(res_pos);
   const size_t o_trow = blob.add(tile_row0);
   const size_t o_tcol = blob.add(tile_cols);
@@ -978,8 +962,10 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.x_tasks = reinterpret_cast<const trs::Task*>(base + o_xtasks);
   d.x_ntasks = (int32_t)T.xtasks.size();
   d.x_rowptr = reinterpret_cast<const int32_t*>(base + o_xrowptr);
-  d.x_sub_delta = reinterpret_cast<const int32_t*>(base + o_spos);
+  d.x_pos = reinterpret_cast<const int32_t*>(base + o_xpos);
   d.x_sub_row = reinterpret_cast<const int32_t*>(base + o_srow);
+  d.full_tasks = reinterpret_cast<const trs::Task*>(base + o_full);
+  d.nfull_tasks = (int32_t)T.full.size();
   std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
   d.x_task_max = T.xtask_max;
   d.res_pos = res_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_rpos);
