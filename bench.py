@@ -192,6 +192,20 @@ def cpu_baseline_sddmm(g, Xh, Yh, flops):
                       f"({t * 1e3:.1f} ms/run) on {cpu_model()}"}
 
 
+def calibration_copy(mib: int) -> None:
+    """One device copy of `mib` MiB (a known byte count for scaling FETCH_SIZE / WRITE_SIZE in
+    rocprofv3 --pmc runs); nothing when mib is 0."""
+    if not mib:
+        return
+    import torch
+    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def bench_sddmm(args, workload, g, K):
     """Config 4: SDDMM out[e] = X[row_e] . Y[col_e] on the R-MAT pattern (hybrid tiling)."""
     import numpy as np
@@ -209,6 +223,7 @@ def bench_sddmm(args, workload, g, K):
     X = torch.from_numpy(Xh).cuda()
     Y = torch.from_numpy(Yh).cuda()
     out = torch.empty(st["nnz"], dtype=torch.float32, device="cuda")
+    calibration_copy(args.calibrate_copy_mib)
     for _ in range(args.warmup):
         plan.sddmm(X, Y, out=out)
     torch.cuda.synchronize()
@@ -352,14 +367,7 @@ def main():
     need = plan.workspace_bytes(K)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
 
-    if args.calibrate_copy_mib:
-        n_el = args.calibrate_copy_mib * (1 << 20) // 4
-        src = torch.ones(n_el, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calibration_copy(args.calibrate_copy_mib)
     for _ in range(args.warmup):
         plan.spmm(B, out=C, workspace=ws)
     torch.cuda.synchronize()
