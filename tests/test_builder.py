@@ -238,3 +238,30 @@ def test_product_matches_reference_digests_at_full_size(name, golden_env):
     bad = [(ob.SLOTS[i][0], list(arrs[i].shape), want["shapes"][i]) for i in range(29)
            if mg.array_digest(arrs[i]) != want["slots"][i]]
     assert not bad, f"arrays differing from the reference: {bad}"
+
+
+def test_dropin_builder_warns_once_about_dropped_entries(golden_env):
+    """The drop-in returns the reference's arrays, which leave out entries of rows with more than
+    two values in a 2:4 group; it says so once per process (DroppedEntriesWarning)."""
+    import warnings
+    import Libra5BlockOnline as L5
+    golden_env({})
+    L5._warned = False
+    g = graphs.erdos_renyi_gcn(nodes=512, edges=4096, seed=0)
+    args = (torch.from_numpy(g.rowptr), torch.from_numpy(g.col), torch.from_numpy(g.val), 32, 32, 3, 8, 16, 16,
+            0.0, 0.5, 12)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        out = L5.block_sptc_2to4_online(*args)
+        L5.block_sptc_2to4_online(*args)
+    dropped = [x for x in w if issubclass(x.category, L5.DroppedEntriesWarning)]
+    assert len(dropped) == 1 and "spill" in str(dropped[0].message)
+    assert len(out) == 30
+    # a diagonal matrix loses nothing: no warning
+    L5._warned = False
+    r = torch.arange(0, 33, dtype=torch.int32)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        L5.block_sptc_2to4_online(r, torch.arange(32, dtype=torch.int32), torch.ones(32), 32, 32, 3, 8, 16, 16,
+                                  0.0, 0.5, 12)
+    assert not [x for x in w if issubclass(x.category, L5.DroppedEntriesWarning)]

@@ -145,3 +145,24 @@ def test_reference_harness_flow_through_dataset(tmp_path, monkeypatch):
     e = osp.spmm_error(full.numpy(), osp.csr_spmm(d.row_pointers.numpy(), d.column_index.numpy(), vals16,
                                                   d.x.numpy(), m=g.m))
     assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e
+
+
+def test_skip_tc_kernel_switch(monkeypatch):
+    """LIBRA_SKIP_TC_KERNEL=1 leaves the TC share out, as the reference's debug switch skips its TC
+    kernel (mGCNkernel_online.cu:1397-1410): the result is the SpMM of every other share."""
+    say("skip tc kernel")
+    g = graphs.sbm(communities=512, seed=2, val_seed=3)
+    t, x = harness_inputs(g, 64, seed=4)
+    arrs = [a.numpy() if a.dtype != torch.float16 else a.float().numpy() for a in t[:29]]
+    tr, tcol, tv = [], [], []
+    osp._tc_to_coo(arrs, tr, tcol, tv)
+    assert len(tr) > 0
+    full = format_reference(t, g, x, False)
+    tc_only = osp.coo_spmm(np.asarray(tr), np.asarray(tcol), np.asarray(tv), x.numpy().astype(np.float64), g.m)
+    monkeypatch.setenv("LIBRA_SKIP_TC_KERNEL", "1")
+    res = parallel_call(t, x, g)
+    e = osp.spmm_error(res[0].numpy(), full - tc_only)
+    assert e["elementwise_ok"], e
+    monkeypatch.setenv("LIBRA_SKIP_TC_KERNEL", "yes")   # only 1 / true / TRUE switch it on
+    res = parallel_call(t, x, g)
+    assert osp.spmm_error(res[0].numpy(), full)["elementwise_ok"]

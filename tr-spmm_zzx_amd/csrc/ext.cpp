@@ -16,6 +16,7 @@
 #include <torch/cuda.h>
 #include <torch/extension.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -163,6 +164,13 @@ void common_checks(int window, int dimN, int mOri, int kOri, int epoches, const 
 
 const uint16_t* h16(const torch::Tensor& t) { return reinterpret_cast<const uint16_t*>(t.data_ptr()); }
 
+// The reference's on/off environment switches: "1", "true" or "TRUE" enable
+// (TR-source/SpMM/mGCNkernel_online.cu:27-32).
+bool env_enabled(const char* name) {
+  const char* v = std::getenv(name);
+  return v && (std::strcmp(v, "1") == 0 || std::strcmp(v, "true") == 0 || std::strcmp(v, "TRUE") == 0);
+}
+
 std::vector<torch::Tensor> parallel_online(
     torch::Tensor t_row_offset, torch::Tensor t_blockNew_offset, torch::Tensor t_column, torch::Tensor t_value,
     torch::Tensor t_window_row, torch::Tensor t_atomic, torch::Tensor t_binary, torch::Tensor c_row_offsets,
@@ -255,12 +263,15 @@ std::vector<torch::Tensor> parallel_online(
 
   trs_parallel_arrays a;
   std::memset(&a, 0, sizeof(a));
-  a.t_row_offset = t_row_offset.data_ptr<int32_t>(); a.n_t_row_offset = parts_t + 1;
+  // LIBRA_SKIP_TC_KERNEL skips the TC share, as the reference's debug switch skips its TC kernel
+  // (mGCNkernel_online.cu:1397-1410)
+  const int tc_parts = env_enabled("LIBRA_SKIP_TC_KERNEL") ? 0 : parts_t;
+  a.t_row_offset = t_row_offset.data_ptr<int32_t>(); a.n_t_row_offset = tc_parts + 1;
   a.t_block_offset = t_blockNew_offset.data_ptr<int32_t>(); a.n_t_block_offset = t_blockNew_offset.numel();
   a.t_column = t_column.data_ptr<int32_t>(); a.n_t_column = t_column.numel();
   a.t_value = h16(t_value); a.n_t_value = t_value.numel();
-  a.t_window_row = t_window_row.data_ptr<int32_t>(); a.n_t_window_row = parts_t;
-  a.t_atomic = t_atomic.data_ptr<int32_t>(); a.n_t_atomic = parts_t;
+  a.t_window_row = t_window_row.data_ptr<int32_t>(); a.n_t_window_row = tc_parts;
+  a.t_atomic = t_atomic.data_ptr<int32_t>(); a.n_t_atomic = tc_parts;
   a.t_binary = t_binary.data_ptr<int64_t>(); a.n_t_binary = t_binary.numel();
   a.c_row_offsets = c_row_offsets.data_ptr<int32_t>(); a.n_c_row_offsets = parts_c + 1;
   a.c_row = c_row.data_ptr<int32_t>(); a.n_c_row = parts_c;
@@ -293,7 +304,7 @@ std::vector<torch::Tensor> parallel_online(
     a.spill_row = sr.data_ptr<int32_t>(); a.spill_col = sc.data_ptr<int32_t>(); a.spill_val = sv.data_ptr<float>();
     a.spill_count = sr.numel();
   }
-  a.parts_t = parts_t; a.parts_c = parts_c; a.partsize_c = partsize_c; a.parts_c_short = parts_c_short;
+  a.parts_t = tc_parts; a.parts_c = parts_c; a.partsize_c = partsize_c; a.parts_c_short = parts_c_short;
   a.window = window; a.m = mOri; a.n = kOri;
   PlanGuard pg;
   ok(trs_plan_create_parallel(&a, nullptr, &pg.p), "forward_fp16_tcu_cuda_sptc_mma_parallel_online");
