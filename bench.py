@@ -314,6 +314,8 @@ def main():
     ap.add_argument("--reorder", choices=["none", "tca", "tca-aligned"], default="none",
                     help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
                          "tca-aligned keeps clusters inside 16-row windows")
+    ap.add_argument("--host-lowering", action="store_true",
+                    help="build the SpMM plan's residual on the host (default: on the device from the input CSR)")
     ap.add_argument("--xcd-split", type=int, default=None,
                     help="plan option xcd_split (rows of >= N residual entries cut by XCD column ranges; "
                          "-1 off; default: the library's)")
@@ -354,8 +356,9 @@ def main():
     log(f"[bench] format built in {fmt.elapsed:.2f}s")
     pre["build_s"] = round(fmt.elapsed, 3)
     t1 = time.time()
-    plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split)
+    plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering)
     pre["plan_s"] = round(time.time() - t1, 3)
+    pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
     if "reorder_s" in pre:
         pre["reorder_s"] = round(pre["reorder_s"], 3)
     st = plan.stats()

@@ -188,6 +188,11 @@ typedef struct trs_plan_options {
                              columns; an SpMM sub-row costs a partial slot, an SDDMM sub-row entry
                              an output index (SDDMM uses the split from K = 128 on).
                              0 = automatic (SpMM 256, SDDMM 512), -1 = off */
+  int32_t host_lowering;  /* trs_plan_create only.  0: when the format holds its input CSR (a format
+                             built in this process from canonical input), the MFMA tiles are cut
+                             from the format on the host and the residual (the input CSR minus the
+                             kept tiles' entries, XCD sub-rows included) is built on the device;
+                             the plan is the same as the host lowering's.  1: always on the host */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);
@@ -266,6 +271,7 @@ typedef struct trs_plan_stats {
   int64_t device_bytes;              /* plan footprint in HBM */
   int64_t mfma_windows;              /* 16-row windows owned by the MFMA window kernel */
   int64_t window_csr_nnz;            /* residual nonzeros inside those windows */
+  int64_t device_lowered;            /* 1: the residual was built on the device (host_lowering) */
 } trs_plan_stats;
 
 int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s);

@@ -1,0 +1,138 @@
+"""GPU: SpMM plans whose residual is built on the device from the format's input CSR.
+
+trs_plan_create lowers on the device when the format holds its input CSR (a format built in this
+process from canonical input): the MFMA tiles are cut from the format arrays on the host, the
+residual -- the input rows minus the kept tiles' entries, XCD sub-rows included -- is written by
+two kernels.  The plan must be the host lowering's: equal statistics and bitwise equal SpMM
+outputs, on every workload shape the host lowering is tested on (tiles kept or demoted, split
+rows, no tiles at all, more or fewer plan rows than input rows), and within the SpMM tolerance of
+the float64 CSR oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmm as osp
+from trspmm import graphs
+import trspmm
+from trspmm import _native as nat
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.cuda.init()
+
+
+def run_plan(plan, Bh):
+    """Output prefilled with NaN: an element no kernel writes fails the comparison."""
+    B = torch.from_numpy(Bh).cuda()
+    out = torch.full((plan.stats()["m"], Bh.shape[1]), float("nan"), device="cuda")
+    C = plan.spmm(B, out=out)
+    torch.cuda.synchronize()
+    return C.cpu().numpy()
+
+
+GRAPHS = [
+    ("er4096", lambda: graphs.erdos_renyi_gcn()),
+    ("rmat14", lambda: graphs.rmat(scale=14, edge_factor=16, seed=42)),
+    ("sbm2k", lambda: graphs.sbm(communities=2048, seed=3, val_seed=3)),
+    ("gridhubs", lambda: graphs.grid_hubs(side=256, hubs=8, hub_degree=20000, seed=6, val_seed=6)),
+    ("rand", lambda: graphs.random_csr(1000, 3000, 0.01, seed=5)),
+]
+
+OPTIONS = [
+    ("default", {}),
+    ("tiles_kept", {"window_row_cap": 1 << 30}),
+    ("split16", {"xcd_split": 16, "window_row_cap": 1 << 30}),
+    ("no_tiles", {"mfma_tc": False, "mfma_sptc": False}),
+    ("no_split", {"xcd_split": -1}),
+]
+
+_cache = {}
+
+
+def graph(name, gen):
+    if name not in _cache:
+        g = gen()
+        _cache[name] = (g, trspmm.build_format(g.rowptr, g.col, g.val))
+    return _cache[name]
+
+
+def compare(f, m, n, Bh, opts, what):
+    dev = trspmm.Plan.from_format(f, m, n, **opts)
+    host = trspmm.Plan.from_format(f, m, n, host_lowering=True, **opts)
+    sd, sh = dev.stats(), host.stats()
+    assert sd["device_lowered"] == 1 and sh["device_lowered"] == 0, what
+    sd.pop("device_lowered")
+    sh.pop("device_lowered")
+    assert sd == sh, f"{what}: stats differ\n device {sd}\n host   {sh}"
+    Cd, Ch = run_plan(dev, Bh), run_plan(host, Bh)
+    assert np.array_equal(Cd, Ch), f"{what}: outputs differ (max |d| {np.nanmax(np.abs(Cd - Ch))})"
+    return Cd, sd
+
+
+@pytest.mark.parametrize("oname,opts", OPTIONS, ids=[o[0] for o in OPTIONS])
+@pytest.mark.parametrize("name,gen", GRAPHS, ids=[g[0] for g in GRAPHS])
+def test_device_lowering_equals_host_lowering(name, gen, oname, opts):
+    say("device lowering", name, oname)
+    g, f = graph(name, gen)
+    Bh = graphs.dense_operand(g.n, 64, seed=21)
+    C, s = compare(f, g.m, g.n, Bh, opts, f"{name}/{oname}")
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m)
+    e = osp.spmm_error(C, R)
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, f"{name}/{oname}: {e}"
+    say("  stats", s)
+
+
+def test_device_lowering_exercises_tiles_and_split_rows():
+    """The option sets above reach both device kernels' branches: kept tiles whose entries are
+    flagged out of their rows, and split rows scattered into XCD sub-rows."""
+    g, f = graph("sbm2k", GRAPHS[2][1])
+    s = trspmm.Plan.from_format(f, g.m, g.n, window_row_cap=1 << 30).stats()
+    assert s["device_lowered"] == 1 and s["mfma_tiles"] > 0 and s["mfma_nnz"] > 0
+    g, f = graph("rmat14", GRAPHS[1][1])
+    s = trspmm.Plan.from_format(f, g.m, g.n, xcd_split=16, window_row_cap=1 << 30).stats()
+    assert s["device_lowered"] == 1 and s["split_rows"] > 0 and s["mfma_tiles"] > 0
+
+
+@pytest.mark.parametrize("extra", [-7, 5])
+def test_device_lowering_with_other_row_counts(extra):
+    """m below the input's rows drops the rows beyond it; m above adds empty rows."""
+    g, f = graph("sbm2k", GRAPHS[2][1])
+    m = g.m + extra
+    say("device lowering m =", m)
+    Bh = graphs.dense_operand(g.n, 32, seed=22)
+    C, _ = compare(f, m, g.n, Bh, {"window_row_cap": 1 << 30}, f"m={m}")
+    R = osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=min(m, g.m))
+    assert np.array_equal(C[g.m:], np.zeros_like(C[g.m:]))
+    e = osp.spmm_error(C[: min(m, g.m)], R[: min(m, g.m)])
+    assert e["elementwise_ok"], e
+
+
+def test_device_lowering_rejects_columns_outside_n():
+    """Columns >= n: the same TRS_ERANGE as the host lowering, before any device work."""
+    g, f = graph("rand", GRAPHS[4][1])
+    for host in (False, True):
+        with pytest.raises(nat.TrsError) as ei:
+            trspmm.Plan.from_format(f, g.m, g.n - 1, host_lowering=host)
+        assert ei.value.code == 5
+
+
+def test_format_read_back_lowers_on_host(tmp_path):
+    """A format written and read back has no input CSR: its plan is lowered on the host."""
+    g, f = graph("er4096", GRAPHS[0][1])
+    p = str(tmp_path / "er.trsf")
+    f.save(p)
+    f2 = trspmm.Format.load(p)
+    s = trspmm.Plan.from_format(f2, g.m, g.n).stats()
+    assert s["device_lowered"] == 0
+    Bh = graphs.dense_operand(g.n, 64, seed=23)
+    assert np.array_equal(run_plan(trspmm.Plan.from_format(f2, g.m, g.n), Bh),
+                          run_plan(trspmm.Plan.from_format(f, g.m, g.n), Bh))

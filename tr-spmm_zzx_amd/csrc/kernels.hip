@@ -26,6 +26,7 @@
 //                   that is not a multiple of 8.
 #include <hip/hip_runtime.h>
 
+#include "half.hpp"
 #include "kernels.hpp"
 
 namespace trs {
@@ -1193,6 +1194,90 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------------
+// Device-side plan lowering.
+
+// One workgroup per tile, one thread per (row, column) slot: binary search of the column in the
+// CSR row (columns ascending) and mark the entry; an entry counts when its flag was clear.
+__global__ __launch_bounds__(256) void k_mark_tile_entries(const TileEntries* __restrict__ tiles, int32_t m,
+                                                           const int32_t* __restrict__ rowptr,
+                                                           const int32_t* __restrict__ col,
+                                                           uint32_t* __restrict__ flag_words,
+                                                           uint32_t* __restrict__ marked) {
+  const TileEntries& t = tiles[blockIdx.x];
+  const int r = threadIdx.x >> 4, k = threadIdx.x & 15;
+  const int row = t.row0 + r;
+  if (!((t.present[r >> 2] >> ((r & 3) * 16 + k)) & 1) || row >= m) return;
+  const int32_t c = t.cols[k];
+  int lo = rowptr[row], hi = rowptr[row + 1];
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (col[mid] < c) lo = mid + 1;
+    else hi = mid;
+  }
+  if (lo < rowptr[row + 1] && col[lo] == c) {
+    const uint32_t bit = 1u << ((lo & 3) * 8);
+    if (!(atomicOr(flag_words + (lo >> 2), bit) & bit)) atomicAdd(marked, 1u);
+  }
+}
+
+// Bits of `mask` below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// One wave per CSR row: 64 entries at a time, destinations from wave ballots, so each row keeps its
+// column order.
+__global__ __launch_bounds__(256) void k_place_entries(int32_t m, const int32_t* __restrict__ rowptr,
+                                                       const int32_t* __restrict__ col,
+                                                       const float* __restrict__ val,
+                                                       const uint8_t* __restrict__ flag,
+                                                       const int32_t* __restrict__ main_rowptr,
+                                                       const int32_t* __restrict__ split_index,
+                                                       const int32_t* __restrict__ cursor,
+                                                       int32_t* __restrict__ col_out, uint16_t* __restrict__ val_out) {
+  const int row = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  if (row >= m) return;
+  const int b = rowptr[row], e = rowptr[row + 1];
+  const int si = split_index[row];
+  if (si >= 0) {
+    int cur[kXcds];
+#pragma unroll
+    for (int x = 0; x < kXcds; ++x) cur[x] = cursor[si * kXcds + x];
+    for (int p = b; p < e; p += 64) {
+      const int q = p + lane;
+      const bool in = q < e;
+      const int32_t c = in ? col[q] : 0;
+      const int xq = xcd_of_column(c);
+      int dst = 0;
+#pragma unroll
+      for (int x = 0; x < kXcds; ++x) {
+        const uint64_t mask = __ballot(in && xq == x);
+        if (in && xq == x) dst = cur[x] + lanes_below(mask);
+        cur[x] += __popcll(mask);
+      }
+      if (in) {
+        col_out[dst] = c;
+        val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, val[q]));
+      }
+    }
+    return;
+  }
+  int out = main_rowptr[row];
+  for (int p = b; p < e; p += 64) {
+    const int q = p + lane;
+    const bool keep = q < e && !(flag && flag[q]);
+    const uint64_t mask = __ballot(keep);
+    if (keep) {
+      const int dst = out + lanes_below(mask);
+      col_out[dst] = col[q];
+      val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, val[q]));
+    }
+    out += __popcll(mask);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
 }
@@ -1203,6 +1288,23 @@ hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
   hipLaunchKernelGGL(k_zero_fill, dim3((unsigned)blocks), dim3(256), 0, stream, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_mark_tile_entries(const TileEntries* tiles, int32_t ntiles, int32_t m, const int32_t* rowptr,
+                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, hipStream_t stream) {
+  if (ntiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_mark_tile_entries, dim3((unsigned)ntiles), dim3(256), 0, stream, tiles, m, rowptr, col,
+                     flag_words, marked);
+  return hipGetLastError();
+}
+
+hipError_t launch_place_entries(int32_t m, const int32_t* rowptr, const int32_t* col, const float* val,
+                                const uint8_t* flag, const int32_t* main_rowptr, const int32_t* split_index,
+                                const int32_t* cursor, int32_t* col_out, uint16_t* val_out, hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_place_entries, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, stream, m, rowptr, col, val, flag,
+                     main_rowptr, split_index, cursor, col_out, val_out);
   return hipGetLastError();
 }
 

@@ -24,7 +24,7 @@ constexpr int kWideFixupSlots = 16;
 constexpr int kXcds = 8;
 // XCD whose L2 serves column c's B row in the SpMM column split: a multiplicative hash spreads hot
 // and cold columns evenly over the XCDs.
-inline int xcd_of_column(int32_t c) { return (int)(((uint32_t)c * 2654435761u) >> 29); }
+__host__ __device__ inline int xcd_of_column(int32_t c) { return (int)(((uint32_t)c * 2654435761u) >> 29); }
 
 // A window handled by the MFMA window kernel: 16 output rows starting at row0 (rows >= m are
 // dropped), dense 16x16 fp16 tiles [tile_begin, tile_end), plus that window's residual rows.
@@ -86,6 +86,22 @@ struct DevicePlan {
 // SDDMM runs a plan's split part from this feature width on (narrower rows measured faster
 // unsplit).
 constexpr int kSddmmSplitMinK = 128;
+
+// Device-side plan lowering (the residual of an SpMM plan built from the input CSR the format keeps).
+// A dense tile's stored entries: rows row0 + r (r < 16), columns cols[k]; bit (r % 4) * 16 + k of
+// present[r / 4] marks entry (r, k).
+struct TileEntries { int32_t row0; int32_t cols[16]; int32_t pad[3]; uint64_t present[4]; };
+// Byte e of the flag words (little-endian) = 1 for every CSR entry e (rows < m, columns ascending)
+// that a tile stores; *marked (zeroed by the caller) counts the entries flagged, each once.
+hipError_t launch_mark_tile_entries(const TileEntries* tiles, int32_t ntiles, int32_t m, const int32_t* rowptr,
+                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, hipStream_t stream);
+// Entries of CSR rows [0, m) into the plan's entry arrays: a row with split_index[r] = i >= 0 is
+// scattered by the XCD of each column to cursor[i * kXcds + x] onward (column order kept); any
+// other row goes, without its flagged entries (flag may be null), to main_rowptr[r] onward.
+// Values are rounded to fp16.
+hipError_t launch_place_entries(int32_t m, const int32_t* rowptr, const int32_t* col, const float* val,
+                                const uint8_t* flag, const int32_t* main_rowptr, const int32_t* split_index,
+                                const int32_t* cursor, int32_t* col_out, uint16_t* val_out, hipStream_t stream);
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,

@@ -98,6 +98,9 @@ struct Lowering {
   struct Tile { int32_t row0; int32_t cols[16]; float a[256]; uint64_t present[4]; int nnz; };
   std::vector<Tile> tiles;
   Status st;
+  // Tiles only: entries outside tiles are not collected (the device lowering takes the residual
+  // from the input CSR instead).
+  bool tiles_only = false;
 
   bool check_col(int64_t c) {
     if (c < 0 || c >= n) {
@@ -107,6 +110,7 @@ struct Lowering {
     return true;
   }
   void add(int64_t r, int64_t c, float v) {
+    if (tiles_only) return;
     if (r < 0 || r >= m) return;   // reference kernels drop rows >= mOri
     if (!check_col(c)) return;
     row.push_back((int32_t)r);
@@ -222,6 +226,7 @@ void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const i
   for (auto& q : part) {
     q.m = L.m;
     q.n = L.n;
+    q.tiles_only = L.tiles_only;
   }
   parallel_parts(T, nwin, 0, [&](int t) { return wcut[t]; }, [&](int64_t wb, int64_t we, int t) {
     lower_groups_range(part[t], s_col, s_val, s_pos, groups, s_win, s_off, wb, we, window, to_mfma, min_fill);
@@ -240,6 +245,7 @@ void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, c
                         bool to_mfma, float min_fill) {
   auto group_row0 = [&](int64_t g, int64_t w) { return (int64_t)(s_win ? s_win[g] : w) * window; };
   auto emit_group = [&](int64_t g, int64_t row0) {
+    if (L.tiles_only) return;
     for (int lr = 0; lr < window; ++lr)
       for (int q = 0; q < 2; ++q) {
         const int p = s_pos[(g * window + lr) * 2 + q];
@@ -251,6 +257,7 @@ void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, c
       }
   };
   if (!s_off || !to_mfma || window != 16) {
+    if (L.tiles_only) return;
     if (s_off) {
       for (int64_t w = w_begin; w < w_end && L.st.ok(); ++w)
         for (int64_t g = s_off[w]; g < s_off[w + 1]; ++g) emit_group(g, group_row0(g, w));
@@ -356,9 +363,13 @@ struct Blob {
   size_t total = 0;
   template <class T>
   size_t add(const std::vector<T>& v) {
+    return add_raw(v.data(), v.size() * sizeof(T));
+  }
+  // src = nullptr: a region the device fills (left as allocated)
+  size_t add_raw(const void* src, size_t bytes) {
     const size_t off = (total + 255) & ~size_t(255);
-    pieces.push_back({v.data(), off, v.size() * sizeof(T)});
-    total = off + v.size() * sizeof(T);
+    pieces.push_back({src, off, bytes});
+    total = off + bytes;
     return off;
   }
   // 256 bytes past the last array: kernels may read whole 16-byte chunks that end past an array
@@ -382,13 +393,122 @@ struct Blob {
 // deterministic.  SDDMM sub-rows are copies of the split rows' column ids, with the output index
 // of each entry (x_pos); since the split only pays from K = 128 on, an SDDMM plan also keeps the
 // unsplit task list of all rows (full) for narrower widths.
+//
+// The work is split in three: place_entries decides where every residual entry goes (from the
+// row lengths and the split rows' columns alone), move_entries puts them there (on the host here;
+// the device lowering does it with kernels), build_tasks cuts the placed rows into tasks.
+
+// Where the residual entries go in the plan's entry arrays.
+struct Placement {
+  bool compact = false;               // SpMM: split rows leave the main part (else they stay, SDDMM)
+  std::vector<int32_t> main_rowptr;   // [m + 1] main part
+  std::vector<uint8_t> split;         // per row
+  std::vector<int32_t> split_rows;    // ascending
+  std::vector<int32_t> cursor;        // [split row i][XCD x]: first position of sub-row (i, x), -1 = none
+  std::vector<int32_t> xrowptr;       // [J + 1] sub-rows, XCD-major
+  std::vector<int32_t> sub_row;       // [J] row of each sub-row
+  int32_t xfirst[trs::kXcds + 1] = {};
+  int64_t total = 0;                  // length of the plan's entry arrays
+  int32_t J() const { return (int32_t)sub_row.size(); }
+};
+
+// rowptr: the residual CSR's row pointers; owned: per 16-row block (empty = none).  The columns of
+// a split row r are col[col_rowptr[r] ..] (col_rowptr = rowptr for the residual CSR itself; the
+// input CSR's row pointers when the residual is built on the device, where split rows -- owned by
+// no window, so no tile took entries from them -- equal their input rows).
+Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, const int32_t* col_rowptr, int32_t m,
+                        int32_t n, const std::vector<uint8_t>& owned, bool compact, int32_t split_min) {
+  Placement P;
+  P.compact = compact;
+  const int64_t nent = rowptr[m];
+  P.split.assign((size_t)m, 0);
+  if (split_min > 0 && n > 0)
+    for (int32_t r = 0; r < m; ++r)
+      if (!(!owned.empty() && owned[r / 16]) && rowptr[r + 1] - rowptr[r] >= split_min) {
+        P.split[r] = 1;
+        P.split_rows.push_back(r);
+      }
+  const size_t ns = P.split_rows.size();
+  // entries per (split row, XCD), counted by the column hash on a few threads
+  std::vector<int32_t> cnt(ns * trs::kXcds, 0);
+  parallel_parts(lowering_threads(), (int64_t)ns, 256, [&](int t) { return (int64_t)ns * t / lowering_threads(); },
+                 [&](int64_t b, int64_t e, int) {
+                   for (int64_t i = b; i < e; ++i) {
+                     const int32_t r = P.split_rows[i];
+                     const int32_t* c = col + col_rowptr[r];
+                     for (int32_t q = 0; q < rowptr[r + 1] - rowptr[r]; ++q) cnt[i * trs::kXcds + trs::xcd_of_column(c[q])]++;
+                   }
+                 });
+  P.main_rowptr.resize((size_t)m + 1);
+  int64_t w = 0;
+  for (int32_t r = 0; r < m; ++r) {
+    P.main_rowptr[r] = (int32_t)w;
+    if (!(compact && P.split[r])) w += rowptr[r + 1] - rowptr[r];
+  }
+  P.main_rowptr[m] = (int32_t)w;
+  if (!compact) w = nent;   // SDDMM: copies after the whole main part
+  P.cursor.assign(ns * trs::kXcds, -1);
+  for (int y = 0; y < trs::kXcds; ++y) {
+    P.xfirst[y] = (int32_t)P.sub_row.size();
+    for (size_t i = 0; i < ns; ++i) {
+      const int32_t c = cnt[i * trs::kXcds + y];
+      if (c == 0) continue;
+      P.cursor[i * trs::kXcds + y] = (int32_t)w;
+      P.sub_row.push_back(P.split_rows[i]);
+      P.xrowptr.push_back((int32_t)w);
+      w += c;
+    }
+  }
+  P.xfirst[trs::kXcds] = (int32_t)P.sub_row.size();
+  P.xrowptr.push_back((int32_t)w);
+  P.total = w;
+  return P;
+}
+
+// The entries of the residual CSR (rowptr / col / val) in their placed order: col_out / val_out
+// of P.total entries; x_pos (SDDMM) gets the residual index of each sub-row entry.
+void move_entries(const Placement& P, const std::vector<int32_t>& rowptr, const int32_t* col, const uint16_t* val,
+                  int32_t m, std::vector<int32_t>& col_out, std::vector<uint16_t>* val_out,
+                  std::vector<int32_t>* x_pos) {
+  const int64_t nent = rowptr[m];
+  col_out.resize((size_t)P.total);
+  if (val_out) val_out->resize((size_t)P.total);
+  if (x_pos) x_pos->resize((size_t)(P.total - (P.compact ? 0 : nent)));
+  // main part, in row order
+  parallel_parts(lowering_threads(), (int64_t)m, 1 << 14, [&](int t) { return (int64_t)m * t / lowering_threads(); },
+                 [&](int64_t rb, int64_t re, int) {
+                   for (int64_t r = rb; r < re; ++r) {
+                     if (P.compact && P.split[r]) continue;
+                     const int32_t d = P.main_rowptr[r];
+                     for (int32_t q = rowptr[r]; q < rowptr[r + 1]; ++q) {
+                       col_out[d + q - rowptr[r]] = col[q];
+                       if (val_out) (*val_out)[d + q - rowptr[r]] = val[q];
+                     }
+                   }
+                 });
+  // sub-rows: each split row's entries by the XCD of their column, in column order
+  const size_t ns = P.split_rows.size();
+  const int64_t xbase = P.compact ? 0 : nent;
+  parallel_parts(lowering_threads(), (int64_t)ns, 256, [&](int t) { return (int64_t)ns * t / lowering_threads(); },
+                 [&](int64_t b, int64_t e, int) {
+                   int32_t cur[trs::kXcds];
+                   for (int64_t i = b; i < e; ++i) {
+                     std::copy(P.cursor.begin() + i * trs::kXcds, P.cursor.begin() + (i + 1) * trs::kXcds, cur);
+                     const int32_t r = P.split_rows[i];
+                     for (int32_t q = rowptr[r]; q < rowptr[r + 1]; ++q) {
+                       const int32_t o = cur[trs::xcd_of_column(col[q])]++;
+                       col_out[o] = col[q];
+                       if (val_out) (*val_out)[o] = val[q];
+                       if (x_pos) (*x_pos)[o - xbase] = q;
+                     }
+                   }
+                 });
+}
+
 struct Tasks {
   std::vector<trs::Task> tasks;      // main part
   std::vector<trs::Task> xtasks;     // split part: queue x = xtasks [xq[x], xq[x + 1])
   int32_t xq[trs::kXcds + 1] = {};
-  std::vector<int32_t> xrowptr;      // sub-row j: entries [xrowptr[j], xrowptr[j + 1]) of col / val
-  std::vector<int32_t> x_pos;        // SDDMM: output index of each sub-row entry
-  std::vector<int32_t> sub_row;      // SDDMM: the row sub-row j belongs to
   std::vector<trs::Task> full;       // SDDMM with a split part: the unsplit layout of every row
   std::vector<trs::Fixup> fix, wfix; // SpMM: {row, first index into slot_list, slots}
   std::vector<int32_t> slot_list;
@@ -399,12 +519,23 @@ struct Tasks {
   Status st;
 };
 
-// rowptr / col / val: the residual CSR (val null for SDDMM).  SpMM moves the split rows' entries
-// out of the main part (their main rows become empty) into the sub-rows; SDDMM keeps the main part
-// whole (outputs follow its order) and appends copies of the split rows' column ids.
-Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::vector<uint16_t>* val, int32_t m,
-                  int32_t n, const std::vector<uint8_t>& owned, bool with_fixup, int32_t split_min,
-                  const trs_plan_options& opt) {
+// Longest tasks first (a stable counting sort on the entry count, which never exceeds the piece
+// length): a workgroup's lane groups then carry tasks of similar length, so none idles while a
+// longer one finishes (R-MAT K = 32 / 64 / 128: -9% / -11% / -5%).
+void sort_longest_first(std::vector<trs::Task>::iterator first, std::vector<trs::Task>::iterator last) {
+  int32_t most = 0;
+  for (auto it = first; it != last; ++it) most = std::max(most, it->nz_end - it->nz_begin);
+  std::vector<int64_t> start((size_t)most + 2, 0);
+  for (auto it = first; it != last; ++it) start[(size_t)(most - (it->nz_end - it->nz_begin)) + 1]++;
+  for (size_t i = 1; i < start.size(); ++i) start[i] += start[i - 1];
+  std::vector<trs::Task> out((size_t)(last - first));
+  for (auto it = first; it != last; ++it) out[(size_t)start[(size_t)(most - (it->nz_end - it->nz_begin))]++] = *it;
+  std::copy(out.begin(), out.end(), first);
+}
+
+// Tasks over the placed rows (the residual row lengths are rowptr's, before placement).
+Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_t m, const std::vector<uint8_t>& owned,
+                  bool with_fixup, const trs_plan_options& opt) {
   Tasks T;
   const int64_t nent = rowptr[m];
   // Entries per packed task: short rows want small tasks (more lane groups in flight, fewer row
@@ -421,103 +552,7 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
   const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
   const int rows_cap = trs::kTaskRows;
   auto is_owned = [&](int32_t r) { return !owned.empty() && owned[r / 16]; };
-
-  // split rows and the column cut points of the XCD ranges, balanced by the split rows' entries
-  std::vector<uint8_t> split((size_t)m, 0);
-  int64_t split_entries = 0;
-  if (split_min > 0 && n > 0)
-    for (int32_t r = 0; r < m; ++r)
-      if (!is_owned(r) && rowptr[r + 1] - rowptr[r] >= split_min) {
-        split[r] = 1;
-        split_entries += rowptr[r + 1] - rowptr[r];
-      }
-  struct Sub { int32_t row; };
-  std::vector<Sub> subs;                 // XCD-major
-  int32_t xfirst[trs::kXcds + 1] = {};
-  if (split_entries > 0) {
-    std::vector<int32_t> rows_split;
-    for (int32_t r = 0; r < m; ++r)
-      if (split[r]) rows_split.push_back(r);
-    const size_t ns = rows_split.size();
-    if (with_fixup) {
-      // SpMM: a column's XCD is a hash of its index, so every XCD gets an even share of hot and
-      // cold columns (contiguous ranges leave the XCD of the rarely used columns with most of the
-      // misses: measured on R-MAT, the other XCDs then wait for it).  Sub-rows are copies, so the
-      // scattered entries cost nothing more.
-      std::vector<int32_t> cnt(ns * trs::kXcds, 0);
-      for (size_t i = 0; i < ns; ++i)
-        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e)
-          cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
-      std::vector<int32_t> rp2((size_t)m + 1), col2((size_t)nent);
-      std::vector<uint16_t> val2((size_t)nent);
-      int64_t w = 0;
-      for (int32_t r = 0; r < m; ++r) {
-        rp2[r] = (int32_t)w;
-        if (split[r]) continue;
-        for (int32_t e = rowptr[r]; e < rowptr[r + 1]; ++e, ++w) {
-          col2[w] = col[e];
-          val2[w] = (*val)[e];
-        }
-      }
-      rp2[m] = (int32_t)w;
-      // sub-row starts, XCD-major; cnt becomes each (row, XCD) write cursor
-      for (int y = 0; y < trs::kXcds; ++y) {
-        xfirst[y] = (int32_t)subs.size();
-        for (size_t i = 0; i < ns; ++i) {
-          int32_t& c = cnt[i * trs::kXcds + y];
-          if (c == 0) { c = -1; continue; }
-          subs.push_back({rows_split[i]});
-          T.xrowptr.push_back((int32_t)w);
-          const int32_t len = c;
-          c = (int32_t)w;
-          w += len;
-        }
-      }
-      xfirst[trs::kXcds] = (int32_t)subs.size();
-      T.xrowptr.push_back((int32_t)w);
-      for (size_t i = 0; i < ns; ++i)
-        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e) {
-          const int32_t q = cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
-          col2[q] = col[e];
-          val2[q] = (*val)[e];
-        }
-      rowptr.swap(rp2);
-      col.swap(col2);
-      val->swap(val2);
-    } else {
-      // SDDMM: the same hashed split; the main part stays whole (its outputs are the identity) and
-      // the sub-rows are copies of the split rows' column ids, each with its output index
-      std::vector<int32_t> cnt(ns * trs::kXcds, 0);
-      for (size_t i = 0; i < ns; ++i)
-        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e)
-          cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
-      int64_t w = nent;
-      col.resize((size_t)nent + (size_t)split_entries);
-      T.x_pos.resize((size_t)split_entries);
-      for (int y = 0; y < trs::kXcds; ++y) {
-        xfirst[y] = (int32_t)subs.size();
-        for (size_t i = 0; i < ns; ++i) {
-          int32_t& c = cnt[i * trs::kXcds + y];
-          if (c == 0) { c = -1; continue; }
-          subs.push_back({rows_split[i]});
-          T.xrowptr.push_back((int32_t)w);
-          T.sub_row.push_back(rows_split[i]);
-          const int32_t len = c;
-          c = (int32_t)w;
-          w += len;
-        }
-      }
-      xfirst[trs::kXcds] = (int32_t)subs.size();
-      T.xrowptr.push_back((int32_t)w);
-      for (size_t i = 0; i < ns; ++i)
-        for (int32_t e = rowptr[rows_split[i]]; e < rowptr[rows_split[i] + 1]; ++e) {
-          const int32_t q = cnt[i * trs::kXcds + trs::xcd_of_column(col[e])]++;
-          col[q] = col[e];
-          T.x_pos[q - nent] = e;
-        }
-    }
-  }
-  const int32_t J = (int32_t)subs.size();
+  const int32_t J = P.J();
   if (with_fixup) T.slots = J;   // sub-row j sums into slot j; piece slots follow
 
   // equal pieces of at most piece_max entries of [b, e) of (sub-)row r
@@ -554,67 +589,61 @@ Tasks build_tasks(std::vector<int32_t>& rowptr, std::vector<int32_t>& col, std::
     return r1;
   };
 
-  // main part (skip_split: without the split rows); longest tasks first, so that a workgroup's
-  // lane groups carry tasks of similar length and none idles while a longer one finishes (R-MAT
-  // K = 32 / 64 / 128: -9% / -11% / -5%)
+  // main part (skip_split: without the split rows), longest tasks first
+  const std::vector<int32_t>& rp = P.main_rowptr;
   auto build_main = [&](bool skip_split, std::vector<trs::Task>& outv) {
     std::vector<trs::Task> pieces, packed;
     std::vector<int32_t> sl;
     int32_t r = 0;
     while (r < m) {
       if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
-      if (skip_split && split[r]) { ++r; continue; }
-      const int32_t deg = rowptr[r + 1] - rowptr[r];
+      if (skip_split && P.split[r]) { ++r; continue; }
+      const int32_t deg = rp[r + 1] - rp[r];
       if (deg > piece_max) {
         sl.clear();
-        cut_pieces(r, rowptr[r], rowptr[r + 1], pieces, &sl);
+        cut_pieces(r, rp[r], rp[r + 1], pieces, &sl);
         add_fixup(r, sl);
         ++r;
         continue;
       }
-      const int32_t r1 = pack(rowptr, r, m, [&](int32_t q) { return is_owned(q) || (skip_split && split[q] != 0); });
-      packed.push_back({r, r1, rowptr[r], rowptr[r1]});
+      const int32_t r1 = pack(rp, r, m, [&](int32_t q) { return is_owned(q) || (skip_split && P.split[q] != 0); });
+      packed.push_back({r, r1, rp[r], rp[r1]});
       r = r1;
     }
     outv.reserve(pieces.size() + packed.size());
     outv.insert(outv.end(), pieces.begin(), pieces.end());
     outv.insert(outv.end(), packed.begin(), packed.end());
-    std::stable_sort(outv.begin(), outv.end(),
-                     [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
+    sort_longest_first(outv.begin(), outv.end());
   };
   build_main(true, T.tasks);
   if (!with_fixup && J > 0) build_main(false, T.full);   // SDDMM: no slots, no fixups to repeat
 
-  // split part: per range, pieces of long sub-rows and runs of the others
+  // split part: per XCD, pieces of long sub-rows and runs of the others, longest first
   if (J > 0) {
     std::vector<std::vector<int32_t>> piece_slots((size_t)J);
     for (int y = 0; y < trs::kXcds; ++y) {
       T.xq[y] = (int32_t)T.xtasks.size();
-      int32_t j = xfirst[y];
-      while (j < xfirst[y + 1]) {
-        const int32_t d = T.xrowptr[j + 1] - T.xrowptr[j];
+      int32_t j = P.xfirst[y];
+      while (j < P.xfirst[y + 1]) {
+        const int32_t d = P.xrowptr[j + 1] - P.xrowptr[j];
         if (d > piece_max) {
-          cut_pieces(j, T.xrowptr[j], T.xrowptr[j + 1], T.xtasks, &piece_slots[j]);
+          cut_pieces(j, P.xrowptr[j], P.xrowptr[j + 1], T.xtasks, &piece_slots[j]);
           ++j;
           continue;
         }
-        const int32_t j1 = pack(T.xrowptr, j, xfirst[y + 1], [&](int32_t q) { return false; });
-        T.xtasks.push_back({j, j1, T.xrowptr[j], T.xrowptr[j1]});
+        const int32_t j1 = pack(P.xrowptr, j, P.xfirst[y + 1], [&](int32_t) { return false; });
+        T.xtasks.push_back({j, j1, P.xrowptr[j], P.xrowptr[j1]});
         j = j1;
       }
+      sort_longest_first(T.xtasks.begin() + T.xq[y], T.xtasks.end());
     }
     T.xq[trs::kXcds] = (int32_t)T.xtasks.size();
-    // longest tasks first in each queue: the lane groups of a workgroup then carry tasks of
-    // similar length, so none idles for long while a long piece finishes
-    for (int y = 0; y < trs::kXcds; ++y)
-      std::stable_sort(T.xtasks.begin() + T.xq[y], T.xtasks.begin() + T.xq[y + 1],
-                       [](const trs::Task& a, const trs::Task& b) { return a.nz_end - a.nz_begin > b.nz_end - b.nz_begin; });
     if (with_fixup) {
-      // a split row's slots in range order: sub-row j's own slot, or its pieces' slots
+      // a split row's slots in XCD order: sub-row j's own slot, or its pieces' slots
       std::vector<int32_t> first((size_t)m, -1);
       std::vector<std::vector<int32_t>> rs;
       for (int32_t jj = 0; jj < J; ++jj) {
-        const int32_t row = subs[jj].row;
+        const int32_t row = P.sub_row[jj];
         if (first[row] < 0) {
           first[row] = (int32_t)rs.size();
           rs.emplace_back();
@@ -681,6 +710,16 @@ void residual_csr(const Lowering& L, bool keep_order, std::vector<int32_t>& rowp
   });
 }
 
+// Blob pieces with a source into device memory at dmem.
+bool copy_pieces(const Blob& blob, void* dmem) {
+  for (const auto& pc : blob.pieces) {
+    if (pc.bytes == 0 || !pc.src) continue;
+    if (hipMemcpy(static_cast<unsigned char*>(dmem) + pc.off, pc.src, pc.bytes, hipMemcpyHostToDevice) != hipSuccess)
+      return false;
+  }
+  return true;
+}
+
 // One hipMalloc holding the whole plan, filled array by array.
 Status upload(const Blob& blob, trs_plan*& P) {
   P = new trs_plan();
@@ -697,22 +736,127 @@ Status upload(const Blob& blob, trs_plan*& P) {
     return fail(TRS_ENOMEM, "hipMalloc of " + std::to_string(blob.size()) + " plan bytes failed");
   }
   P->dbytes = blob.size();
-  for (const auto& pc : blob.pieces) {
-    if (pc.bytes == 0) continue;
-    if (hipMemcpy(static_cast<unsigned char*>(P->dmem) + pc.off, pc.src, pc.bytes, hipMemcpyHostToDevice) !=
-        hipSuccess) {
-      delete P;
-      P = nullptr;
-      return fail(TRS_EDEVICE, "plan upload failed");
-    }
+  if (!copy_pieces(blob, P->dmem)) {
+    delete P;
+    P = nullptr;
+    return fail(TRS_EDEVICE, "plan upload failed");
   }
   return Status{};
 }
 
-// Residual CSR + tasks + MFMA windows -> device plan.
-Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
+// Internal status of the device lowering: the format's tiles and its input CSR disagree (a tile
+// entry the CSR does not hold, or two tiles holding one entry) or its temporaries could not be
+// allocated; the caller then lowers on the host.
+constexpr int kLowerOnHost = -100;
+
+// Entries stored by tile t, rows < m: the present bits (tile_add sets each once per entry).
+int64_t tile_present(const Lowering::Tile& t) {
+  int64_t c = 0;
+  for (int i = 0; i < 4; ++i) c += __builtin_popcountll(t.present[i]);
+  return c;
+}
+
+// Tile entries in row r (0..15) of tile t.
+int tile_row_entries(const Lowering::Tile& t, int r) {
+  return __builtin_popcountll((t.present[r / 4] >> ((r % 4) * 16)) & 0xffffull);
+}
+
+// Device half of the device lowering: the input CSR of rows [0, m) goes up once, the kept tiles'
+// entries are flagged in it, and every row is written to its placed position -- main rows without
+// their flagged entries, split rows scattered into their XCD sub-rows -- as col_out / val_out
+// (main_rowptr, col_out, val_out: device addresses inside the plan).  Temporaries live in one
+// allocation freed before returning.
+Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowering::Tile>& tiles,
+                          int64_t expect_marked, const Placement& PL, const int32_t* main_rowptr, int32_t* col_out,
+                          uint16_t* val_out) {
+  const int32_t rows = std::min(m, f.rows);
+  const int64_t cnnz = f.csr_rowptr[rows];
+  std::vector<int32_t> rp((size_t)m + 1, (int32_t)cnnz);
+  std::copy(f.csr_rowptr.begin(), f.csr_rowptr.begin() + rows + 1, rp.begin());
+  std::vector<trs::TileEntries> te(tiles.size());
+  for (size_t i = 0; i < tiles.size(); ++i) {
+    te[i] = trs::TileEntries{};
+    te[i].row0 = tiles[i].row0;
+    std::copy(tiles[i].cols, tiles[i].cols + 16, te[i].cols);
+    std::copy(tiles[i].present, tiles[i].present + 4, te[i].present);
+  }
+  std::vector<int32_t> split_index((size_t)m, -1);
+  for (size_t i = 0; i < PL.split_rows.size(); ++i) split_index[PL.split_rows[i]] = (int32_t)i;
+  Blob tmp;
+  const size_t o_rp = tmp.add(rp);
+  const size_t o_col = tmp.add_raw(f.csr_col.data(), (size_t)cnnz * 4);
+  const size_t o_val = tmp.add_raw(f.csr_val.data(), (size_t)cnnz * 4);
+  const size_t o_te = tmp.add(te);
+  const size_t o_si = tmp.add(split_index);
+  const size_t o_cur = tmp.add(PL.cursor);
+  // entry flags as bytes of 32-bit words (the marking kernel sets them with word atomics), then
+  // the count of entries marked
+  const size_t flag_bytes = ((size_t)cnnz + 3) & ~size_t(3);
+  const size_t o_flag = tmp.add_raw(nullptr, flag_bytes + 256);
+  void* dmem = nullptr;
+  if (hipMalloc(&dmem, tmp.size()) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(kLowerOnHost, "device lowering temporaries: hipMalloc failed");
+  }
+  unsigned char* base = static_cast<unsigned char*>(dmem);
+  auto done = [&](Status st) {
+    (void)hipFree(dmem);
+    return st;
+  };
+  if (!copy_pieces(tmp, dmem) || hipMemset(base + o_flag, 0, flag_bytes + 256) != hipSuccess)
+    return done(fail(TRS_EDEVICE, "device lowering: upload failed"));
+  const int32_t* d_rp = reinterpret_cast<const int32_t*>(base + o_rp);
+  const int32_t* d_col = reinterpret_cast<const int32_t*>(base + o_col);
+  uint32_t* d_flag = reinterpret_cast<uint32_t*>(base + o_flag);
+  uint32_t* d_marked = reinterpret_cast<uint32_t*>(base + o_flag + flag_bytes);
+  if (!tiles.empty()) {
+    if (trs::launch_mark_tile_entries(reinterpret_cast<const trs::TileEntries*>(base + o_te), (int32_t)tiles.size(), m,
+                                      d_rp, d_col, d_flag, d_marked, nullptr) != hipSuccess)
+      return done(fail(TRS_EDEVICE, "device lowering: tile marking launch failed"));
+    uint32_t marked = 0;
+    if (hipMemcpy(&marked, d_marked, 4, hipMemcpyDeviceToHost) != hipSuccess)
+      return done(fail(TRS_EDEVICE, "device lowering: tile marking failed"));
+    // every kept tile entry found once in the CSR: then each row loses exactly its tile entries
+    // and the placement below stays inside the rows' ranges
+    if ((int64_t)marked != expect_marked)
+      return done(fail(kLowerOnHost, "device lowering: tiles and input CSR disagree"));
+  }
+  if (trs::launch_place_entries(m, d_rp, d_col, reinterpret_cast<const float*>(base + o_val),
+                                tiles.empty() ? nullptr : reinterpret_cast<const uint8_t*>(d_flag), main_rowptr,
+                                reinterpret_cast<const int32_t*>(base + o_si),
+                                reinterpret_cast<const int32_t*>(base + o_cur), col_out, val_out, nullptr) != hipSuccess ||
+      hipStreamSynchronize(nullptr) != hipSuccess)
+    return done(fail(TRS_EDEVICE, "device lowering: entry placement failed"));
+  return done(Status{});
+}
+
+// Residual CSR + tasks + MFMA windows -> device plan.  With src (the format that holds its input
+// CSR), L carries the tiles only and the residual -- the input CSR minus the kept tiles' entries --
+// is built on the device; the plan equals the host lowering's (same arrays, same statistics).
+Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const trs_format* src = nullptr) {
   if (!L.st.ok()) return L.st;
   const int32_t m = L.m;
+  // device lowering: row lengths of the input CSR (rows beyond its rows are empty)
+  std::vector<int32_t> csr_len;
+  if (src) {
+    const int32_t rows = std::min(m, src->rows);
+    const int64_t cnnz = src->csr_rowptr[rows];
+    // column range (the host lowering rejects a residual or tile column outside [0, n))
+    const int T = lowering_threads();
+    std::vector<int64_t> bad((size_t)T, INT64_MAX);
+    parallel_parts(T, cnnz, 1 << 16, [&](int t) { return cnnz * t / T; }, [&](int64_t b, int64_t e, int t) {
+      for (int64_t q = b; q < e; ++q)
+        if (src->csr_col[q] < 0 || src->csr_col[q] >= L.n) {
+          bad[t] = q;
+          break;
+        }
+    });
+    const int64_t q = *std::min_element(bad.begin(), bad.end());
+    if (q != INT64_MAX) L.check_col(src->csr_col[q]);
+    if (!L.st.ok()) return L.st;
+    csr_len.assign((size_t)m, 0);
+    for (int32_t r = 0; r < rows; ++r) csr_len[r] = src->csr_rowptr[r + 1] - src->csr_rowptr[r];
+  }
 
   // MFMA windows: 16-row blocks owning at least one tile (tile order inside a window kept).
   std::stable_sort(L.tiles.begin(), L.tiles.end(),
@@ -728,7 +872,18 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   const int row_cap = opt.window_row_cap > 0 ? opt.window_row_cap : 128;
   if (!L.tiles.empty()) {
     std::vector<int32_t> len((size_t)m, 0);
-    for (int32_t r : L.row) len[r]++;
+    if (src) {
+      // input row length minus the tile entries of the row
+      len = csr_len;
+      for (const auto& t : L.tiles) {
+        if (t.nnz != tile_present(t)) return fail(kLowerOnHost, "device lowering: a tile slot holds two entries");
+        for (int r = 0; r < 16 && t.row0 + r < m; ++r) len[t.row0 + r] -= tile_row_entries(t, r);
+      }
+      for (int32_t r = 0; r < m; ++r)
+        if (len[r] < 0) return fail(kLowerOnHost, "device lowering: tiles hold entries the input CSR lacks");
+    } else {
+      for (int32_t r : L.row) len[r]++;
+    }
     std::vector<uint8_t> demote(nblocks, 0);
     bool any_demote = false;
     for (int32_t b = 0; b < nblocks; ++b) {
@@ -742,6 +897,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
       for (const auto& t : L.tiles) {
         if (!demote[t.row0 / 16]) { kept.push_back(t); continue; }
         owned[t.row0 / 16] = 0;
+        if (src) continue;   // its entries stay in the input CSR
         for (int r = 0; r < 16; ++r)
           for (int k = 0; k < 16; ++k)
             if (t.cols[k] >= 0 && Lowering::tile_has(t, r, k)) L.add((int64_t)t.row0 + r, t.cols[k], t.a[r * 16 + k]);
@@ -750,14 +906,27 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
       if (!L.st.ok()) return L.st;
     }
   }
-  const int64_t nent = (int64_t)L.row.size();
-  if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
-
   // residual CSR sorted by (row, column); equal keys keep insertion order
   std::vector<int32_t> rowptr;
-  std::vector<int32_t> col(nent);
-  std::vector<uint16_t> val(nent);
-  {
+  std::vector<int32_t> col;
+  std::vector<uint16_t> val;
+  int64_t nent = 0;
+  int64_t expect_marked = 0;
+  if (src) {
+    // the input rows minus the kept tiles' entries (columns ascending, as the host sort leaves them)
+    std::vector<int32_t> len(csr_len);
+    for (const auto& t : L.tiles) {
+      expect_marked += tile_present(t);
+      for (int r = 0; r < 16 && t.row0 + r < m; ++r) len[t.row0 + r] -= tile_row_entries(t, r);
+    }
+    rowptr.assign((size_t)m + 1, 0);
+    for (int32_t r = 0; r < m; ++r) rowptr[r + 1] = rowptr[r] + len[r];
+    nent = rowptr[m];
+  } else {
+    nent = (int64_t)L.row.size();
+    if (nent > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 residual entries");
+    col.resize((size_t)nent);
+    val.resize((size_t)nent);
     std::vector<int64_t> perm;
     residual_csr(L, false, rowptr, perm);
     parallel_chunks(nent, [&](int64_t b, int64_t e, int) {
@@ -786,19 +955,24 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   // residual tasks over rows not owned by an MFMA window
   // XCD column split for SpMM (each sub-row costs a partial slot of 4 K bytes written and read back)
   const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSpmmSplitMin;
-  Tasks T = build_tasks(rowptr, col, &val, m, L.n, owned, true, split_min, opt);
+  const Placement PL = src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, owned, true, split_min)
+                           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, owned, true, split_min);
+  std::vector<int32_t> col2;
+  std::vector<uint16_t> val2;
+  if (!src) move_entries(PL, rowptr, col.data(), val.data(), m, col2, &val2, nullptr);
+  Tasks T = build_tasks(PL, rowptr, m, owned, true, opt);
   if (!T.st.ok()) return T.st;
   const int32_t slots = T.slots;
   const int64_t split_rows = T.split_rows;
 
   // one device allocation
   Blob blob;
-  const size_t o_rowptr = blob.add(rowptr);
-  const size_t o_col = blob.add(col);
-  const size_t o_val = blob.add(val);
+  const size_t o_rowptr = blob.add(PL.main_rowptr);
+  const size_t o_col = src ? blob.add_raw(nullptr, (size_t)PL.total * 4) : blob.add(col2);
+  const size_t o_val = src ? blob.add_raw(nullptr, (size_t)PL.total * 2) : blob.add(val2);
   const size_t o_tasks = blob.add(T.tasks);
   const size_t o_xtasks = blob.add(T.xtasks);
-  const size_t o_xrowptr = blob.add(T.xrowptr);
+  const size_t o_xrowptr = blob.add(PL.xrowptr);
   const size_t o_fix = blob.add(T.fix);
   const size_t o_wfix = blob.add(T.wfix);
   const size_t o_slots = blob.add(T.slot_list);
@@ -811,6 +985,15 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
     if (!us.ok()) return us;
   }
   unsigned char* base = static_cast<unsigned char*>(P->dmem);
+  if (src) {
+    const Status ds = residual_on_device(*src, m, L.tiles, expect_marked, PL,
+                                         reinterpret_cast<const int32_t*>(base + o_rowptr),
+                                         reinterpret_cast<int32_t*>(base + o_col), reinterpret_cast<uint16_t*>(base + o_val));
+    if (!ds.ok()) {
+      delete P;
+      return ds;
+    }
+  }
   trs::DevicePlan& d = P->dp;
   d.m = m;
   d.n = L.n;
@@ -862,6 +1045,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out) {
   for (const auto& w : mwin)
     for (int32_t r = w.row0; r < std::min(m, w.row0 + 16); ++r) wnnz += rowptr[r + 1] - rowptr[r];
   s.window_csr_nnz = wnnz;
+  s.device_lowered = src ? 1 : 0;
   *out = P;
   return Status{};
 }
@@ -929,17 +1113,20 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSddmmSplitMin;
   // the split part's outputs are contiguous runs of the residual order: only without tiles, whose
   // merge interleaves output positions
-  Tasks T = build_tasks(rowptr, col, nullptr, m, L.n, {}, false, te.empty() ? split_min : 0, opt);
+  const Placement PL = place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, te.empty() ? split_min : 0);
+  std::vector<int32_t> col2, x_pos;
+  move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos);
+  Tasks T = build_tasks(PL, rowptr, m, {}, false, opt);
   if (!T.st.ok()) return T.st;
 
   Blob blob;
   const size_t o_rowptr = blob.add(rowptr);
-  const size_t o_col = blob.add(col);
+  const size_t o_col = blob.add(col2);
   const size_t o_tasks = blob.add(T.tasks);
   const size_t o_xtasks = blob.add(T.xtasks);
-  const size_t o_xrowptr = blob.add(T.xrowptr);
-  const size_t o_xpos = blob.add(T.x_pos);
-  const size_t o_srow = blob.add(T.sub_row);
+  const size_t o_xrowptr = blob.add(PL.xrowptr);
+  const size_t o_xpos = blob.add(x_pos);
+  const size_t o_srow = blob.add(PL.sub_row);
   const size_t o_full = blob.add(T.full);
   const size_t o_rpos = blob.add(res_pos);
   const size_t o_trow = blob.add(tile_row0);
@@ -1028,6 +1215,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->stage = 0;
   o->occupancy = 0;
   o->xcd_split = 0;
+  o->host_lowering = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }
@@ -1040,6 +1228,19 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
     return report(fail(TRS_ENOTCANON, "trs_plan_create: input rows were not strictly increasing; the format "
                                       "arrays cannot describe duplicate or unsorted entries"));
   const trs_plan_options o = resolve(opt);
+  if (!o.host_lowering && !f->csr_rowptr.empty()) {
+    // device lowering: the tiles from the format, the residual from its input CSR
+    Lowering D;
+    D.m = m;
+    D.n = n;
+    D.tiles_only = true;
+    lower_tc(D, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
+             f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
+    lower_groups(D, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
+                 f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
+    const Status ds = finalize(D, o, out, f);
+    if (ds.code != kLowerOnHost) return report(ds);
+  }
   Lowering L;
   L.m = m;
   L.n = n;
