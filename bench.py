@@ -214,8 +214,13 @@ def bench_sddmm(args, workload, g, K):
     from trspmm import _native as nat, graphs
     t0 = time.time()
     fmt = trspmm.build_format(g.rowptr, g.col, g.val)
-    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split)
+    torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of plan_s
+    torch.cuda.synchronize()
+    t1 = time.time()
+    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering)
     st = plan.stats()
+    pre = {"build_s": round(fmt.elapsed, 3), "plan_s": round(time.time() - t1, 3),
+           "plan_lowering": "device" if st["device_lowered"] else "host"}
     del fmt
     log(f"[bench] sddmm plan {st} ({time.time() - t0:.1f}s)")
     Xh = graphs.dense_operand(g.m, K, seed=4)
@@ -263,7 +268,7 @@ def bench_sddmm(args, workload, g, K):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
             "config": {"workload": workload, "m": g.m, "n": g.n, "nnz": g.nnz, "K": K, "mfma_tiles": st["mfma_tiles"],
                        "mfma_nnz": st["mfma_nnz"], "parallelism": "none"},
-            "roofline": roof,
+            "roofline": roof, "preprocess": pre,
             "cold": {"ms_per_step": round(ms_cold, 5), "value": round(flops / (ms_cold * 1e-3) / 1e9, 2),
                      "note": "median step with a 1 GiB write before each (L2 and MALL flushed)"}}
     if not args.no_cpu_baseline:
@@ -315,7 +320,7 @@ def main():
                     help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
                          "tca-aligned keeps clusters inside 16-row windows")
     ap.add_argument("--host-lowering", action="store_true",
-                    help="build the SpMM plan's residual on the host (default: on the device from the input CSR)")
+                    help="build the plan's residual on the host (default: on the device from the input CSR)")
     ap.add_argument("--xcd-split", type=int, default=None,
                     help="plan option xcd_split (rows of >= N residual entries cut by XCD column ranges; "
                          "-1 off; default: the library's)")
@@ -355,6 +360,8 @@ def main():
     fmt = trspmm.build_format(g.rowptr, g.col, g.val)
     log(f"[bench] format built in {fmt.elapsed:.2f}s")
     pre["build_s"] = round(fmt.elapsed, 3)
+    torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of plan_s
+    torch.cuda.synchronize()
     t1 = time.time()
     plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering)
     pre["plan_s"] = round(time.time() - t1, 3)

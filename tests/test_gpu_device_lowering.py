@@ -1,12 +1,12 @@
-"""GPU: SpMM plans whose residual is built on the device from the format's input CSR.
+"""GPU: SpMM and SDDMM plans whose residual is built on the device from the format's input CSR.
 
-trs_plan_create lowers on the device when the format holds its input CSR (a format built in this
-process from canonical input): the MFMA tiles are cut from the format arrays on the host, the
-residual -- the input rows minus the kept tiles' entries, XCD sub-rows included -- is written by
-two kernels.  The plan must be the host lowering's: equal statistics and bitwise equal SpMM
-outputs, on every workload shape the host lowering is tested on (tiles kept or demoted, split
-rows, no tiles at all, more or fewer plan rows than input rows), and within the SpMM tolerance of
-the float64 CSR oracle.
+trs_plan_create / trs_plan_create_sddmm lower on the device when the format holds its input CSR
+(a format built in this process from canonical input): the MFMA tiles are cut from the format
+arrays on the host, the residual -- the input rows minus the kept tiles' entries, XCD sub-rows
+included, with the SDDMM output index of every entry -- is written by two kernels.  The plan must
+be the host lowering's: equal statistics and bitwise equal SpMM / SDDMM outputs, on every
+workload shape the host lowering is tested on (tiles kept or demoted, split rows, no tiles at all,
+more or fewer plan rows than input rows), and within the tolerance of the float64 CSR oracle.
 """
 import numpy as np
 import pytest
@@ -65,6 +65,30 @@ def graph(name, gen):
     return _cache[name]
 
 
+def run_sddmm(plan, Xh, Yh):
+    """Output prefilled with NaN: an entry no kernel writes fails the comparison."""
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    out = torch.full((plan.stats()["nnz"],), float("nan"), device="cuda")
+    S = plan.sddmm(X, Y, out=out)
+    torch.cuda.synchronize()
+    return S.cpu().numpy()
+
+
+def compare_sddmm(f, m, n, K, opts, what, seed=31):
+    dev = trspmm.Plan.for_sddmm(f, m, n, **opts)
+    host = trspmm.Plan.for_sddmm(f, m, n, host_lowering=True, **opts)
+    sd, sh = dev.stats(), host.stats()
+    assert sd["device_lowered"] == 1 and sh["device_lowered"] == 0, what
+    sd.pop("device_lowered")
+    sh.pop("device_lowered")
+    assert sd == sh, f"{what}: SDDMM stats differ\n device {sd}\n host   {sh}"
+    Xh = graphs.dense_operand(m, K, seed=seed)
+    Yh = graphs.dense_operand(n, K, seed=seed + 1)
+    Sd, Sh = run_sddmm(dev, Xh, Yh), run_sddmm(host, Xh, Yh)
+    assert np.array_equal(Sd, Sh), f"{what}: SDDMM outputs differ"
+    return Sd, Xh, Yh, sd
+
+
 def compare(f, m, n, Bh, opts, what):
     dev = trspmm.Plan.from_format(f, m, n, **opts)
     host = trspmm.Plan.from_format(f, m, n, host_lowering=True, **opts)
@@ -91,15 +115,45 @@ def test_device_lowering_equals_host_lowering(name, gen, oname, opts):
     say("  stats", s)
 
 
+SDDMM_OPTIONS = [
+    ("default", {}),
+    ("split16", {"xcd_split": 16}),
+    ("no_tiles", {"mfma_tc": False, "mfma_sptc": False}),
+    ("no_split", {"xcd_split": -1}),
+]
+
+
+@pytest.mark.parametrize("oname,opts", SDDMM_OPTIONS, ids=[o[0] for o in SDDMM_OPTIONS])
+@pytest.mark.parametrize("name,gen", GRAPHS, ids=[g[0] for g in GRAPHS])
+@pytest.mark.parametrize("K", [64, 128])
+def test_device_lowering_equals_host_lowering_sddmm(name, gen, oname, opts, K):
+    """K = 128 takes the split part of the SDDMM launcher, K = 64 the unsplit task list."""
+    say("device lowering sddmm", name, oname, K)
+    g, f = graph(name, gen)
+    S, Xh, Yh, s = compare_sddmm(f, g.m, g.n, K, opts, f"{name}/{oname}/K{K}")
+    nnz = int(g.rowptr[g.m])
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[:nnz], Xh, Yh)
+    # fp16 products accumulated in fp32 (the SDDMM tolerance of the other SDDMM parity tests)
+    tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))
+    assert S.shape == R.shape and np.max(np.abs(S - R)) <= tol, f"{name}/{oname}: {np.max(np.abs(S - R))}"
+    say("  stats", s)
+
+
 def test_device_lowering_exercises_tiles_and_split_rows():
     """The option sets above reach both device kernels' branches: kept tiles whose entries are
     flagged out of their rows, and split rows scattered into XCD sub-rows."""
     g, f = graph("sbm2k", GRAPHS[2][1])
     s = trspmm.Plan.from_format(f, g.m, g.n, window_row_cap=1 << 30).stats()
     assert s["device_lowered"] == 1 and s["mfma_tiles"] > 0 and s["mfma_nnz"] > 0
+    s = trspmm.Plan.for_sddmm(f, g.m, g.n).stats()
+    assert s["device_lowered"] == 1 and s["mfma_tiles"] > 0
     g, f = graph("rmat14", GRAPHS[1][1])
     s = trspmm.Plan.from_format(f, g.m, g.n, xcd_split=16, window_row_cap=1 << 30).stats()
     assert s["device_lowered"] == 1 and s["split_rows"] > 0 and s["mfma_tiles"] > 0
+    # SDDMM splits only without tiles; its sub-rows show as extra tasks
+    s1 = trspmm.Plan.for_sddmm(f, g.m, g.n, xcd_split=16, mfma_tc=False, mfma_sptc=False).stats()
+    s0 = trspmm.Plan.for_sddmm(f, g.m, g.n, xcd_split=-1, mfma_tc=False, mfma_sptc=False).stats()
+    assert s1["device_lowered"] == 1 and s1["mfma_tiles"] == 0 and s1["tasks"] > s0["tasks"]
 
 
 @pytest.mark.parametrize("extra", [-7, 5])
@@ -114,6 +168,7 @@ def test_device_lowering_with_other_row_counts(extra):
     assert np.array_equal(C[g.m:], np.zeros_like(C[g.m:]))
     e = osp.spmm_error(C[: min(m, g.m)], R[: min(m, g.m)])
     assert e["elementwise_ok"], e
+    compare_sddmm(f, m, g.n, 64, {}, f"sddmm m={m}")
 
 
 def test_device_lowering_rejects_columns_outside_n():

@@ -1203,7 +1203,8 @@ __global__ __launch_bounds__(256) void k_mark_tile_entries(const TileEntries* __
                                                            const int32_t* __restrict__ rowptr,
                                                            const int32_t* __restrict__ col,
                                                            uint32_t* __restrict__ flag_words,
-                                                           uint32_t* __restrict__ marked) {
+                                                           uint32_t* __restrict__ marked,
+                                                           int32_t* __restrict__ tile_pos) {
   const TileEntries& t = tiles[blockIdx.x];
   const int r = threadIdx.x >> 4, k = threadIdx.x & 15;
   const int row = t.row0 + r;
@@ -1218,6 +1219,7 @@ __global__ __launch_bounds__(256) void k_mark_tile_entries(const TileEntries* __
   if (lo < rowptr[row + 1] && col[lo] == c) {
     const uint32_t bit = 1u << ((lo & 3) * 8);
     if (!(atomicOr(flag_words + (lo >> 2), bit) & bit)) atomicAdd(marked, 1u);
+    if (tile_pos) tile_pos[(int64_t)blockIdx.x * 256 + threadIdx.x] = lo;
   }
 }
 
@@ -1228,27 +1230,20 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 
 // One wave per CSR row: 64 entries at a time, destinations from wave ballots, so each row keeps its
 // column order.
-__global__ __launch_bounds__(256) void k_place_entries(int32_t m, const int32_t* __restrict__ rowptr,
-                                                       const int32_t* __restrict__ col,
-                                                       const float* __restrict__ val,
-                                                       const uint8_t* __restrict__ flag,
-                                                       const int32_t* __restrict__ main_rowptr,
-                                                       const int32_t* __restrict__ split_index,
-                                                       const int32_t* __restrict__ cursor,
-                                                       int32_t* __restrict__ col_out, uint16_t* __restrict__ val_out) {
+__global__ __launch_bounds__(256) void k_place_entries(const PlaceEntries a) {
   const int row = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
-  if (row >= m) return;
-  const int b = rowptr[row], e = rowptr[row + 1];
-  const int si = split_index[row];
+  if (row >= a.m) return;
+  const int b = a.rowptr[row], e = a.rowptr[row + 1];
+  const int si = a.split_index[row];
   if (si >= 0) {
     int cur[kXcds];
 #pragma unroll
-    for (int x = 0; x < kXcds; ++x) cur[x] = cursor[si * kXcds + x];
+    for (int x = 0; x < kXcds; ++x) cur[x] = a.cursor[si * kXcds + x];
     for (int p = b; p < e; p += 64) {
       const int q = p + lane;
       const bool in = q < e;
-      const int32_t c = in ? col[q] : 0;
+      const int32_t c = in ? a.col[q] : 0;
       const int xq = xcd_of_column(c);
       int dst = 0;
 #pragma unroll
@@ -1258,21 +1253,23 @@ __global__ __launch_bounds__(256) void k_place_entries(int32_t m, const int32_t*
         cur[x] += __popcll(mask);
       }
       if (in) {
-        col_out[dst] = c;
-        val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, val[q]));
+        a.col_out[dst] = c;
+        if (a.val_out) a.val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, a.val[q]));
+        if (a.x_pos) a.x_pos[dst - a.x_base] = q;
       }
     }
-    return;
+    if (a.compact) return;
   }
-  int out = main_rowptr[row];
+  int out = a.main_rowptr[row];
   for (int p = b; p < e; p += 64) {
     const int q = p + lane;
-    const bool keep = q < e && !(flag && flag[q]);
+    const bool keep = q < e && !(a.flag && a.flag[q]);
     const uint64_t mask = __ballot(keep);
     if (keep) {
       const int dst = out + lanes_below(mask);
-      col_out[dst] = col[q];
-      val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, val[q]));
+      a.col_out[dst] = a.col[q];
+      if (a.val_out) a.val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, a.val[q]));
+      if (a.res_pos) a.res_pos[dst] = q;
     }
     out += __popcll(mask);
   }
@@ -1292,19 +1289,17 @@ hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
 }
 
 hipError_t launch_mark_tile_entries(const TileEntries* tiles, int32_t ntiles, int32_t m, const int32_t* rowptr,
-                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, hipStream_t stream) {
+                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, int32_t* tile_pos,
+                                    hipStream_t stream) {
   if (ntiles <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_mark_tile_entries, dim3((unsigned)ntiles), dim3(256), 0, stream, tiles, m, rowptr, col,
-                     flag_words, marked);
+                     flag_words, marked, tile_pos);
   return hipGetLastError();
 }
 
-hipError_t launch_place_entries(int32_t m, const int32_t* rowptr, const int32_t* col, const float* val,
-                                const uint8_t* flag, const int32_t* main_rowptr, const int32_t* split_index,
-                                const int32_t* cursor, int32_t* col_out, uint16_t* val_out, hipStream_t stream) {
-  if (m <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_place_entries, dim3((unsigned)((m + 3) / 4)), dim3(256), 0, stream, m, rowptr, col, val, flag,
-                     main_rowptr, split_index, cursor, col_out, val_out);
+hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream) {
+  if (a.m <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_place_entries, dim3((unsigned)((a.m + 3) / 4)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -87,21 +87,39 @@ struct DevicePlan {
 // unsplit).
 constexpr int kSddmmSplitMinK = 128;
 
-// Device-side plan lowering (the residual of an SpMM plan built from the input CSR the format keeps).
+// Device-side plan lowering (the residual of a plan built from the input CSR the format keeps).
 // A dense tile's stored entries: rows row0 + r (r < 16), columns cols[k]; bit (r % 4) * 16 + k of
 // present[r / 4] marks entry (r, k).
 struct TileEntries { int32_t row0; int32_t cols[16]; int32_t pad[3]; uint64_t present[4]; };
 // Byte e of the flag words (little-endian) = 1 for every CSR entry e (rows < m, columns ascending)
 // that a tile stores; *marked (zeroed by the caller) counts the entries flagged, each once.
+// tile_pos (optional, SDDMM): tile_pos[t * 256 + r * 16 + k] = CSR index of stored entry (r, k).
 hipError_t launch_mark_tile_entries(const TileEntries* tiles, int32_t ntiles, int32_t m, const int32_t* rowptr,
-                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, hipStream_t stream);
-// Entries of CSR rows [0, m) into the plan's entry arrays: a row with split_index[r] = i >= 0 is
-// scattered by the XCD of each column to cursor[i * kXcds + x] onward (column order kept); any
-// other row goes, without its flagged entries (flag may be null), to main_rowptr[r] onward.
-// Values are rounded to fp16.
-hipError_t launch_place_entries(int32_t m, const int32_t* rowptr, const int32_t* col, const float* val,
-                                const uint8_t* flag, const int32_t* main_rowptr, const int32_t* split_index,
-                                const int32_t* cursor, int32_t* col_out, uint16_t* val_out, hipStream_t stream);
+                                    const int32_t* col, uint32_t* flag_words, uint32_t* marked, int32_t* tile_pos,
+                                    hipStream_t stream);
+// Entries of CSR rows [0, m) into the plan's entry arrays.  Row r with split_index[r] = i >= 0 is
+// scattered by the XCD of each column to cursor[i * kXcds + x] onward (column order kept), with
+// x_pos[position - x_base] = CSR index when x_pos is set; compact (SpMM) plans store such a row
+// only there.  Every other row -- and in a non-compact (SDDMM) plan every row -- goes, without its
+// flagged entries (flag may be null), to main_rowptr[r] onward, with res_pos[position] = CSR index
+// when res_pos is set.  Values (val_out set) are rounded to fp16.
+struct PlaceEntries {
+  int32_t m = 0;
+  const int32_t* rowptr = nullptr;
+  const int32_t* col = nullptr;
+  const float* val = nullptr;
+  const uint8_t* flag = nullptr;
+  const int32_t* main_rowptr = nullptr;
+  const int32_t* split_index = nullptr;
+  const int32_t* cursor = nullptr;
+  int32_t* col_out = nullptr;
+  uint16_t* val_out = nullptr;
+  int32_t* res_pos = nullptr;
+  int32_t* x_pos = nullptr;
+  int64_t x_base = 0;
+  int32_t compact = 1;
+};
+hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream);
 
 // ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,

@@ -761,14 +761,25 @@ int tile_row_entries(const Lowering::Tile& t, int r) {
   return __builtin_popcountll((t.present[r / 4] >> ((r % 4) * 16)) & 0xffffull);
 }
 
+// Where the device lowering writes (device addresses inside the plan; null = not in this plan).
+struct DeviceOut {
+  const int32_t* main_rowptr = nullptr;
+  int32_t* col = nullptr;
+  uint16_t* val = nullptr;        // SpMM: fp16 values
+  int32_t* res_pos = nullptr;     // SDDMM with tiles: output index of each residual entry
+  int32_t* x_pos = nullptr;       // SDDMM split part: output index of each sub-row entry
+  int64_t x_base = 0;             // x_pos[i] belongs to entry x_base + i
+  int32_t* tile_pos = nullptr;    // SDDMM with tiles: output index of each stored tile slot, else -1
+  bool compact = true;            // SpMM: split rows only in their sub-rows
+};
+
 // Device half of the device lowering: the input CSR of rows [0, m) goes up once, the kept tiles'
 // entries are flagged in it, and every row is written to its placed position -- main rows without
-// their flagged entries, split rows scattered into their XCD sub-rows -- as col_out / val_out
-// (main_rowptr, col_out, val_out: device addresses inside the plan).  Temporaries live in one
-// allocation freed before returning.
+// their flagged entries, split rows scattered into their XCD sub-rows.  Outputs follow the input
+// CSR order, so an entry's output index is its CSR index.  Temporaries live in one allocation
+// freed before returning.
 Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowering::Tile>& tiles,
-                          int64_t expect_marked, const Placement& PL, const int32_t* main_rowptr, int32_t* col_out,
-                          uint16_t* val_out) {
+                          int64_t expect_marked, const Placement& PL, const DeviceOut& o) {
   const int32_t rows = std::min(m, f.rows);
   const int64_t cnnz = f.csr_rowptr[rows];
   std::vector<int32_t> rp((size_t)m + 1, (int32_t)cnnz);
@@ -785,7 +796,7 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   Blob tmp;
   const size_t o_rp = tmp.add(rp);
   const size_t o_col = tmp.add_raw(f.csr_col.data(), (size_t)cnnz * 4);
-  const size_t o_val = tmp.add_raw(f.csr_val.data(), (size_t)cnnz * 4);
+  const size_t o_val = tmp.add_raw(o.val ? f.csr_val.data() : nullptr, o.val ? (size_t)cnnz * 4 : 0);
   const size_t o_te = tmp.add(te);
   const size_t o_si = tmp.add(split_index);
   const size_t o_cur = tmp.add(PL.cursor);
@@ -810,8 +821,10 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   uint32_t* d_flag = reinterpret_cast<uint32_t*>(base + o_flag);
   uint32_t* d_marked = reinterpret_cast<uint32_t*>(base + o_flag + flag_bytes);
   if (!tiles.empty()) {
+    if (o.tile_pos && hipMemset(o.tile_pos, 0xff, tiles.size() * 256 * sizeof(int32_t)) != hipSuccess)
+      return done(fail(TRS_EDEVICE, "device lowering: tile slot clear failed"));
     if (trs::launch_mark_tile_entries(reinterpret_cast<const trs::TileEntries*>(base + o_te), (int32_t)tiles.size(), m,
-                                      d_rp, d_col, d_flag, d_marked, nullptr) != hipSuccess)
+                                      d_rp, d_col, d_flag, d_marked, o.tile_pos, nullptr) != hipSuccess)
       return done(fail(TRS_EDEVICE, "device lowering: tile marking launch failed"));
     uint32_t marked = 0;
     if (hipMemcpy(&marked, d_marked, 4, hipMemcpyDeviceToHost) != hipSuccess)
@@ -821,13 +834,70 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
     if ((int64_t)marked != expect_marked)
       return done(fail(kLowerOnHost, "device lowering: tiles and input CSR disagree"));
   }
-  if (trs::launch_place_entries(m, d_rp, d_col, reinterpret_cast<const float*>(base + o_val),
-                                tiles.empty() ? nullptr : reinterpret_cast<const uint8_t*>(d_flag), main_rowptr,
-                                reinterpret_cast<const int32_t*>(base + o_si),
-                                reinterpret_cast<const int32_t*>(base + o_cur), col_out, val_out, nullptr) != hipSuccess ||
-      hipStreamSynchronize(nullptr) != hipSuccess)
+  trs::PlaceEntries a;
+  a.m = m;
+  a.rowptr = d_rp;
+  a.col = d_col;
+  a.val = o.val ? reinterpret_cast<const float*>(base + o_val) : nullptr;
+  a.flag = tiles.empty() ? nullptr : reinterpret_cast<const uint8_t*>(d_flag);
+  a.main_rowptr = o.main_rowptr;
+  a.split_index = reinterpret_cast<const int32_t*>(base + o_si);
+  a.cursor = reinterpret_cast<const int32_t*>(base + o_cur);
+  a.col_out = o.col;
+  a.val_out = o.val;
+  a.res_pos = o.res_pos;
+  a.x_pos = o.x_pos;
+  a.x_base = o.x_base;
+  a.compact = o.compact ? 1 : 0;
+  if (trs::launch_place_entries(a, nullptr) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess)
     return done(fail(TRS_EDEVICE, "device lowering: entry placement failed"));
   return done(Status{});
+}
+
+// Device lowering, host side: the column range check the host lowering makes (a residual or tile
+// column outside [0, n) is TRS_ERANGE) over the input CSR's rows [0, m), and their lengths (rows
+// beyond the input's are empty).
+Status input_rows(const trs_format& src, Lowering& L, std::vector<int32_t>& csr_len) {
+  const int32_t m = L.m;
+  const int32_t rows = std::min(m, src.rows);
+  const int64_t cnnz = src.csr_rowptr[rows];
+  const int T = lowering_threads();
+  std::vector<int64_t> bad((size_t)T, INT64_MAX);
+  parallel_parts(T, cnnz, 1 << 16, [&](int t) { return cnnz * t / T; }, [&](int64_t b, int64_t e, int t) {
+    for (int64_t q = b; q < e; ++q)
+      if (src.csr_col[q] < 0 || src.csr_col[q] >= L.n) {
+        bad[t] = q;
+        break;
+      }
+  });
+  const int64_t q = *std::min_element(bad.begin(), bad.end());
+  if (q != INT64_MAX) L.check_col(src.csr_col[q]);
+  if (!L.st.ok()) return L.st;
+  csr_len.assign((size_t)m, 0);
+  for (int32_t r = 0; r < rows; ++r) csr_len[r] = src.csr_rowptr[r + 1] - src.csr_rowptr[r];
+  // a tile slot added twice (duplicate input entries) holds a sum the input CSR does not
+  for (const auto& t : L.tiles)
+    if (t.nnz != tile_present(t)) return fail(kLowerOnHost, "device lowering: a tile slot holds two entries");
+  return Status{};
+}
+
+// Residual row pointers of the device lowering: the input rows minus the tiles' entries; a
+// negative length means the tiles hold entries the input CSR lacks.
+Status residual_rows(const std::vector<int32_t>& csr_len, const std::vector<Lowering::Tile>& tiles, int32_t m,
+                     std::vector<int32_t>& rowptr, int64_t* tile_entries) {
+  std::vector<int32_t> len(csr_len);
+  int64_t te = 0;
+  for (const auto& t : tiles) {
+    te += tile_present(t);
+    for (int r = 0; r < 16 && t.row0 + r < m; ++r) len[t.row0 + r] -= tile_row_entries(t, r);
+  }
+  rowptr.assign((size_t)m + 1, 0);
+  for (int32_t r = 0; r < m; ++r) {
+    if (len[r] < 0) return fail(kLowerOnHost, "device lowering: tiles hold entries the input CSR lacks");
+    rowptr[r + 1] = rowptr[r] + len[r];
+  }
+  if (tile_entries) *tile_entries = te;
+  return Status{};
 }
 
 // Residual CSR + tasks + MFMA windows -> device plan.  With src (the format that holds its input
@@ -839,23 +909,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   // device lowering: row lengths of the input CSR (rows beyond its rows are empty)
   std::vector<int32_t> csr_len;
   if (src) {
-    const int32_t rows = std::min(m, src->rows);
-    const int64_t cnnz = src->csr_rowptr[rows];
-    // column range (the host lowering rejects a residual or tile column outside [0, n))
-    const int T = lowering_threads();
-    std::vector<int64_t> bad((size_t)T, INT64_MAX);
-    parallel_parts(T, cnnz, 1 << 16, [&](int t) { return cnnz * t / T; }, [&](int64_t b, int64_t e, int t) {
-      for (int64_t q = b; q < e; ++q)
-        if (src->csr_col[q] < 0 || src->csr_col[q] >= L.n) {
-          bad[t] = q;
-          break;
-        }
-    });
-    const int64_t q = *std::min_element(bad.begin(), bad.end());
-    if (q != INT64_MAX) L.check_col(src->csr_col[q]);
-    if (!L.st.ok()) return L.st;
-    csr_len.assign((size_t)m, 0);
-    for (int32_t r = 0; r < rows; ++r) csr_len[r] = src->csr_rowptr[r + 1] - src->csr_rowptr[r];
+    const Status is = input_rows(*src, L, csr_len);
+    if (!is.ok()) return is;
   }
 
   // MFMA windows: 16-row blocks owning at least one tile (tile order inside a window kept).
@@ -874,13 +929,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     std::vector<int32_t> len((size_t)m, 0);
     if (src) {
       // input row length minus the tile entries of the row
-      len = csr_len;
-      for (const auto& t : L.tiles) {
-        if (t.nnz != tile_present(t)) return fail(kLowerOnHost, "device lowering: a tile slot holds two entries");
-        for (int r = 0; r < 16 && t.row0 + r < m; ++r) len[t.row0 + r] -= tile_row_entries(t, r);
-      }
-      for (int32_t r = 0; r < m; ++r)
-        if (len[r] < 0) return fail(kLowerOnHost, "device lowering: tiles hold entries the input CSR lacks");
+      std::vector<int32_t> rp;
+      const Status rs = residual_rows(csr_len, L.tiles, m, rp, nullptr);
+      if (!rs.ok()) return rs;
+      for (int32_t r = 0; r < m; ++r) len[r] = rp[r + 1] - rp[r];
     } else {
       for (int32_t r : L.row) len[r]++;
     }
@@ -914,13 +966,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   int64_t expect_marked = 0;
   if (src) {
     // the input rows minus the kept tiles' entries (columns ascending, as the host sort leaves them)
-    std::vector<int32_t> len(csr_len);
-    for (const auto& t : L.tiles) {
-      expect_marked += tile_present(t);
-      for (int r = 0; r < 16 && t.row0 + r < m; ++r) len[t.row0 + r] -= tile_row_entries(t, r);
-    }
-    rowptr.assign((size_t)m + 1, 0);
-    for (int32_t r = 0; r < m; ++r) rowptr[r + 1] = rowptr[r] + len[r];
+    const Status rs = residual_rows(csr_len, L.tiles, m, rowptr, &expect_marked);
+    if (!rs.ok()) return rs;
     nent = rowptr[m];
   } else {
     nent = (int64_t)L.row.size();
@@ -986,9 +1033,11 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   }
   unsigned char* base = static_cast<unsigned char*>(P->dmem);
   if (src) {
-    const Status ds = residual_on_device(*src, m, L.tiles, expect_marked, PL,
-                                         reinterpret_cast<const int32_t*>(base + o_rowptr),
-                                         reinterpret_cast<int32_t*>(base + o_col), reinterpret_cast<uint16_t*>(base + o_val));
+    DeviceOut o;
+    o.main_rowptr = reinterpret_cast<const int32_t*>(base + o_rowptr);
+    o.col = reinterpret_cast<int32_t*>(base + o_col);
+    o.val = reinterpret_cast<uint16_t*>(base + o_val);
+    const Status ds = residual_on_device(*src, m, L.tiles, expect_marked, PL, o);
     if (!ds.ok()) {
       delete P;
       return ds;
@@ -1053,16 +1102,27 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
 // SDDMM plan: residual CSR (+ the output index of each entry when tiles exist) and independent
 // tiles with the output index of each stored slot.  Outputs follow the (row, column) order of all
 // entries, i.e. the input CSR order for canonical input; keep_order keeps a plain CSR as given.
-Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order, trs_plan** out) {
+//
+// With src (the format that holds its input CSR), L carries the tiles only and the residual is
+// built on the device as for SpMM plans; the output index of an entry is then its input CSR index.
+Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order, trs_plan** out,
+                      const trs_format* src = nullptr) {
   if (!L.st.ok()) return L.st;
+  std::vector<int32_t> csr_len;
+  if (src) {
+    const Status is = input_rows(*src, L, csr_len);
+    if (!is.ok()) return is;
+  }
   // Tiles pay for themselves only when they carry a real share of the entries: otherwise the
   // per-entry output index they force on the residual costs more than MFMA saves (measured on
   // R-MAT 2^20, K=128: tiles with 2.7% of the entries made SDDMM 15% slower).  Hand them back.
   {
     int64_t tile_entries = 0;
     for (const auto& t : L.tiles) tile_entries += t.nnz;
-    const int64_t total = tile_entries + (int64_t)L.row.size();
+    const int64_t total = src ? (int64_t)std::accumulate(csr_len.begin(), csr_len.end(), (int64_t)0)
+                              : tile_entries + (int64_t)L.row.size();
     if (!L.tiles.empty() && (double)tile_entries < 0.10 * (double)total) {
+      if (src) L.tiles.clear();   // their entries stay in the input CSR
       for (const auto& t : L.tiles)
         for (int r = 0; r < 16; ++r)
           for (int k = 0; k < 16; ++k)
@@ -1071,27 +1131,44 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
     }
   }
   const int32_t m = L.m;
-  const int64_t nent = (int64_t)L.row.size();
   std::vector<int32_t> rowptr;
-  std::vector<int64_t> perm;
-  residual_csr(L, keep_order && L.tiles.empty(), rowptr, perm);
-  std::vector<int32_t> col(nent);
-  parallel_chunks(nent, [&](int64_t b, int64_t e, int) {
-    for (int64_t i = b; i < e; ++i) col[i] = L.col[perm[i]];
-  });
+  std::vector<int32_t> col;
+  int64_t nent = 0;
+  int64_t expect_marked = 0;
+  if (src) {
+    const Status rs = residual_rows(csr_len, L.tiles, m, rowptr, &expect_marked);
+    if (!rs.ok()) return rs;
+    nent = rowptr[m];
+  } else {
+    nent = (int64_t)L.row.size();
+    std::vector<int64_t> perm;
+    residual_csr(L, keep_order && L.tiles.empty(), rowptr, perm);
+    col.resize((size_t)nent);
+    parallel_chunks(nent, [&](int64_t b, int64_t e, int) {
+      for (int64_t i = b; i < e; ++i) col[i] = L.col[perm[i]];
+    });
+  }
 
   // tile entries in (row, column) order, merged with the residual rows
   struct TE { int32_t row, col, slot; };   // slot = tile * 256 + r * 16 + k
   std::vector<TE> te;
-  for (size_t t = 0; t < L.tiles.size(); ++t)
+  for (size_t t = 0; t < L.tiles.size() && !src; ++t)
     for (int r = 0; r < 16; ++r)
       for (int k = 0; k < 16; ++k)
         if (L.tiles[t].cols[k] >= 0 && Lowering::tile_has(L.tiles[t], r, k) && L.tiles[t].row0 + r < m)
           te.push_back({L.tiles[t].row0 + r, L.tiles[t].cols[k], (int32_t)(t * 256 + r * 16 + k)});
   std::sort(te.begin(), te.end(), [](const TE& a, const TE& b) { return a.row != b.row ? a.row < b.row : a.col < b.col; });
-  if (nent + (int64_t)te.size() > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 entries");
+  const int64_t tile_entries = src ? expect_marked : (int64_t)te.size();
+  if (nent + tile_entries > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 entries");
+  const bool with_pos = tile_entries > 0;
   std::vector<int32_t> res_pos, tile_pos, tile_row0, tile_cols;
-  if (!te.empty()) {
+  if (src && with_pos) {
+    for (const auto& t : L.tiles) {
+      tile_row0.push_back(t.row0);
+      tile_cols.insert(tile_cols.end(), t.cols, t.cols + 16);
+    }
+  }
+  if (!src && !te.empty()) {
     res_pos.resize(nent);
     tile_pos.assign(L.tiles.size() * 256, -1);
     int32_t next = 0;
@@ -1113,31 +1190,51 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSddmmSplitMin;
   // the split part's outputs are contiguous runs of the residual order: only without tiles, whose
   // merge interleaves output positions
-  const Placement PL = place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, te.empty() ? split_min : 0);
+  // (device lowering: split rows hold no tile entries -- there are none -- so their columns are
+  // the input rows')
+  const int32_t split = with_pos ? 0 : split_min;
+  const Placement PL = src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, {}, false, split)
+                           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, split);
   std::vector<int32_t> col2, x_pos;
-  move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos);
+  if (!src) move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos);
   Tasks T = build_tasks(PL, rowptr, m, {}, false, opt);
   if (!T.st.ok()) return T.st;
 
   Blob blob;
+  const size_t n_xpos = (size_t)(PL.total - nent);
   const size_t o_rowptr = blob.add(rowptr);
-  const size_t o_col = blob.add(col2);
+  const size_t o_col = src ? blob.add_raw(nullptr, (size_t)PL.total * 4) : blob.add(col2);
   const size_t o_tasks = blob.add(T.tasks);
   const size_t o_xtasks = blob.add(T.xtasks);
   const size_t o_xrowptr = blob.add(PL.xrowptr);
-  const size_t o_xpos = blob.add(x_pos);
+  const size_t o_xpos = src ? blob.add_raw(nullptr, n_xpos * 4) : blob.add(x_pos);
   const size_t o_srow = blob.add(PL.sub_row);
   const size_t o_full = blob.add(T.full);
-  const size_t o_rpos = blob.add(res_pos);
+  const size_t o_rpos = src ? blob.add_raw(nullptr, with_pos ? (size_t)nent * 4 : 0) : blob.add(res_pos);
   const size_t o_trow = blob.add(tile_row0);
   const size_t o_tcol = blob.add(tile_cols);
-  const size_t o_tpos = blob.add(tile_pos);
+  const size_t o_tpos = src ? blob.add_raw(nullptr, with_pos ? L.tiles.size() * 256 * 4 : 0) : blob.add(tile_pos);
   trs_plan* P = nullptr;
   {
     const Status us = upload(blob, P);
     if (!us.ok()) return us;
   }
   unsigned char* base = static_cast<unsigned char*>(P->dmem);
+  if (src) {
+    DeviceOut o;
+    o.main_rowptr = reinterpret_cast<const int32_t*>(base + o_rowptr);
+    o.col = reinterpret_cast<int32_t*>(base + o_col);
+    o.res_pos = with_pos ? reinterpret_cast<int32_t*>(base + o_rpos) : nullptr;
+    o.x_pos = n_xpos ? reinterpret_cast<int32_t*>(base + o_xpos) : nullptr;
+    o.x_base = nent;
+    o.tile_pos = with_pos ? reinterpret_cast<int32_t*>(base + o_tpos) : nullptr;
+    o.compact = false;
+    const Status ds = residual_on_device(*src, m, with_pos ? L.tiles : std::vector<Lowering::Tile>{}, expect_marked, PL, o);
+    if (!ds.ok()) {
+      delete P;
+      return ds;
+    }
+  }
   trs::DevicePlan& d = P->dp;
   d.m = m;
   d.n = L.n;
@@ -1155,11 +1252,11 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.nfull_tasks = (int32_t)T.full.size();
   std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
   d.x_task_max = T.xtask_max;
-  d.res_pos = res_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_rpos);
-  d.tile_row0 = tile_row0.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_trow);
-  d.tile_cols = tile_cols.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tcol);
-  d.tile_pos = tile_pos.empty() ? nullptr : reinterpret_cast<const int32_t*>(base + o_tpos);
-  d.ntiles = tile_pos.empty() ? 0 : (int32_t)L.tiles.size();
+  d.res_pos = with_pos ? reinterpret_cast<const int32_t*>(base + o_rpos) : nullptr;
+  d.tile_row0 = with_pos ? reinterpret_cast<const int32_t*>(base + o_trow) : nullptr;
+  d.tile_cols = with_pos ? reinterpret_cast<const int32_t*>(base + o_tcol) : nullptr;
+  d.tile_pos = with_pos ? reinterpret_cast<const int32_t*>(base + o_tpos) : nullptr;
+  d.ntiles = with_pos ? (int32_t)L.tiles.size() : 0;
   d.feature_lanes = opt.feature_lanes;
   d.streaming = opt.streaming < 0 ? 2 : (opt.streaming & 2);
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
@@ -1174,12 +1271,34 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   s.n = L.n;
   s.csr_nnz = nent;
   s.mfma_tiles = d.ntiles;
-  s.mfma_nnz = (int64_t)te.size();
-  s.nnz = nent + (int64_t)te.size();
+  s.mfma_nnz = tile_entries;
+  s.nnz = nent + tile_entries;
   s.tasks = (int64_t)(T.tasks.size() + T.xtasks.size());
   s.device_bytes = (int64_t)blob.size();
+  s.device_lowered = src ? 1 : 0;
   *out = P;
   return Status{};
+}
+
+// Every share of a builder output: TC sub-blocks, residual parts, 2:4 groups, spill.
+void lower_format(Lowering& L, const trs_format& f, const trs_plan_options& o) {
+  lower_tc(L, f.t_rowoff.data(), (int64_t)f.t_winrow.size(), f.t_blockoff.data(), f.t_col.data(), f.t_val.data(),
+           nullptr, (int64_t)f.t_val.size(), f.t_winrow.data(), f.t_bin.data(), o.mfma_tc != 0);
+  lower_residual(L, f.c_off.data(), f.c_row.data(), (int64_t)f.c_row.size(), f.c_col.data(), f.c_val.data(), nullptr,
+                 (int64_t)f.c_col.size());
+  lower_residual(L, f.cs_off.data(), f.cs_row.data(), (int64_t)f.cs_row.size(), f.cs_col.data(), f.cs_val.data(),
+                 nullptr, (int64_t)f.cs_col.size());
+  lower_groups(L, f.s_col.data(), f.s_val.data(), f.s_pos.data(), (int64_t)f.s_win.size(), f.s_win.data(),
+               f.s_offsets.data(), (int64_t)f.s_offsets.size() - 1, f.window, o.mfma_sptc != 0, o.sptc_min_fill);
+  for (size_t i = 0; i < f.spill_row.size() && L.st.ok(); ++i) L.add(f.spill_row[i], f.spill_col[i], f.spill_val[i]);
+}
+
+// The tiles of a builder output only (L.tiles_only): the shares that can become MFMA tiles.
+void lower_format_tiles(Lowering& L, const trs_format& f, const trs_plan_options& o) {
+  lower_tc(L, f.t_rowoff.data(), (int64_t)f.t_winrow.size(), f.t_blockoff.data(), f.t_col.data(), f.t_val.data(),
+           nullptr, (int64_t)f.t_val.size(), f.t_winrow.data(), f.t_bin.data(), o.mfma_tc != 0);
+  lower_groups(L, f.s_col.data(), f.s_val.data(), f.s_pos.data(), (int64_t)f.s_win.size(), f.s_win.data(),
+               f.s_offsets.data(), (int64_t)f.s_offsets.size() - 1, f.window, o.mfma_sptc != 0, o.sptc_min_fill);
 }
 
 int report(const Status& s) {
@@ -1234,10 +1353,7 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
     D.m = m;
     D.n = n;
     D.tiles_only = true;
-    lower_tc(D, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
-             f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
-    lower_groups(D, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
-                 f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
+    lower_format_tiles(D, *f, o);
     const Status ds = finalize(D, o, out, f);
     if (ds.code != kLowerOnHost) return report(ds);
   }
@@ -1246,15 +1362,7 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
   L.n = n;
   const size_t approx = f->t_val.size() + f->c_val.size() + f->cs_val.size() + f->s_val.size() / 2 + f->spill_val.size();
   L.row.reserve(approx); L.col.reserve(approx); L.val.reserve(approx);
-  lower_tc(L, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
-           f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
-  lower_residual(L, f->c_off.data(), f->c_row.data(), (int64_t)f->c_row.size(), f->c_col.data(), f->c_val.data(),
-                 nullptr, (int64_t)f->c_col.size());
-  lower_residual(L, f->cs_off.data(), f->cs_row.data(), (int64_t)f->cs_row.size(), f->cs_col.data(),
-                 f->cs_val.data(), nullptr, (int64_t)f->cs_col.size());
-  lower_groups(L, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
-               f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
-  for (size_t i = 0; i < f->spill_row.size() && L.st.ok(); ++i) L.add(f->spill_row[i], f->spill_col[i], f->spill_val[i]);
+  lower_format(L, *f, o);
   return report(finalize(L, o, out));
 }
 
@@ -1265,18 +1373,19 @@ int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_p
   if (!f->canonical)
     return report(fail(TRS_ENOTCANON, "trs_plan_create_sddmm: input rows were not strictly increasing"));
   const trs_plan_options o = resolve(opt);
+  if (!o.host_lowering && !f->csr_rowptr.empty()) {
+    Lowering D;
+    D.m = m;
+    D.n = n;
+    D.tiles_only = true;
+    lower_format_tiles(D, *f, o);
+    const Status ds = finalize_sddmm(D, o, false, out, f);
+    if (ds.code != kLowerOnHost) return report(ds);
+  }
   Lowering L;
   L.m = m;
   L.n = n;
-  lower_tc(L, f->t_rowoff.data(), (int64_t)f->t_winrow.size(), f->t_blockoff.data(), f->t_col.data(),
-           f->t_val.data(), nullptr, (int64_t)f->t_val.size(), f->t_winrow.data(), f->t_bin.data(), o.mfma_tc != 0);
-  lower_residual(L, f->c_off.data(), f->c_row.data(), (int64_t)f->c_row.size(), f->c_col.data(), f->c_val.data(),
-                 nullptr, (int64_t)f->c_col.size());
-  lower_residual(L, f->cs_off.data(), f->cs_row.data(), (int64_t)f->cs_row.size(), f->cs_col.data(),
-                 f->cs_val.data(), nullptr, (int64_t)f->cs_col.size());
-  lower_groups(L, f->s_col.data(), f->s_val.data(), f->s_pos.data(), (int64_t)f->s_win.size(), f->s_win.data(),
-               f->s_offsets.data(), (int64_t)f->s_offsets.size() - 1, f->window, o.mfma_sptc != 0, o.sptc_min_fill);
-  for (size_t i = 0; i < f->spill_row.size() && L.st.ok(); ++i) L.add(f->spill_row[i], f->spill_col[i], f->spill_val[i]);
+  lower_format(L, *f, o);
   return report(finalize_sddmm(L, o, false, out));
 }
 

@@ -249,13 +249,16 @@ class Plan:
                   sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
-                  streaming: Optional[int] = None, xcd_split: Optional[int] = None) -> "Plan":
+                  streaming: Optional[int] = None, xcd_split: Optional[int] = None,
+                  host_lowering: bool = False) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
-        residual outputs with non-temporal stores."""
+        residual outputs with non-temporal stores.  host_lowering=True builds the residual on the
+        host even when the format holds its input CSR (the plan is the same)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
                      streaming=streaming, xcd_split=xcd_split)
+        o.host_lowering = int(bool(host_lowering))
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
                   "trs_plan_create_sddmm")
