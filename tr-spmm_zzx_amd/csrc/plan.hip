@@ -89,6 +89,13 @@ void parallel_chunks(int64_t n, Fn&& fn) {
   parallel_parts(T, n, 1 << 16, [&](int t) { return n * t / T; }, fn);
 }
 
+// fn over [0, n) tiles (about 1 KB each) in parallel pieces.
+template <class Fn>
+void parallel_tiles(int64_t n, Fn&& fn) {
+  const int T = lowering_threads();
+  parallel_parts(T, n, 1024, [&](int t) { return n * t / T; }, fn);
+}
+
 // Host-side staging of one plan.
 struct Lowering {
   int32_t m = 0, n = 0;
@@ -136,11 +143,12 @@ struct Lowering {
 
 float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// TC sub-blocks -> MFMA tiles (pairs of sub-blocks of one part, 16 columns) or entries.
-void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_t* t_blockoff,
-              const int32_t* t_col, const float* vals_f32, const uint16_t* vals_f16, int64_t nvals,
-              const int32_t* t_winrow, const int64_t* t_bin, bool to_mfma) {
-  for (int64_t p = 0; p < nparts && L.st.ok(); ++p) {
+// TC sub-blocks of parts [p_begin, p_end) -> MFMA tiles (pairs of sub-blocks of one part, 16
+// columns) or entries.
+void lower_tc_range(Lowering& L, const int32_t* t_rowoff, int64_t p_begin, int64_t p_end, const int32_t* t_blockoff,
+                    const int32_t* t_col, const float* vals_f32, const uint16_t* vals_f16, int64_t nvals,
+                    const int32_t* t_winrow, const int64_t* t_bin, bool to_mfma) {
+  for (int64_t p = p_begin; p < p_end && L.st.ok(); ++p) {
     const int32_t s0 = t_rowoff[p], s1 = t_rowoff[p + 1];
     const int32_t row0 = t_winrow[p];
     const bool mfma = to_mfma && row0 % 16 == 0 && row0 >= 0;
@@ -182,6 +190,37 @@ void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_
       }
       if (mfma) L.tiles.push_back(T);
     }
+  }
+}
+
+// Parts are independent: ranges of parts are lowered in parallel into private buffers and appended
+// in part order, so the result (and the first error) equals the serial one.
+void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_t* t_blockoff, const int32_t* t_col,
+              const float* vals_f32, const uint16_t* vals_f16, int64_t nvals, const int32_t* t_winrow,
+              const int64_t* t_bin, bool to_mfma) {
+  const int T = lowering_threads();
+  if (nparts < 4096 || T <= 1) {
+    lower_tc_range(L, t_rowoff, 0, nparts, t_blockoff, t_col, vals_f32, vals_f16, nvals, t_winrow, t_bin, to_mfma);
+    return;
+  }
+  std::vector<Lowering> part(T);
+  for (auto& q : part) {
+    q.m = L.m;
+    q.n = L.n;
+    q.tiles_only = L.tiles_only;
+  }
+  parallel_parts(T, nparts, 0, [&](int t) { return nparts * t / T; }, [&](int64_t pb, int64_t pe, int t) {
+    lower_tc_range(part[t], t_rowoff, pb, pe, t_blockoff, t_col, vals_f32, vals_f16, nvals, t_winrow, t_bin, to_mfma);
+  });
+  for (auto& q : part) {
+    if (!q.st.ok()) {
+      if (L.st.ok()) L.st = q.st;
+      return;
+    }
+    L.row.insert(L.row.end(), q.row.begin(), q.row.end());
+    L.col.insert(L.col.end(), q.col.begin(), q.col.end());
+    L.val.insert(L.val.end(), q.val.begin(), q.val.end());
+    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
   }
 }
 
@@ -744,6 +783,21 @@ Status upload(const Blob& blob, trs_plan*& P) {
   return Status{};
 }
 
+// Tiles by row0, equal row0 in their order: a stable sort of indices, then one gather (a tile is
+// over 1 KB, too large to move around in a sort).
+void sort_tiles(std::vector<Lowering::Tile>& tiles) {
+  auto less = [&](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; };
+  if (std::is_sorted(tiles.begin(), tiles.end(), less)) return;
+  std::vector<int32_t> order(tiles.size());
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return tiles[a].row0 < tiles[b].row0; });
+  std::vector<Lowering::Tile> sorted(tiles.size());
+  parallel_tiles((int64_t)tiles.size(), [&](int64_t b, int64_t e, int) {
+    for (int64_t i = b; i < e; ++i) sorted[i] = tiles[order[i]];
+  });
+  tiles.swap(sorted);
+}
+
 // Internal status of the device lowering: the format's tiles and its input CSR disagree (a tile
 // entry the CSR does not hold, or two tiles holding one entry) or its temporaries could not be
 // allocated; the caller then lowers on the host.
@@ -914,8 +968,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   }
 
   // MFMA windows: 16-row blocks owning at least one tile (tile order inside a window kept).
-  std::stable_sort(L.tiles.begin(), L.tiles.end(),
-                   [](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; });
+  sort_tiles(L.tiles);
   const int32_t nblocks = (m + 15) / 16;
   std::vector<uint8_t> owned(nblocks, 0);
   for (const auto& t : L.tiles) owned[t.row0 / 16] = 1;
@@ -993,11 +1046,13 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   std::vector<int32_t> tile_cols(L.tiles.size() * 16);
   std::vector<uint16_t> tile_a(L.tiles.size() * 256);
   int64_t mfma_nnz = 0;
-  for (size_t t = 0; t < L.tiles.size(); ++t) {
-    for (int k = 0; k < 16; ++k) tile_cols[t * 16 + k] = L.tiles[t].cols[k];
-    for (int i = 0; i < 256; ++i) tile_a[t * 256 + i] = trs::half_bits(L.tiles[t].a[i]);
-    mfma_nnz += L.tiles[t].nnz;
-  }
+  for (const auto& t : L.tiles) mfma_nnz += t.nnz;
+  parallel_tiles((int64_t)L.tiles.size(), [&](int64_t b, int64_t e, int) {
+    for (int64_t t = b; t < e; ++t) {
+      for (int k = 0; k < 16; ++k) tile_cols[t * 16 + k] = L.tiles[t].cols[k];
+      for (int i = 0; i < 256; ++i) tile_a[t * 256 + i] = trs::half_bits(L.tiles[t].a[i]);
+    }
+  });
 
   // residual tasks over rows not owned by an MFMA window
   // XCD column split for SpMM (each sub-row costs a partial slot of 4 K bytes written and read back)
