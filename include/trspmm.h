@@ -187,7 +187,9 @@ typedef struct trs_plan_options {
                              i mod 8), so each XCD's L2 holds B (or Y) rows of an eighth of the
                              columns; an SpMM sub-row costs a partial slot, an SDDMM sub-row entry
                              an output index (SDDMM uses the split from K = 128 on).
-                             0 = automatic (SpMM 256, SDDMM 512), -1 = off */
+                             0 = automatic (SpMM 256, SDDMM 512, and only when those rows read
+                             their columns at least 4 times each on average: no L2 reuse to gain
+                             otherwise), -1 = off */
   int32_t host_lowering;  /* trs_plan_create only.  0: when the format holds its input CSR (a format
                              built in this process from canonical input), the MFMA tiles are cut
                              from the format on the host and the residual (the input CSR minus the

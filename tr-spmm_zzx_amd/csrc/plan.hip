@@ -63,6 +63,11 @@ Status fail(int code, const std::string& m) { return Status{code, m}; }
 // unsplit layout below K = 128, where the split measured slower: K = 32 / 64 / 96 +65% / +20% / +8%).
 constexpr int32_t kSpmmSplitMin = 256;
 constexpr int32_t kSddmmSplitMin = 512;
+// ... and only when those rows' entries are at least this many times their distinct columns:
+// R-MAT's rows of >= 256 entries gather 20.0M times from 0.60M columns (33x), the 64 hubs of the
+// grid+hubs graph 6.4M times from 3.3M columns (1.9x), where the split measured +9% at K = 128
+// (1.144 -> 1.249 ms) and +3% at K = 64.
+constexpr int32_t kSplitMinReuse = 4;
 
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
@@ -455,8 +460,14 @@ struct Placement {
 // a split row r are col[col_rowptr[r] ..] (col_rowptr = rowptr for the residual CSR itself; the
 // input CSR's row pointers when the residual is built on the device, where split rows -- owned by
 // no window, so no tile took entries from them -- equal their input rows).
+//
+// min_reuse > 0 (the automatic split): split only when the candidate rows' entries are at least
+// min_reuse times their distinct columns.  The split buys L2 reuse of B rows; columns the long rows
+// read once or twice each (uniformly random hub rows) have none to buy, and the split's extra
+// launch and partial slots then cost time.
 Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, const int32_t* col_rowptr, int32_t m,
-                        int32_t n, const std::vector<uint8_t>& owned, bool compact, int32_t split_min) {
+                        int32_t n, const std::vector<uint8_t>& owned, bool compact, int32_t split_min,
+                        int32_t min_reuse = 0) {
   Placement P;
   P.compact = compact;
   const int64_t nent = rowptr[m];
@@ -467,6 +478,37 @@ Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, 
         P.split[r] = 1;
         P.split_rows.push_back(r);
       }
+  if (min_reuse > 0 && !P.split_rows.empty()) {
+    // distinct columns of the candidate rows: per-thread bitmaps, OR-ed
+    const int T = lowering_threads();
+    const size_t ns = P.split_rows.size();
+    const size_t words = ((size_t)n + 63) / 64;
+    std::vector<std::vector<uint64_t>> seen(T);
+    std::vector<int64_t> entries(T, 0);
+    parallel_parts(T, (int64_t)ns, 256, [&](int t) { return (int64_t)ns * t / T; }, [&](int64_t b, int64_t e, int t) {
+      std::vector<uint64_t>& bits = seen[t];
+      bits.assign(words, 0);
+      for (int64_t i = b; i < e; ++i) {
+        const int32_t r = P.split_rows[i];
+        const int32_t* c = col + col_rowptr[r];
+        const int32_t len = rowptr[r + 1] - rowptr[r];
+        for (int32_t q = 0; q < len; ++q) bits[(uint32_t)c[q] >> 6] |= 1ull << (c[q] & 63);
+        entries[t] += len;
+      }
+    });
+    int64_t distinct = 0, total = 0;
+    for (int t = 0; t < T; ++t) total += entries[t];
+    for (size_t w = 0; w < words; ++w) {
+      uint64_t x = 0;
+      for (int t = 0; t < T; ++t)
+        if (!seen[t].empty()) x |= seen[t][w];
+      distinct += __builtin_popcountll(x);
+    }
+    if (total < (int64_t)min_reuse * distinct) {
+      for (int32_t r : P.split_rows) P.split[r] = 0;
+      P.split_rows.clear();
+    }
+  }
   const size_t ns = P.split_rows.size();
   // entries per (split row, XCD), counted by the column hash on a few threads
   std::vector<int32_t> cnt(ns * trs::kXcds, 0);
@@ -1057,8 +1099,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   // residual tasks over rows not owned by an MFMA window
   // XCD column split for SpMM (each sub-row costs a partial slot of 4 K bytes written and read back)
   const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSpmmSplitMin;
-  const Placement PL = src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, owned, true, split_min)
-                           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, owned, true, split_min);
+  const int32_t reuse = opt.xcd_split == 0 ? kSplitMinReuse : 0;
+  const Placement PL =
+      src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, owned, true, split_min, reuse)
+          : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, owned, true, split_min, reuse);
   std::vector<int32_t> col2;
   std::vector<uint16_t> val2;
   if (!src) move_entries(PL, rowptr, col.data(), val.data(), m, col2, &val2, nullptr);
@@ -1248,8 +1292,10 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   // (device lowering: split rows hold no tile entries -- there are none -- so their columns are
   // the input rows')
   const int32_t split = with_pos ? 0 : split_min;
-  const Placement PL = src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, {}, false, split)
-                           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, split);
+  const int32_t reuse = opt.xcd_split == 0 ? kSplitMinReuse : 0;
+  const Placement PL =
+      src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, {}, false, split, reuse)
+          : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, split, reuse);
   std::vector<int32_t> col2, x_pos;
   if (!src) move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos);
   Tasks T = build_tasks(PL, rowptr, m, {}, false, opt);
