@@ -446,8 +446,8 @@ int env_int(const char* name, int dflt) {       // block_online.cpp:124-128
   return v ? std::atoi(v) : dflt;
 }
 
-template <class T>
-void append_at(std::vector<T>& dst, size_t at, const std::vector<T>& src) {
+template <class T, class A>
+void append_at(std::vector<T, A>& dst, size_t at, const std::vector<T>& src) {
   if (!src.empty()) std::memcpy(dst.data() + at, src.data(), src.size() * sizeof(T));
 }
 
@@ -625,9 +625,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
     append_at(F->spill_val, o.sp, W.sp_val);
     W = Win();   // release per-window memory early
   }
-  const auto t1 = std::chrono::high_resolution_clock::now();
-  F->elapsed = std::chrono::duration<double>(t1 - t0).count();
-  // keep the input CSR for device-side plan lowering (not part of the reference's build time)
+  // keep the input CSR for device-side plan lowering (counted in the build time)
   if (canonical) {
     try {
       F->csr_rowptr.assign(rowptr, rowptr + (size_t)rows + 1);
@@ -636,6 +634,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
     } catch (const std::bad_alloc&) {
       F->csr_rowptr.clear(); F->csr_col.clear(); F->csr_val.clear();
       F->csr_col.shrink_to_fit(); F->csr_val.shrink_to_fit();
+      F->elapsed = std::chrono::duration<double>(std::chrono::high_resolution_clock::now() - t0).count();
       *out = F;
       return TRS_OK;   // the plan then lowers on the host
     }
@@ -647,6 +646,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
       std::memcpy(F->csr_val.data() + b, val + b, (size_t)(e - b) * sizeof(float));
     }
   }
+  F->elapsed = std::chrono::duration<double>(std::chrono::high_resolution_clock::now() - t0).count();
   *out = F;
   return TRS_OK;
 }
