@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <numeric>
+#include <immintrin.h>
 #include <omp.h>
 #include <vector>
 
@@ -408,30 +409,34 @@ void build_window(const int32_t* rowptr, const int32_t* col, const float* val, i
       if (!S.covered[e - e0]) { W.sp_row.push_back(r); W.sp_col.push_back(col[e]); W.sp_val.push_back(val[e]); }
 
   // ---- tiles of 4 groups (block_online.cpp:796-841) ----
-  for (int base = 0; base < ng; base += 4) {
-    W.tile_group.push_back(base);
+  const int ntile = (ng + 3) / 4;
+  W.tile_group.resize(ntile);
+  W.tile_cols.resize((size_t)ntile * 16);
+  W.packed_meta.resize((size_t)ntile * 8);
+  W.packed_a.resize((size_t)ntile * 64);
+  for (int ti = 0; ti < ntile; ++ti) {
+    const int base = ti * 4;
+    W.tile_group[ti] = base;
     for (int k = 0; k < 16; ++k) {
       const int g = base + k / 4;
-      W.tile_cols.push_back(g < ng ? W.s_col[g * 4 + k % 4] : -1);
+      W.tile_cols[(size_t)ti * 16 + k] = g < ng ? W.s_col[g * 4 + k % 4] : -1;
     }
     for (int rg = 0; rg < 8; ++rg) {
-      float a0[8], a1[8];
+      // per chunk c: the two values of row rg, then the two of row rg + 8 (one int32 word each,
+      // low half first)
+      float a[16];
       uint32_t meta = 0;
       for (int c = 0; c < 4; ++c) {
-        float v0, v1;
         int p0, p1;
-        load_chunk(W, base + c, ng, rg, window, v0, v1, p0, p1);
-        a0[2 * c] = v0; a0[2 * c + 1] = v1;
+        load_chunk(W, base + c, ng, rg, window, a[4 * c], a[4 * c + 1], p0, p1);
         meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (4 * c);
-        load_chunk(W, base + c, ng, rg + 8, window, v0, v1, p0, p1);
-        a1[2 * c] = v0; a1[2 * c + 1] = v1;
+        load_chunk(W, base + c, ng, rg + 8, window, a[4 * c + 2], a[4 * c + 3], p0, p1);
         meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (16 + 4 * c);
       }
-      W.packed_meta.push_back((int32_t)meta);
-      for (int t = 0; t < 4; ++t) {
-        W.packed_a.push_back((int32_t)((uint32_t)trs::half_bits(a0[2 * t]) | ((uint32_t)trs::half_bits(a0[2 * t + 1]) << 16)));
-        W.packed_a.push_back((int32_t)((uint32_t)trs::half_bits(a1[2 * t]) | ((uint32_t)trs::half_bits(a1[2 * t + 1]) << 16)));
-      }
+      W.packed_meta[(size_t)ti * 8 + rg] = (int32_t)meta;
+      uint16_t h[16];
+      trs::half_bits_n(a, h, 16);
+      std::memcpy(&W.packed_a[((size_t)ti * 8 + rg) * 8], h, sizeof(h));
     }
   }
 }
@@ -458,6 +463,28 @@ uint16_t half_bits(float f) {
   uint32_t x;
   std::memcpy(&x, &f, 4);
   return half_bits_of(x);
+}
+
+namespace {
+// 8 conversions with the x86 F16C instruction (IEEE round to nearest even, like half_bits_of for
+// every input but NaN, whose payload the instruction keeps: those lanes are redone by
+// half_bits_of).
+__attribute__((target("avx,f16c"))) void half_bits8_f16c(const float* src, uint16_t* dst) {
+  const __m256 x = _mm256_loadu_ps(src);
+  _mm_storeu_si128(reinterpret_cast<__m128i*>(dst), _mm256_cvtps_ph(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+  const __m256 nan = _mm256_cmp_ps(x, x, _CMP_UNORD_Q);
+  if (!_mm256_testz_ps(nan, nan))
+    for (int i = 0; i < 8; ++i)
+      if (src[i] != src[i]) dst[i] = half_bits(src[i]);
+}
+const bool has_f16c = __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx");
+}  // namespace
+
+void half_bits_n(const float* src, uint16_t* dst, int64_t n) {
+  int64_t i = 0;
+  if (has_f16c)
+    for (; i + 8 <= n; i += 8) half_bits8_f16c(src + i, dst + i);
+  for (; i < n; ++i) dst[i] = half_bits(src[i]);
 }
 }  // namespace trs
 

@@ -63,4 +63,5 @@ struct trs_format {
 namespace trs {
 void set_error(const std::string& msg);
 uint16_t half_bits(float f);   // IEEE binary16, round to nearest even (c10::Half semantics)
+void half_bits_n(const float* src, uint16_t* dst, int64_t n);   // the same for n values
 }  // namespace trs
