@@ -129,6 +129,10 @@ def test_reference_harness_flow_through_dataset(tmp_path, monkeypatch):
             d.num_nodes_dst, 3)
     out, ms, tc, cl, cs, sp = L6.forward_fp16_tcu_cuda_sptc_mma_parallel_online(*args)
     assert out.shape == (g.m, 64) and float(ms) > 0
+    # per-path completion times from the common start (mGCNkernel_online.cu:1676-1687), paths in
+    # launch order residual -> MFMA windows -> fixups
+    tc, cl, cs, sp = float(tc), float(cl), float(cs), float(sp)
+    assert 0 < cl <= tc <= cs and sp == tc, (float(ms), tc, cl, cs, sp)
     t = [getattr(d, n) for n in ("t_rowNew_offsetTensor", "t_blockTensor", "t_columnTensor", "t_valueTensor",
                                  "t_window_rowTensor", "t_atomicTensor", "t_binaryTensor", "c_row_offsetTensor",
                                  "c_rowTensor", "c_atomicTensor", "c_colTensor", "c_valueTensor",

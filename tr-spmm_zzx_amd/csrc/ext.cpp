@@ -309,11 +309,21 @@ std::vector<torch::Tensor> parallel_online(
   PlanGuard pg;
   ok(trs_plan_create_parallel(&a, nullptr, &pg.p), "forward_fp16_tcu_cuda_sptc_mma_parallel_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
-  // per-share times: the MFMA window kernel carries the TC (and dense 2:4) share, the residual
-  // task kernel the long residual parts, the fixup the split rows; 2:4 groups are folded into
-  // those two kernels, so no separate time exists for them (0)
-  return {res.out, torch::tensor(res.ms), torch::tensor(res.kernel_ms[1]), torch::tensor(res.kernel_ms[0]),
-          torch::tensor(res.kernel_ms[2]), torch::tensor(0.0f)};
+  // Per-path times with the reference's meaning (mGCNkernel_online.cu:1676-1687): the time from
+  // the common start of the `epoches` launches to the completion of that path, divided by
+  // `epoches`.  Here the paths are kernels of one stream, run in the order residual tasks ->
+  // MFMA windows -> split-row fixups in every launch: path X completes (epoches - 1) steps plus
+  // its offset inside the last step after the start.  TC = the MFMA window kernel (dense TC and
+  // 2:4 tiles), cuda_long = the residual task kernel, cuda_short = the fixups; the 2:4 groups
+  // finish with the MFMA window kernel (dense tiles) and the residual kernel (the rest), so their
+  // completion is the later of the two, the MFMA window kernel's.
+  const float e = (float)epoches;
+  auto completion = [&](float offset) { return ((e - 1.f) * res.ms + offset) / e; };
+  const float t_long = completion(res.kernel_ms[0]);
+  const float t_tc = completion(res.kernel_ms[0] + res.kernel_ms[1]);
+  const float t_short = completion(res.kernel_ms[0] + res.kernel_ms[1] + res.kernel_ms[2]);
+  return {res.out, torch::tensor(res.ms), torch::tensor(t_tc), torch::tensor(t_long), torch::tensor(t_short),
+          torch::tensor(t_tc)};
 }
 
 std::vector<torch::Tensor> sptc_online(torch::Tensor s_column, torch::Tensor s_value, torch::Tensor s_pos,

@@ -604,17 +604,16 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
 
   for (int t = w.tile_begin; t < w.tile_end; ++t) {
     __syncthreads();
-    // stage the 16 gathered B rows (features [fbase, fbase + KC)) into LDS; loads unconditional
-    // (empty column slots read row 0, features past K read the row's last VEC) and then zeroed
+    // stage the 16 gathered B rows (features [fbase, fbase + KC)) into LDS; empty column slots
+    // and features past K are zeros, not gathered
     const int per_row = KC / VEC;
     for (int idx = threadIdx.x; idx < 16 * per_row; idx += 256) {
       const int k = idx / per_row;
       const int ff = (idx % per_row) * VEC;
       const int c = P.tile_cols[t * 16 + k];
-      const bool in = c >= 0 && fbase + ff < K;
       BFrag<VEC> b;
-      b.load(B + row_offset(c >= 0 ? c : 0, ldb) + (fbase + ff < K ? fbase + ff : K - VEC));
-      if (!in) b.zero();
+      if (c >= 0 && fbase + ff < K) b.load(B + row_offset(c, ldb) + fbase + ff);
+      else b.zero();
       if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * KCB + ff) = b.v;
       else if constexpr (VEC == 4) *reinterpret_cast<half4_t*>(bst + k * KCB + ff) = b.v;
       else if constexpr (VEC == 2) *reinterpret_cast<half2_t*>(bst + k * KCB + ff) = b.v;
