@@ -285,7 +285,7 @@ def load_traffic(kernel: str, workload: str):
         return None, None
     with open(path) as f:
         d = json.load(f)
-    src = f"profiles/{os.path.basename(path)[:-5]}.md ({d.get('measured', 'earlier run')}; a separate " \
+    src = f"{d.get('source', 'profiles/' + os.path.basename(path))} ({d.get('measured', 'earlier run')}; a separate " \
           "rocprofv3 --pmc run, not this one)"
     return d.get("hbm_bytes_per_launch"), src
 
