@@ -168,7 +168,8 @@ typedef struct trs_plan_options {
                              residual SDDMM outputs (keeps them from evicting gathered B / Y
                              rows); 0 plain; -1 automatic (bit 1) */
   int32_t window_row_cap; /* longest residual row an MFMA window may carry before its tiles go
-                             back to the residual path (0 = automatic) */
+                             back to the residual path, when that row is also more than twice
+                             its window's mean residual row (0 = automatic: 128) */
   int32_t xcd_run;        /* workgroups are remapped so each of the 8 XCDs (own L2) runs this many
                              consecutive work items in a row; 1 = hardware round robin,
                              0 = automatic */
@@ -195,6 +196,13 @@ typedef struct trs_plan_options {
                              from the format on the host and the residual (the input CSR minus the
                              kept tiles' entries, XCD sub-rows included) is built on the device;
                              the plan is the same as the host lowering's.  1: always on the host */
+  int32_t sptc_sparse;    /* SpMM plans: 1 = MFMA tiles whose every row has at most 2 entries in
+                             each group of 4 columns (the 2:4 group tiles, and TC tiles that happen
+                             to be 2:4) run on gfx950's sparse v_smfmac_f32_16x16x64_f16, four tiles
+                             (64 columns) per instruction, their values stored compressed with
+                             2-bit column indices, as the reference runs its packed 2:4 tiles on
+                             mma.sp (mGCNkernel_online.cu:812-933) (default); 0 = every tile on
+                             the dense v_mfma_f32_16x16x16_f16 with zero fill */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);
@@ -274,6 +282,7 @@ typedef struct trs_plan_stats {
   int64_t mfma_windows;              /* 16-row windows owned by the MFMA window kernel */
   int64_t window_csr_nnz;            /* residual nonzeros inside those windows */
   int64_t device_lowered;            /* 1: the residual was built on the device (host_lowering) */
+  int64_t sparse_tiles;              /* of mfma_tiles, those run on the sparse MFMA (sptc_sparse) */
 } trs_plan_stats;
 
 int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s);

@@ -121,6 +121,15 @@ std::vector<torch::Tensor> block_sptc_2to4_online_with_spill(torch::Tensor row1,
                     sptc_min_util, sptc_threshold, true);
 }
 
+// Plan options of the operators whose reference kernels run 2:4 tiles on sparse tensor cores
+// (mma.sp, mGCNkernel_online.cu:570-786, 812-933): 2:4 tiles on gfx950's sparse MFMA.
+trs_plan_options sparse_tile_options() {
+  trs_plan_options o;
+  trs_plan_options_default(&o);
+  o.sptc_sparse = 1;
+  return o;
+}
+
 struct RunResult {
   torch::Tensor out;
   float ms = 0.f;
@@ -307,7 +316,8 @@ std::vector<torch::Tensor> parallel_online(
   a.parts_t = tc_parts; a.parts_c = parts_c; a.partsize_c = partsize_c; a.parts_c_short = parts_c_short;
   a.window = window; a.m = mOri; a.n = kOri;
   PlanGuard pg;
-  ok(trs_plan_create_parallel(&a, nullptr, &pg.p), "forward_fp16_tcu_cuda_sptc_mma_parallel_online");
+  const trs_plan_options po = sparse_tile_options();
+  ok(trs_plan_create_parallel(&a, &po, &pg.p), "forward_fp16_tcu_cuda_sptc_mma_parallel_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
   // Per-path times with the reference's meaning (mGCNkernel_online.cu:1676-1687): the time from
   // the common start of the `epoches` launches to the completion of that path, divided by
@@ -380,8 +390,9 @@ std::vector<torch::Tensor> sptc_mma_online(torch::Tensor s_column, torch::Tensor
   TORCH_CHECK(s_value.size(0) == groups, "s_value group count mismatch");
   TORCH_CHECK(s_pos.size(0) == groups, "s_pos group count mismatch");
   PlanGuard pg;
+  const trs_plan_options po = sparse_tile_options();
   ok(trs_plan_create_sptc(s_column.data_ptr<int32_t>(), s_value.data_ptr<float>(), s_pos.data_ptr<int8_t>(), groups,
-                          nullptr, s_offsets.data_ptr<int32_t>(), s_offsets.numel(), window, mOri, kOri, nullptr,
+                          nullptr, s_offsets.data_ptr<int32_t>(), s_offsets.numel(), window, mOri, kOri, &po,
                           &pg.p),
      "forward_fp16_sptc_mma_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
@@ -415,9 +426,10 @@ std::vector<torch::Tensor> sptc_mma_packed_online(torch::Tensor s_tile_column, t
   TORCH_CHECK(s_packed_a.size(0) == tiles, "s_packed_a tile count mismatch");
   TORCH_CHECK(s_packed_meta.size(0) == tiles, "s_packed_meta tile count mismatch");
   PlanGuard pg;
+  const trs_plan_options po = sparse_tile_options();
   ok(trs_plan_create_sptc_packed(s_tile_column.data_ptr<int32_t>(), s_packed_a.data_ptr<int32_t>(),
                                  s_packed_meta.data_ptr<int32_t>(), s_window_tile_offset.data_ptr<int32_t>(), tiles,
-                                 s_window_tile_offset.numel(), window, mOri, kOri, nullptr, &pg.p),
+                                 s_window_tile_offset.numel(), window, mOri, kOri, &po, &pg.p),
      "forward_fp16_sptc_mma_packed_online");
   auto res = run_plan(pg.p, rhs_matrix, dimN, mOri, kOri, epoches);
   return {res.out, torch::tensor(res.ms)};

@@ -26,6 +26,8 @@
 //                   that is not a multiple of 8.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "half.hpp"
 #include "kernels.hpp"
 
@@ -35,6 +37,7 @@ namespace {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half16_t __attribute__((ext_vector_type(16)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
@@ -592,7 +595,8 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
   float* otile = reinterpret_cast<float*>(smem);
   _Float16* bst = reinterpret_cast<_Float16*>(otile + 16 * KCP);
 
-  const MfmaWindow w = P.mwin[xcd_remap(blockIdx.x, gridDim.x, P.xcd_run)];
+  const int wi = xcd_remap(blockIdx.x, gridDim.x, P.xcd_run);
+  const MfmaWindow w = P.mwin[wi];
   const int fbase = blockIdx.y * KC;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -630,6 +634,45 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) b[i] = bst[(4 * (lane >> 4) + i) * KCB + nt * 16 + (lane & 15)];
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[j], 0, 0, 0);
+      }
+    }
+  }
+  // 2:4 quads on the sparse MFMA (layout in DevicePlan): per 64-feature chunk j, the quad's 64 B
+  // rows are staged row-major ([64][72] fp16, reusing the dense staging space); lane l's B operand
+  // is B[k][16 * wave + l % 16] for k = 8 (l / 16) + s (s < 8) and 32 + 8 (l / 16) + s - 8 (s >= 8)
+  if (P.win_quad) {
+    constexpr int QS = 72;   // staged row stride (fp16)
+    const int qb = P.win_quad[wi], qe = P.win_quad[wi + 1];
+    for (int q = qb; q < qe; ++q) {
+      const half8_t a = reinterpret_cast<const half8_t*>(P.quad_a)[(int64_t)q * 64 + lane];
+      const int idx = P.quad_idx[(int64_t)q * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < NTILE; ++j) {
+        __syncthreads();
+        const int per_row = 64 / VEC;
+        for (int i2 = threadIdx.x; i2 < 64 * per_row; i2 += 256) {
+          const int k = i2 / per_row;
+          const int ff = (i2 % per_row) * VEC;
+          const int c = P.quad_cols[(int64_t)q * 64 + k];
+          const int f = fbase + 64 * j + ff;
+          BFrag<VEC> b;
+          if (c >= 0 && f < K) b.load(B + row_offset(c, ldb) + f);
+          else b.zero();
+          if constexpr (VEC == 8) *reinterpret_cast<half8_t*>(bst + k * QS + ff) = b.v;
+          else if constexpr (VEC == 4) *reinterpret_cast<half4_t*>(bst + k * QS + ff) = b.v;
+          else if constexpr (VEC == 2) *reinterpret_cast<half2_t*>(bst + k * QS + ff) = b.v;
+          else bst[k * QS + ff] = b.v;
+        }
+        __syncthreads();
+        if (wave + 4 * j < ntn) {
+          half16_t b;
+#pragma unroll
+          for (int s2 = 0; s2 < 16; ++s2) {
+            const int k = s2 < 8 ? 8 * (lane >> 4) + s2 : 32 + 8 * (lane >> 4) + (s2 - 8);
+            b[s2] = bst[k * QS + wave * 16 + (lane & 15)];
+          }
+          acc[j] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(a, b, acc[j], idx, 0, 0);
+        }
       }
     }
   }
@@ -1096,7 +1139,9 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     const int kc16 = ((K + 15) / 16) * 16;
     const int KC = kc16 < 256 ? kc16 : 256;
     dim3 grid(p.nmwin, (K + KC - 1) / KC);
-    const size_t shm = (size_t)16 * (KC + 4) * 4 + (size_t)16 * (KC + 8) * 2;
+    // staging space: 16 dense-tile B rows of KC features, or a quad's 64 rows of 64 (stride 72)
+    const size_t stage = std::max<size_t>((size_t)16 * (KC + 8), p.nquads > 0 ? (size_t)64 * 72 : 0);
+    const size_t shm = (size_t)16 * (KC + 4) * 4 + stage * 2;
     if (KC <= 64) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 1>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
     else if (KC <= 128) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 2>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
     else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 4>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);

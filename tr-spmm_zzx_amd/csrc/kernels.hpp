@@ -48,6 +48,16 @@ struct DevicePlan {
   const int32_t* tile_cols = nullptr;  // [tiles][16]
   const uint16_t* tile_a = nullptr;    // [tiles][16 rows][16 cols] fp16 (SpMM)
   int32_t ntiles = 0;
+  // SpMM 2:4 quads (sptc_sparse): window i owns quads [win_quad[i], win_quad[i + 1]); quad q covers
+  // four 16-column tiles, tile b as columns 16 b .. 16 b + 15 (quad_cols[q][64], -1 = none); lane l
+  // of v_smfmac_f32_16x16x64_f16 holds row l % 16 of tile l / 16: quad_a[q][l][8] fp16, two values
+  // per group of 4 columns, at the 2-bit column positions packed in quad_idx[q][l] (value j at
+  // bits 2j .. 2j + 1).
+  const int32_t* win_quad = nullptr;
+  const int32_t* quad_cols = nullptr;
+  const uint16_t* quad_a = nullptr;
+  const uint16_t* quad_idx = nullptr;
+  int32_t nquads = 0;
   // SDDMM plans: output index of each residual entry (null = identity; see res_off) and, per tile, its first
   // row and the output index of each of its 256 (row, column) slots (-1 = not stored)
   const int32_t* res_pos = nullptr;

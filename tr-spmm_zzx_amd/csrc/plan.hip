@@ -69,6 +69,15 @@ constexpr int32_t kSddmmSplitMin = 512;
 // (1.144 -> 1.249 ms) and +3% at K = 64.
 constexpr int32_t kSplitMinReuse = 4;
 
+// A tile-owning window goes back to the residual kernel when its longest residual row exceeds
+// window_row_cap and this many times the mean of its rows: the window kernel walks each row with
+// one lane group, so only a row far longer than its neighbours stalls the workgroup (R-MAT hub
+// windows).  Windows of uniformly long rows keep their tiles: a block graph of 2048-node
+// communities (p_in 0.2, 54.7M entries, ~280 residual entries in every row) ran at 0.924 / 2.082 ms
+// (K = 128 / 256) with every window handed back under the length rule alone, 0.796 / 1.473 ms with
+// this one; R-MAT, SBM and grid+hubs plans are unchanged (ratio 4 measured the same as 2).
+constexpr int32_t kWindowRowRatio = 2;
+
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
   const unsigned h = std::thread::hardware_concurrency();
@@ -840,6 +849,69 @@ void sort_tiles(std::vector<Lowering::Tile>& tiles) {
   tiles.swap(sorted);
 }
 
+// A tile whose every row holds at most 2 entries in each group of 4 columns (2:4 structured).
+bool is_two_four(const Lowering::Tile& t) {
+  for (int r = 0; r < 16; ++r) {
+    const uint64_t bits = (t.present[r / 4] >> ((r % 4) * 16)) & 0xffffull;
+    for (int g = 0; g < 4; ++g)
+      if (__builtin_popcountll((bits >> (4 * g)) & 0xfull) > 2) return false;
+  }
+  return true;
+}
+
+// Sparse-MFMA operands of 2:4 tiles, four tiles (a quad, 64 columns) at a time, in the lane layout
+// of v_smfmac_f32_16x16x64_f16 (kernels.hpp, DevicePlan::quad_*).
+struct Quads {
+  std::vector<int32_t> cols;    // [quad][64]
+  std::vector<uint16_t> a;      // [quad][64 lanes][8] fp16
+  std::vector<uint16_t> idx;    // [quad][64 lanes]: 2-bit positions, value j at bits 2j .. 2j + 1
+  int32_t count = 0;
+};
+
+// Tiles [b, e) (at most 4) as the next quad; missing tiles are empty.  In each (row, group of 4
+// columns) the present entries, at most 2, take the group's two slots in column order; a single
+// entry is paired with a zero at another position (position 1 if it sits at 0, else 0), an empty
+// group with zeros at 0 and 1, so every slot pair names two distinct positions in ascending order.
+void add_quad(Quads& Q, const std::vector<Lowering::Tile>& tiles, size_t b, size_t e) {
+  const size_t q = (size_t)Q.count++;
+  Q.cols.resize((q + 1) * 64, -1);
+  Q.a.resize((q + 1) * 64 * 8, 0);
+  Q.idx.resize((q + 1) * 64, 0);
+  for (size_t lb = 0; lb < 4 && b + lb < e; ++lb) {
+    const Lowering::Tile& t = tiles[b + lb];
+    for (int k = 0; k < 16; ++k) Q.cols[q * 64 + lb * 16 + k] = t.cols[k];
+    for (int r = 0; r < 16; ++r) {
+      const size_t lane = q * 64 + lb * 16 + r;
+      uint32_t ix = 0;
+      for (int g = 0; g < 4; ++g) {
+        int pos[2] = {0, 1};
+        float val[2] = {0.f, 0.f};
+        int n = 0;
+        for (int p = 0; p < 4; ++p)
+          if (Lowering::tile_has(t, r, 4 * g + p)) {
+            pos[n] = p;
+            val[n] = t.a[r * 16 + 4 * g + p];
+            ++n;
+          }
+        if (n == 1 && pos[0] != 0) {   // one entry at p > 0: a zero at 0 first
+          pos[1] = pos[0];
+          val[1] = val[0];
+          pos[0] = 0;
+          val[0] = 0.f;
+        } else if (n == 1) {
+          pos[1] = 1;
+          val[1] = 0.f;
+        }
+        for (int h = 0; h < 2; ++h) {
+          Q.a[lane * 8 + 2 * g + h] = trs::half_bits(val[h]);
+          ix |= (uint32_t)pos[h] << (2 * (2 * g + h));
+        }
+      }
+      Q.idx[lane] = (uint16_t)ix;
+    }
+  }
+}
+
 // Internal status of the device lowering: the format's tiles and its input CSR disagree (a tile
 // entry the CSR does not hold, or two tiles holding one entry) or its temporaries could not be
 // allocated; the caller then lowers on the host.
@@ -1035,8 +1107,14 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     bool any_demote = false;
     for (int32_t b = 0; b < nblocks; ++b) {
       if (!owned[b]) continue;
-      for (int32_t r = b * 16; r < std::min(m, b * 16 + 16); ++r)
-        if (len[r] > row_cap) demote[b] = 1;
+      int64_t longest = 0, sum = 0, rows = 0;
+      for (int32_t r = b * 16; r < std::min(m, b * 16 + 16); ++r) {
+        longest = std::max<int64_t>(longest, len[r]);
+        sum += len[r];
+        ++rows;
+      }
+      // only a row much longer than its window's others stalls the workgroup
+      demote[b] = longest > row_cap && longest * rows > (int64_t)kWindowRowRatio * sum;
       any_demote |= demote[b] != 0;
     }
     if (any_demote) {
@@ -1079,10 +1157,24 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     });
   }
   std::vector<trs::MfmaWindow> mwin;
+  // sptc_sparse: a window's 2:4 tiles go behind its dense ones and into quads of four
+  const bool sparse = opt.sptc_sparse != 0;
+  std::vector<int32_t> win_quad(1, 0);
+  Quads Q;
+  int64_t sparse_tiles = 0;
   for (size_t i = 0; i < L.tiles.size();) {
     size_t j = i;
     while (j < L.tiles.size() && L.tiles[j].row0 == L.tiles[i].row0) ++j;
-    mwin.push_back({L.tiles[i].row0, (int32_t)i, (int32_t)j, 0});
+    size_t dense_end = j;
+    if (sparse) {
+      dense_end = (size_t)(std::stable_partition(L.tiles.begin() + i, L.tiles.begin() + j,
+                                                 [](const Lowering::Tile& t) { return !is_two_four(t); }) -
+                           L.tiles.begin());
+      for (size_t b = dense_end; b < j; b += 4) add_quad(Q, L.tiles, b, std::min(j, b + 4));
+      sparse_tiles += (int64_t)(j - dense_end);
+      win_quad.push_back(Q.count);
+    }
+    mwin.push_back({L.tiles[i].row0, (int32_t)i, (int32_t)dense_end, 0});
     i = j;
   }
   std::vector<int32_t> tile_cols(L.tiles.size() * 16);
@@ -1125,6 +1217,10 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   const size_t o_mwin = blob.add(mwin);
   const size_t o_tcol = blob.add(tile_cols);
   const size_t o_ta = blob.add(tile_a);
+  const size_t o_wq = blob.add(win_quad);
+  const size_t o_qcol = blob.add(Q.cols);
+  const size_t o_qa = blob.add(Q.a);
+  const size_t o_qidx = blob.add(Q.idx);
   trs_plan* P = nullptr;
   {
     const Status us = upload(blob, P);
@@ -1167,6 +1263,13 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   d.tile_cols = reinterpret_cast<const int32_t*>(base + o_tcol);
   d.tile_a = reinterpret_cast<const uint16_t*>(base + o_ta);
   d.ntiles = (int32_t)L.tiles.size();
+  if (Q.count > 0) {
+    d.win_quad = reinterpret_cast<const int32_t*>(base + o_wq);
+    d.quad_cols = reinterpret_cast<const int32_t*>(base + o_qcol);
+    d.quad_a = reinterpret_cast<const uint16_t*>(base + o_qa);
+    d.quad_idx = reinterpret_cast<const uint16_t*>(base + o_qidx);
+    d.nquads = Q.count;
+  }
   d.feature_lanes = opt.feature_lanes;
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
@@ -1194,6 +1297,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     for (int32_t r = w.row0; r < std::min(m, w.row0 + 16); ++r) wnnz += rowptr[r + 1] - rowptr[r];
   s.window_csr_nnz = wnnz;
   s.device_lowered = src ? 1 : 0;
+  s.sparse_tiles = sparse_tiles;
   *out = P;
   return Status{};
 }
@@ -1436,6 +1540,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->occupancy = 0;
   o->xcd_split = 0;
   o->host_lowering = 0;
+  o->sptc_sparse = 1;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }

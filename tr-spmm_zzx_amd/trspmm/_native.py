@@ -31,14 +31,15 @@ class PlanOptions(ctypes.Structure):
     _fields_ = [("mfma_tc", c_i32), ("mfma_sptc", c_i32), ("sptc_min_fill", c_f32), ("task_nnz", c_i32),
                 ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
                 ("xcd_run", c_i32), ("sddmm_unroll", c_i32), ("stage", c_i32),
-                ("occupancy", c_i32), ("xcd_split", c_i32), ("host_lowering", c_i32)]
+                ("occupancy", c_i32), ("xcd_split", c_i32), ("host_lowering", c_i32),
+                ("sptc_sparse", c_i32)]
 
 
 class PlanStats(ctypes.Structure):
     _fields_ = [("m", c_i64), ("n", c_i64), ("nnz", c_i64), ("mfma_tiles", c_i64), ("mfma_nnz", c_i64),
                 ("csr_nnz", c_i64), ("tasks", c_i64), ("split_rows", c_i64), ("partial_slots", c_i64),
                 ("device_bytes", c_i64), ("mfma_windows", c_i64), ("window_csr_nnz", c_i64),
-                ("device_lowered", c_i64)]
+                ("device_lowered", c_i64), ("sparse_tiles", c_i64)]
 
 
 class ReorderParams(ctypes.Structure):

@@ -232,14 +232,17 @@ class Plan:
                     feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
                     stage: Optional[int] = None, occupancy: Optional[int] = None,
-                    xcd_split: Optional[int] = None, host_lowering: bool = False) -> "Plan":
+                    xcd_split: Optional[int] = None, host_lowering: bool = False,
+                    sptc_sparse: bool = True) -> "Plan":
         """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default).  host_lowering=True builds the
-        residual on the host even when the format holds its input CSR (the plan is the same)."""
+        residual on the host even when the format holds its input CSR (the plan is the same);
+        sptc_sparse=False runs 2:4 tiles on the dense MFMA with zero fill instead of the sparse one."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap,
                      xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split)
         o.host_lowering = int(bool(host_lowering))
+        o.sptc_sparse = int(bool(sptc_sparse))
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
         return cls(h.value)
