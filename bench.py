@@ -321,6 +321,8 @@ def main():
                          "tca-aligned keeps clusters inside 16-row windows")
     ap.add_argument("--host-lowering", action="store_true",
                     help="build the plan's residual on the host (default: on the device from the input CSR)")
+    ap.add_argument("--feature-lanes", type=int, default=None,
+                    help="plan option feature_lanes (lanes per lane group; fewer lanes = several feature passes)")
     ap.add_argument("--window-row-cap", type=int, default=None,
                     help="plan option window_row_cap (tiled windows with a longer residual row go back to the "
                          "residual kernel; default 128)")
@@ -367,7 +369,7 @@ def main():
     torch.cuda.synchronize()
     t1 = time.time()
     plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                   window_row_cap=args.window_row_cap)
+                                   window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes)
     pre["plan_s"] = round(time.time() - t1, 3)
     pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
     if "reorder_s" in pre:

@@ -6,7 +6,7 @@ columns) compressed -- two fp16 values and two 2-bit column positions per row an
 four tiles per sparse MFMA instruction.  Checked against the float64 CSR oracle at the SpMM
 tolerance, and against the dense-tile plan over the same tiles (the same fp16 products, summed in
 another order inside the MFMA: equal to fp32 rounding), for feature widths that take each staging
-load width (16-, 8-, 4- and 2-byte) and 1, 2 and 4 MFMA n-tiles per wave.
+load width (16-, 8-, 4- and 2-byte) and 1 and 2 MFMA n-tiles per wave.
 """
 import numpy as np
 import pytest

@@ -577,7 +577,7 @@ __global__ __launch_bounds__(256) void k_spmm_fixup(DevicePlan P, int K, float* 
 }
 
 // ------------------------------------------------------------------------------------------------
-// MFMA window kernel.  KC = features per workgroup (multiple of 16, <= 256); NT = MFMA n-tiles
+// MFMA window kernel.  KC = features per workgroup (multiple of 16, <= 128); NT = MFMA n-tiles
 // (16 features each) per wave = KC / 64 rounded up (template NTILE).
 // MFMA 16x16x16 f16 operand layout (lane l, j = 0..3):
 //   A: A[l % 16][4 * (l / 16) + j]      B: B[4 * (l / 16) + j][l % 16]
@@ -1071,6 +1071,11 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   // 4.59 -> 3.21, K=65 3.14 -> 2.42, K=81 3.20 -> 2.78, K=33 1.47 -> 1.35; grid+hubs K=66 1.99 ->
   // 2.07, K=33 1.41 -> 1.46.  K=97, an eighth fewer slots in seven passes: 3.25 -> 3.33)
   if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
+  // passes of at most 128 features for 16-byte loads: each pass gathers 256-byte slices of B
+  // rows, twice as many of which fit an XCD's L2 as whole 512-byte rows (R-MAT 2^20, K = 256:
+  // 1.730 ms in one pass of 32 lanes, 1.522 in two of 16, 1.837 in four of 8; K = 128 in two
+  // passes of 64 features: 0.748 -> 0.910)
+  if (p.feature_lanes <= 0 && VEC == 8 && lpg > 16) lpg = 16;
   // at least 4 lanes, whose column/value loads are shared, also where K < 4 leaves lanes idle
   // (same-box A/B: R-MAT K=1 0.316 -> 0.183 ms, K=2 0.255 -> 0.201; grid+hubs K=1 0.201 -> 0.122,
   // K=2 0.237 -> 0.175; 8 lanes at K=3: R-MAT 0.214 -> 0.258)
@@ -1137,14 +1142,15 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {
     const int kc16 = ((K + 15) / 16) * 16;
-    const int KC = kc16 < 256 ? kc16 : 256;
+    // at most 128 features per workgroup: wider B slices in flight per window cost L2 capacity
+    // (SBM 1M, K = 256: 0.912 ms with 256 features per workgroup, 0.871 with two of 128)
+    const int KC = kc16 < 128 ? kc16 : 128;
     dim3 grid(p.nmwin, (K + KC - 1) / KC);
     // staging space: 16 dense-tile B rows of KC features, or a quad's 64 rows of 64 (stride 72)
     const size_t stage = std::max<size_t>((size_t)16 * (KC + 8), p.nquads > 0 ? (size_t)64 * 72 : 0);
     const size_t shm = (size_t)16 * (KC + 4) * 4 + stage * 2;
     if (KC <= 64) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 1>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
-    else if (KC <= 128) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 2>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
-    else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 4>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
+    else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 2>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
   }
   if (ev) (void)hipEventRecord(ev[2], s);
   if (p.nfixups > 0 || p.nwfixups > 0) {
