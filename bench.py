@@ -217,7 +217,8 @@ def bench_sddmm(args, workload, g, K):
     torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of plan_s
     torch.cuda.synchronize()
     t1 = time.time()
-    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering)
+    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
+                                 feature_lanes=args.feature_lanes)
     st = plan.stats()
     pre = {"build_s": round(fmt.elapsed, 3), "plan_s": round(time.time() - t1, 3),
            "plan_lowering": "device" if st["device_lowered"] else "host"}

@@ -125,9 +125,11 @@ SDDMM_OPTIONS = [
 
 @pytest.mark.parametrize("oname,opts", SDDMM_OPTIONS, ids=[o[0] for o in SDDMM_OPTIONS])
 @pytest.mark.parametrize("name,gen", GRAPHS, ids=[g[0] for g in GRAPHS])
-@pytest.mark.parametrize("K", [64, 128])
+@pytest.mark.parametrize("K", [64, 128, 256])
 def test_device_lowering_equals_host_lowering_sddmm(name, gen, oname, opts, K):
-    """K = 128 takes the split part of the SDDMM launcher, K = 64 the unsplit task list."""
+    """K = 128 takes the split part of the SDDMM launcher, K = 64 the unsplit task list, K = 256
+    two 128-feature passes, the second adding to the outputs (tile and split-part output indices
+    included)."""
     say("device lowering sddmm", name, oname, K)
     g, f = graph(name, gen)
     S, Xh, Yh, s = compare_sddmm(f, g.m, g.n, K, opts, f"{name}/{oname}/K{K}")

@@ -66,8 +66,8 @@ def test_sddmm_long_rows_and_empty_rows():
 
 @pytest.mark.parametrize("K", [72, 128, 256])
 def test_staged_and_unstaged_sddmm_agree(K):
-    """16-lane groups (K = 65..128) stage each task's column ids in LDS (16-byte chunks from an
-    8-entry-aligned base); K = 256 never stages.  Tasks here start at every offset mod 8 and hold
+    """16-lane groups (K = 65..128, and each 128-feature pass of K = 256) stage each task's column
+    ids in LDS (16-byte chunks from an 8-entry-aligned base).  Tasks here start at every offset mod 8 and hold
     up to 256 entries (rows of 100-256 entries, split rows beyond): staged and unstaged
     (stage = -1) plans against the closed form, and bitwise equal to each other (same summation
     order)."""

@@ -780,10 +780,11 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // column ids are first staged in LDS (as in k_spmm_tasks), so batches do not re-read their cache
 // lines through L2.  SPF: the next batch's column ids are loaded under the current gathers.  NTO:
 // outputs are written with non-temporal stores, so they do not evict gathered Y rows from L2.
+// acc: add to the outputs instead of writing them (a later feature pass of the same entries).
 template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
-                                                     float* __restrict__ out) {
+                                                     float* __restrict__ out, int acc) {
   constexpr int GPW = 64 / LPG;
   constexpr int FPP = LPG * VEC;               // features per pass
   constexpr int UB = U < LPG ? U : LPG;        // entries per reduce_scatter batch
@@ -905,8 +906,9 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       if (li % (LPG / UB) == 0 && p + e < t.nz_end) {
         const int q = p + e;
         float* o = &out[P.res_pos ? P.res_pos[q - P.res_off] : q];
-        if constexpr (NTO) __builtin_nontemporal_store(sum, o);
-        else *o = sum;
+        const float v = acc ? sum + *o : sum;
+        if constexpr (NTO) __builtin_nontemporal_store(v, o);
+        else *o = v;
       }
     }
   }
@@ -1168,14 +1170,23 @@ template <int VEC>
 hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                             int K, float* out, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
-  {
-    int lpg = lanes_for(K, VEC);
+  // feature passes of at most 128 features for 16-byte loads, each over all entries, the later
+  // ones adding to the outputs: 256-byte slices of Y rows keep twice as many rows in an XCD's L2
+  // as whole 512-byte rows, for one extra read and write of each output per pass (R-MAT 2^20
+  // pattern, K = 256: 1.793 ms in one pass of 32 lanes, 1.742 in two of 16)
+  const int fpass = VEC == 8 && K > 128 && p.feature_lanes <= 0 ? 128 : K;
+  for (int f0 = 0; f0 < K; f0 += fpass) {
+    const int Kp = K - f0 < fpass ? K - f0 : fpass;
+    const uint16_t* Xp = X + f0;
+    const uint16_t* Yp = Y + f0;
+    const int acc = f0 > 0 ? 1 : 0;
+    int lpg = lanes_for(Kp, VEC);
     // fewer lanes than features: the kernel loops over feature chunks per batch (no second walk
     // of the entries), so narrow loads take the group width with the fewest lane slots (same-box
     // A/B on R-MAT: K=66 1.49 ms with 64 lanes -> 0.91 with 16, K=82 1.50 -> 0.99, K=130 2.00 ->
     // 1.72, K=33 1.40 -> 0.73, K=65 1.87 -> 1.20)
     while (p.feature_lanes > 0 && lpg > p.feature_lanes && lpg > 1) lpg >>= 1;
-    if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(K, VEC, lpg);
+    if (p.feature_lanes <= 0 && VEC <= 2) lpg = fewer_lane_slots(Kp, VEC, lpg);
     // at least 8 lanes, so that a group writes 8 consecutive sums (32 bytes) per store and the
     // outputs stream; lanes past K add zeros (R-MAT K=4 0.329 -> 0.258 ms, K=2 0.327 -> 0.259,
     // K=1 0.467 -> 0.260)
@@ -1193,7 +1204,8 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // 16-byte runs, as 4-lane groups write at K=16, lose: 0.418 -> 0.469)
     const bool ls = p.task_max <= kStageMax && p.stage >= 0;
     const bool nto = (p.streaming & 2) != 0;
-#define TRS_SD_LAUNCH(...) hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, X, ldx, Y, ldy, K, out)
+#define TRS_SD_LAUNCH(...) \
+  hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, Xp, ldx, Yp, ldy, Kp, out, acc)
 #define TRS_SD_U(L, U)                                                                                     \
     constexpr bool nt_ok = (U < L ? U : L) >= 8;                                                           \
     if constexpr (L == 16) {                                                                               \
