@@ -193,3 +193,22 @@ def test_format_read_back_lowers_on_host(tmp_path):
     Bh = graphs.dense_operand(g.n, 64, seed=23)
     assert np.array_equal(run_plan(trspmm.Plan.from_format(f2, g.m, g.n), Bh),
                           run_plan(trspmm.Plan.from_format(f, g.m, g.n), Bh))
+
+
+def test_device_lowering_empty_and_tiny_graphs():
+    """No entries at all, one row, one entry: the device path handles every empty case the host
+    path does (same statistics, same outputs)."""
+    cases = [
+        (np.zeros(17, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32), 16, 8),
+        (np.array([0, 1], np.int32), np.array([3], np.int32), np.array([2.5], np.float32), 1, 4),
+        (np.array([0, 0, 2, 2], np.int32), np.array([0, 5], np.int32), np.array([1.0, -1.0], np.float32), 3, 6),
+    ]
+    for rowptr, col, val, m, n in cases:
+        f = trspmm.build_format(rowptr, col, val)
+        Bh = graphs.dense_operand(n, 16, seed=24)
+        C, _ = compare(f, m, n, Bh, {}, f"m={m} nnz={len(col)}")
+        R = osp.csr_spmm(rowptr, col, val, Bh, m=m)
+        assert np.array_equal(np.isnan(C), np.zeros_like(C, bool))
+        e = osp.spmm_error(C, R)
+        assert e["elementwise_ok"], e
+        compare_sddmm(f, m, n, 16, {}, f"sddmm m={m} nnz={len(col)}")

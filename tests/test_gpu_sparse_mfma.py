@@ -114,3 +114,23 @@ def test_sparse_mfma_single_entry_groups():
         C = run_plan(plan, Bh)
         e = osp.spmm_error(C, R)
         assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, (sp, plan.stats(), e)
+
+
+@pytest.mark.parametrize("m", [2000, 2047])
+def test_sparse_mfma_rows_past_m(m):
+    """Windows that run past the last row (m not a multiple of 16): the tiles' rows >= m carry no
+    entries, and no output row past m is written."""
+    g = graphs.random_csr(m, 2048, 0.2, seed=9)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n, window_row_cap=1 << 30)
+    s = plan.stats()
+    assert s["sparse_tiles"] > 0, s
+    Bh = graphs.dense_operand(g.n, 128, seed=44)
+    B = torch.from_numpy(Bh).cuda()
+    out = torch.full((g.m + 16, 128), float("nan"), device="cuda")
+    plan.spmm(B, out=out[: g.m])
+    torch.cuda.synchronize()
+    C = out.cpu().numpy()
+    assert np.isnan(C[g.m:]).all()
+    e = osp.spmm_error(C[: g.m], osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m))
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e
