@@ -26,7 +26,10 @@
 #include <cstring>
 #include <numeric>
 #include <immintrin.h>
+#include <memory>
+#include <memory_resource>
 #include <omp.h>
+#include <optional>
 #include <vector>
 
 #include "format.hpp"
@@ -34,29 +37,42 @@
 
 namespace {
 
+// A window's output arrays live until the serialisation copies them into the format, so they are
+// allocated from a per-thread monotonic arena (released once, after the build) instead of the
+// general heap: freeing and re-allocating them window after window returned memory to the system
+// and faulted it back in, which doubled a first build in a fresh process (grid+hubs 0.76 s against
+// 0.35 s for a second one, R-MAT 0.45 s against 0.26 s on the GPU box host).
+template <class T>
+using wvec = std::pmr::vector<T>;
+
 struct Cuda {
-  std::vector<int32_t> cnt, row, atomic, col;
-  std::vector<float> val;
+  wvec<int32_t> cnt, row, atomic, col;
+  wvec<float> val;
+  explicit Cuda(std::pmr::memory_resource* r) : cnt(r), row(r), atomic(r), col(r), val(r) {}
 };
 
 struct Win {
   // TC
-  std::vector<int32_t> t_parts, t_subcnt, t_col, t_atomic;
-  std::vector<int64_t> t_bin;
-  std::vector<float> t_val;
+  wvec<int32_t> t_parts, t_subcnt, t_col, t_atomic;
+  wvec<int64_t> t_bin;
+  wvec<float> t_val;
   // CUDA residual, long and short parts
   Cuda lng, sht;
   // SPTC groups
-  std::vector<int32_t> s_col;
-  std::vector<uint8_t> s_mask;
-  std::vector<float> s_val;
-  std::vector<int8_t> s_pos;
+  wvec<int32_t> s_col;
+  wvec<uint8_t> s_mask;
+  wvec<float> s_val;
+  wvec<int8_t> s_pos;
   // tiles (tile_group holds the window-local first group)
-  std::vector<int32_t> tile_group, tile_cols, packed_a, packed_meta;
+  wvec<int32_t> tile_group, tile_cols, packed_a, packed_meta;
   // spill
-  std::vector<int32_t> sp_row, sp_col;
-  std::vector<float> sp_val;
+  wvec<int32_t> sp_row, sp_col;
+  wvec<float> sp_val;
   bool canonical = true;
+  explicit Win(std::pmr::memory_resource* r)
+      : t_parts(r), t_subcnt(r), t_col(r), t_atomic(r), t_bin(r), t_val(r), lng(r), sht(r), s_col(r), s_mask(r),
+        s_val(r), s_pos(r), tile_group(r), tile_cols(r), packed_a(r), packed_meta(r), sp_row(r), sp_col(r),
+        sp_val(r) {}
 };
 
 struct Params {
@@ -451,8 +467,8 @@ int env_int(const char* name, int dflt) {       // block_online.cpp:124-128
   return v ? std::atoi(v) : dflt;
 }
 
-template <class T, class A>
-void append_at(std::vector<T, A>& dst, size_t at, const std::vector<T>& src) {
+template <class T, class A, class B>
+void append_at(std::vector<T, A>& dst, size_t at, const std::vector<T, B>& src) {
   if (!src.empty()) std::memcpy(dst.data() + at, src.data(), src.size() * sizeof(T));
 }
 
@@ -546,13 +562,21 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
   }
 
   const int nwin = (rows + P.window - 1) / P.window;
-  std::vector<Win> wins(nwin);
   const int nthreads = prm->num_threads > 0 ? prm->num_threads : omp_get_max_threads();
+  // declared before the windows, so that windows still held on an early return are destroyed
+  // while their arenas exist
+  std::vector<std::unique_ptr<std::pmr::monotonic_buffer_resource>> arena(nthreads);
+  std::vector<std::optional<Win>> wins(nwin);
 #pragma omp parallel num_threads(nthreads)
   {
     Scratch S;
+    auto& a = arena[omp_get_thread_num()];
+    a = std::make_unique<std::pmr::monotonic_buffer_resource>(size_t(4) << 20);
 #pragma omp for schedule(dynamic, 16)
-    for (int w = 0; w < nwin; ++w) build_window(rowptr, col, val, rows, w, P, S, wins[w]);
+    for (int w = 0; w < nwin; ++w) {
+      wins[w].emplace(a.get());
+      build_window(rowptr, col, val, rows, w, P, S, *wins[w]);
+    }
   }
 
   // ---- serialisation in window order (block_online.cpp:736-776, 789-794, 840, 844-870) ----
@@ -564,7 +588,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
   off[0] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   bool canonical = true;
   for (int w = 0; w < nwin; ++w) {
-    const Win& W = wins[w];
+    const Win& W = *wins[w];
     Off o = off[w];
     o.parts += W.t_parts.size();
     o.subs += W.t_subcnt.size();
@@ -608,7 +632,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
   }
 #pragma omp parallel for schedule(dynamic, 64) num_threads(nthreads)
   for (int w = 0; w < nwin; ++w) {
-    Win& W = wins[w];
+    const Win& W = *wins[w];
     const Off& o = off[w];
     // TC
     int32_t acc = (int32_t)o.subs;
@@ -650,7 +674,7 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
     append_at(F->packed_meta, o.tiles * 8, W.packed_meta);
     append_at(F->spill_row, o.sp, W.sp_row); append_at(F->spill_col, o.sp, W.sp_col);
     append_at(F->spill_val, o.sp, W.sp_val);
-    W = Win();   // release per-window memory early
+    wins[w].reset();
   }
   // keep the input CSR for device-side plan lowering (counted in the build time)
   if (canonical) {
