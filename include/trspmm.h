@@ -209,7 +209,10 @@ void trs_plan_options_default(trs_plan_options* o);
 
 /* Full-accuracy plan from the builder output: TC + 2:4 groups + residual + spill == input.
  * Replaces the device half of Libra6SpMMOnline.forward_fp16_tcu_cuda_sptc_mma_parallel_online
- * (TR-source/SpMM/mGCN_online.cpp:760-1138) for callers that keep the trs_format. */
+ * (TR-source/SpMM/mGCN_online.cpp:760-1138) for callers that keep the trs_format.  A format built
+ * in this process from canonical input keeps its input CSR, and then the residual is built on the
+ * device (opt->host_lowering; the plan is the same either way).  Synchronous: returns when the
+ * plan is on the device. */
 int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt,
                     trs_plan** out);
 
@@ -264,7 +267,8 @@ int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_p
 /* SDDMM plan over the builder output, on the SpMM tiling: dense 16x16 tiles (TC blocks, 2:4 group
  * tiles with fill >= sptc_min_fill) run as MFMA dot products sampled at the stored entries, the
  * rest as wave64 CSR dot products.  Outputs follow the input's CSR order (the format must come
- * from canonical CSR).  No reference counterpart (the reference has no SDDMM). */
+ * from canonical CSR).  Lowered on the device like trs_plan_create's plans.  No reference
+ * counterpart (the reference has no SDDMM). */
 int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt,
                           trs_plan** out);
 
