@@ -157,6 +157,29 @@ struct Lowering {
 
 float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// The private results of parallel lowering pieces, appended in piece order (sized once: a tile is
+// over 1 KB).  stop_at_error: stop at the first failed piece (nothing after it is needed).
+void append_parts(Lowering& L, std::vector<Lowering>& part, bool stop_at_error) {
+  size_t nr = L.row.size(), nt = L.tiles.size();
+  for (const auto& q : part) {
+    nr += q.row.size();
+    nt += q.tiles.size();
+  }
+  L.row.reserve(nr);
+  L.col.reserve(nr);
+  L.val.reserve(nr);
+  L.tiles.reserve(nt);
+  for (auto& q : part) {
+    if (!q.st.ok() && L.st.ok()) L.st = q.st;
+    if (!q.st.ok() && stop_at_error) return;
+    L.row.insert(L.row.end(), q.row.begin(), q.row.end());
+    L.col.insert(L.col.end(), q.col.begin(), q.col.end());
+    L.val.insert(L.val.end(), q.val.begin(), q.val.end());
+    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
+    std::vector<Lowering::Tile>().swap(q.tiles);
+  }
+}
+
 // TC sub-blocks of parts [p_begin, p_end) -> MFMA tiles (pairs of sub-blocks of one part, 16
 // columns) or entries.
 void lower_tc_range(Lowering& L, const int32_t* t_rowoff, int64_t p_begin, int64_t p_end, const int32_t* t_blockoff,
@@ -226,16 +249,7 @@ void lower_tc(Lowering& L, const int32_t* t_rowoff, int64_t nparts, const int32_
   parallel_parts(T, nparts, 0, [&](int t) { return nparts * t / T; }, [&](int64_t pb, int64_t pe, int t) {
     lower_tc_range(part[t], t_rowoff, pb, pe, t_blockoff, t_col, vals_f32, vals_f16, nvals, t_winrow, t_bin, to_mfma);
   });
-  for (auto& q : part) {
-    if (!q.st.ok()) {
-      if (L.st.ok()) L.st = q.st;
-      return;
-    }
-    L.row.insert(L.row.end(), q.row.begin(), q.row.end());
-    L.col.insert(L.col.end(), q.col.begin(), q.col.end());
-    L.val.insert(L.val.end(), q.val.begin(), q.val.end());
-    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
-  }
+  append_parts(L, part, true);
 }
 
 void lower_residual(Lowering& L, const int32_t* off, const int32_t* rows, int64_t nparts, const int32_t* cols,
@@ -284,13 +298,7 @@ void lower_groups(Lowering& L, const int32_t* s_col, const float* s_val, const i
   parallel_parts(T, nwin, 0, [&](int t) { return wcut[t]; }, [&](int64_t wb, int64_t we, int t) {
     lower_groups_range(part[t], s_col, s_val, s_pos, groups, s_win, s_off, wb, we, window, to_mfma, min_fill);
   });
-  for (auto& q : part) {
-    if (!q.st.ok() && L.st.ok()) L.st = q.st;
-    L.row.insert(L.row.end(), q.row.begin(), q.row.end());
-    L.col.insert(L.col.end(), q.col.begin(), q.col.end());
-    L.val.insert(L.val.end(), q.val.begin(), q.val.end());
-    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
-  }
+  append_parts(L, part, false);
 }
 
 void lower_groups_range(Lowering& L, const int32_t* s_col, const float* s_val, const int8_t* s_pos, int64_t groups,
