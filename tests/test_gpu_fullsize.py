@@ -109,3 +109,31 @@ def test_fullsize_sddmm_sampled(K):
     Ysum = pattern @ Yh.astype(np.float64)
     total = float(np.sum(Xh.astype(np.float64) * Ysum))
     assert abs(float(got.astype(np.float64).sum()) - total) <= 1e-7 * g.nnz * np.sqrt(K)
+
+
+@pytest.mark.parametrize("name,K", [("rmat20", 128), ("sbm1m", 256)])
+def test_fullsize_device_lowering_equals_host_lowering(name, K):
+    """BASELINE configs 2 and 3 at full size: the plan whose residual is built on the device and
+    the host-lowered plan have the same statistics and give bitwise equal SpMM and SDDMM outputs
+    (compared on the device)."""
+    print("fullsize lowering", name, K, flush=True)
+    g, f = graph(name)
+    dev = trspmm.Plan.from_format(f, g.m, g.n)
+    host = trspmm.Plan.from_format(f, g.m, g.n, host_lowering=True)
+    sd, sh = dev.stats(), host.stats()
+    assert sd.pop("device_lowered") == 1 and sh.pop("device_lowered") == 0
+    assert sd == sh, (sd, sh)
+    B = torch.from_numpy(graphs.dense_operand(g.n, K, seed=2)).cuda()
+    Cd = dev.spmm(B)
+    Ch = host.spmm(B)
+    torch.cuda.synchronize()
+    assert torch.equal(Cd, Ch)
+    del Cd, Ch, dev, host
+    sdev = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    shost = trspmm.Plan.for_sddmm(f, g.m, g.n, host_lowering=True)
+    sd, sh = sdev.stats(), shost.stats()
+    assert sd.pop("device_lowered") == 1 and sh.pop("device_lowered") == 0
+    assert sd == sh, (sd, sh)
+    X = torch.from_numpy(graphs.dense_operand(g.m, 128, seed=4)).cuda()
+    Y = torch.from_numpy(graphs.dense_operand(g.n, 128, seed=5)).cuda()
+    assert torch.equal(sdev.sddmm(X, Y), shost.sddmm(X, Y))
