@@ -377,3 +377,19 @@ def test_xcd_column_split_matches_oracle_and_unsplit_rows(K):
     deg = np.diff(g.rowptr[: g.m + 1])
     keep = deg < 48
     assert keep.sum() > g.m // 2 and np.array_equal(C1[keep], C2[keep])
+
+
+@pytest.mark.parametrize("K", [200, 256, 520])
+def test_feature_passes_with_split_rows(K):
+    """K > 128 runs the residual kernel in passes of 128 features (16-lane groups): every pass
+    writes its features of the main rows and of the split rows' partial slots, and the fixup sums
+    each pass's slots.  Against the oracle on an R-MAT graph with many XCD-split rows."""
+    say("feature passes", K)
+    g = graphs.rmat(scale=14, edge_factor=16, seed=12)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n, xcd_split=48)
+    assert plan.stats()["split_rows"] > 100
+    Bh = dense_B(g.n, K, seed=13)
+    C = run_plan(plan, Bh)
+    check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"passes K={K}")
+    assert np.array_equal(C, run_plan(plan, Bh))
