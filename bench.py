@@ -218,7 +218,7 @@ def bench_sddmm(args, workload, g, K):
     torch.cuda.synchronize()
     t1 = time.time()
     plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                 feature_lanes=args.feature_lanes)
+                                 feature_lanes=args.feature_lanes, hot_rows=args.hot_rows)
     st = plan.stats()
     pre = {"build_s": round(fmt.elapsed, 3), "plan_s": round(time.time() - t1, 3),
            "plan_lowering": "device" if st["device_lowered"] else "host"}
@@ -229,15 +229,17 @@ def bench_sddmm(args, workload, g, K):
     X = torch.from_numpy(Xh).cuda()
     Y = torch.from_numpy(Yh).cuda()
     out = torch.empty(st["nnz"], dtype=torch.float32, device="cuda")
+    need = plan.sddmm_workspace_bytes(K)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     calibration_copy(args.calibrate_copy_mib)
     for _ in range(args.warmup):
-        plan.sddmm(X, Y, out=out)
+        plan.sddmm(X, Y, out=out, workspace=ws)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
-        plan.sddmm(X, Y, out=out)
+        plan.sddmm(X, Y, out=out, workspace=ws)
     e1.record()
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
@@ -245,10 +247,11 @@ def bench_sddmm(args, workload, g, K):
     gflops = flops / (ms_step * 1e-3) / 1e9
     ms = (ctypes.c_float * 2)()
     nat.check(nat.lib().trs_sddmm_f16_kernel_ms(plan.handle, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), K,
-                                                out.data_ptr(), int(torch.cuda.current_stream().cuda_stream), 10, ms),
+                                                out.data_ptr(), ws.data_ptr(), need,
+                                                int(torch.cuda.current_stream().cuda_stream), 10, ms),
               "trs_sddmm_f16_kernel_ms")
     kms = list(ms)
-    ms_cold = cold_ms(lambda: plan.sddmm(X, Y, out=out), max(5, min(args.steps, 10)))
+    ms_cold = cold_ms(lambda: plan.sddmm(X, Y, out=out, workspace=ws), max(5, min(args.steps, 10)))
     names = ["sddmm_tasks", "sddmm_mfma"]
     dom = int(np.argmax(kms))
     M, N = g.m, g.n
@@ -258,6 +261,7 @@ def bench_sddmm(args, workload, g, K):
         nr = st["csr_nnz"]
         bytes_k = 8 * nr + 4 * (M + 1) + 2 * M * K + 2 * N * K
         impl = (4 * nr if st["mfma_tiles"] else 0) + 16 * st["tasks"]   # output index, task descriptors
+        impl += 4 * K * st["hot_rows"] if need else 0                   # staged hot rows: read + write
     else:
         bytes_k = 8 * st["mfma_nnz"] + 2 * M * K + 2 * N * K
         impl = st["mfma_tiles"] * (64 + 1024) - 4 * st["mfma_nnz"]      # column ids, dense output slots
@@ -330,6 +334,9 @@ def main():
     ap.add_argument("--xcd-split", type=int, default=None,
                     help="plan option xcd_split (rows of >= N residual entries cut by XCD column ranges; "
                          "-1 off; default: the library's)")
+    ap.add_argument("--hot-rows", type=int, default=None,
+                    help="plan option hot_rows (B / Y rows of the most gathered columns staged per call; -1 off; "
+                         "default: the library's)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -370,7 +377,8 @@ def main():
     torch.cuda.synchronize()
     t1 = time.time()
     plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                   window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes)
+                                   window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes,
+                                   hot_rows=args.hot_rows)
     pre["plan_s"] = round(time.time() - t1, 3)
     pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
     if "reorder_s" in pre:
@@ -414,6 +422,7 @@ def main():
         rows_k = M - rows_w
         bytes_k = 6 * nnz_k + 4 * (rows_k + 1) + 2 * N * K + 4 * rows_k * K
         impl = 16 * st["tasks"] + 4 * K * st["partial_slots"]          # task descriptors, partial slots
+        impl += 4 * K * st["hot_rows"] if K >= 128 and K % 8 == 0 else 0  # staged hot rows: read + write
     elif dom == 1:  # MFMA windows: tile entries + the windows' residual entries, their rows
         bytes_k = 6 * (st["mfma_nnz"] + nnz_w) + 4 * (rows_w + 1) + 2 * N * K + 4 * rows_w * K
         impl = st["mfma_tiles"] * (512 + 64) - 6 * st["mfma_nnz"]      # dense 16x16 tiles + column ids

@@ -203,6 +203,13 @@ typedef struct trs_plan_options {
                              2-bit column indices, as the reference runs its packed 2:4 tiles on
                              mma.sp (mGCNkernel_online.cu:812-933) (default); 0 = every tile on
                              the dense v_mfma_f32_16x16x16_f16 with zero fill */
+  int32_t hot_rows;       /* staged hot rows: the B (Y) rows of the columns the residual task
+                             kernels gather most are copied into a dense buffer at the start of a
+                             call (workspace), and the task kernels read them there; the plan keeps
+                             a second copy of its column ids with those columns renumbered.  Used
+                             for K >= 128 (K % 8 == 0) on 16-byte aligned operands.  0 = automatic
+                             (16384 rows, at most n / 16, and only when they take >= 30% of the
+                             gathers), > 0 = that many rows, -1 = off */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);
@@ -287,6 +294,8 @@ typedef struct trs_plan_stats {
   int64_t window_csr_nnz;            /* residual nonzeros inside those windows */
   int64_t device_lowered;            /* 1: the residual was built on the device (host_lowering) */
   int64_t sparse_tiles;              /* of mfma_tiles, those run on the sparse MFMA (sptc_sparse) */
+  int64_t hot_rows;                  /* staged hot rows (option hot_rows; 0 = none) */
+  int64_t hot_entries;               /* entries whose B (Y) rows are staged */
 } trs_plan_stats;
 
 int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s);
@@ -295,7 +304,8 @@ void trs_plan_free(trs_plan* p);
 /* ---------------------------------------------------------------------------------------------
  * Execution.
  * ------------------------------------------------------------------------------------------- */
-/* Bytes of device workspace trs_spmm_f16 needs for feature width K (0 when none). */
+/* Bytes of device workspace trs_spmm_f16 needs for feature width K (0 when none): the partial
+ * slots of split rows and, for K >= 128, the plan's staged hot B rows (option hot_rows). */
 int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K);
 
 /* C[m, K] (float32, row stride ldc) = A_plan (m x n) * B[n, K] (fp16, row stride ldb).
@@ -322,6 +332,18 @@ int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_t ldb, int3
 int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                   int32_t K, float* out, void* stream);
 
+/* Bytes of device workspace trs_sddmm_f16_ws uses at feature width K: the plan's staged hot Y rows
+ * (plan option hot_rows; 0 when the plan or K stages none).  No reference counterpart. */
+int64_t trs_sddmm_workspace_bytes(const trs_plan* p, int32_t K);
+
+/* trs_sddmm_f16 with a workspace of trs_sddmm_workspace_bytes(p, K) bytes (fewer: TRS_EINVAL),
+ * into which the call copies the plan's hot Y rows before the dot products gather them there.  The
+ * same outputs, bitwise (only where a row is read from changes); trs_sddmm_f16 runs unstaged.  A
+ * workspace is the call's own: calls that overlap need separate workspaces.  No reference
+ * counterpart. */
+int trs_sddmm_f16_ws(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
+                     int32_t K, float* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Launch-by-launch timing helper for the reference operators' `epoches` semantics
  * (mGCNkernel_online.cu:1604-1712): `warmup` untimed calls, then `iters` timed calls bracketed by
  * HIP events on `stream`; *ms_avg = mean time per call.  C holds the result of the last call. */
@@ -338,10 +360,12 @@ int trs_spmm_f16_kernel_ms(const trs_plan* p, const uint16_t* B, int64_t ldb, in
                            int64_t ldc, void* workspace, int64_t workspace_bytes, void* stream,
                            int32_t iters, float* ms);
 
-/* SDDMM counterpart of trs_spmm_f16_kernel_ms: ms[0] = CSR dot-product kernel, ms[1] = MFMA tile
+/* SDDMM counterpart of trs_spmm_f16_kernel_ms (calls as trs_sddmm_f16_ws; workspace may be NULL
+ * for unstaged calls): ms[0] = CSR dot-product kernel (with the hot-row copy), ms[1] = MFMA tile
  * kernel (averages over `iters` calls).  No reference counterpart. */
 int trs_sddmm_f16_kernel_ms(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y,
-                            int64_t ldy, int32_t K, float* out, void* stream, int32_t iters, float* ms);
+                            int64_t ldy, int32_t K, float* out, void* workspace, int64_t workspace_bytes,
+                            void* stream, int32_t iters, float* ms);
 
 const char* trs_last_error(void);
 

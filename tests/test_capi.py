@@ -30,8 +30,8 @@ def test_every_declared_symbol_is_exported():
 
 def test_struct_layouts_match_header():
     assert ctypes.sizeof(nat.BuildParams) == 12 * 4
-    assert ctypes.sizeof(nat.PlanOptions) == 15 * 4
-    assert ctypes.sizeof(nat.PlanStats) == 14 * 8
+    assert ctypes.sizeof(nat.PlanOptions) == 16 * 4
+    assert ctypes.sizeof(nat.PlanStats) == 16 * 8
     assert ctypes.sizeof(nat.ReorderParams) == 40
     assert ctypes.sizeof(nat.MatchStats) == 16 * 8
 

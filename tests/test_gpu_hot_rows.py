@@ -1,0 +1,186 @@
+"""GPU: staged hot rows (plan option hot_rows).
+
+A plan with a hot set keeps a second copy of its column ids in which every entry of the most
+gathered columns is renumbered ~rank; at K >= 128 a call copies those B (Y) rows into a dense
+buffer in the workspace and the task kernels gather them there.  Only where a row is read from
+changes, so the outputs are bitwise equal to the unstaged plan's (same products, same order), and
+both match the float64 oracle.  Covered: the automatic choice (R-MAT stages, a block graph does
+not), widths that stage (128, 136, 256, 200) and ones that do not (64, 120), the split part (XCD
+sub-rows) and MFMA windows beside staged rows, workspace sizes, a workspace too small, the
+entry point without workspace (trs_sddmm_f16) and the one that allocates nothing.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import spmm as osp
+from trspmm import _native as nat
+from trspmm import graphs
+import trspmm
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    torch.cuda.init()
+
+
+_cache = {}
+
+
+def rmat():
+    if "rmat" not in _cache:
+        g = graphs.rmat(scale=16, edge_factor=16, seed=21)
+        _cache["rmat"] = (g, trspmm.build_format(g.rowptr, g.col, g.val))
+    return _cache["rmat"]
+
+
+def run_spmm(plan, Bh, ws_pad=0):
+    B = torch.from_numpy(Bh).cuda()
+    K = Bh.shape[1]
+    out = torch.full((plan.stats()["m"], K), float("nan"), device="cuda")
+    need = plan.workspace_bytes(K)
+    ws = torch.empty(need + ws_pad, dtype=torch.uint8, device="cuda")
+    plan.spmm(B, out=out, workspace=ws[ws_pad:] if ws_pad else ws)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_automatic_choice():
+    g, f = rmat()
+    p = trspmm.Plan.from_format(f, g.m, g.n)
+    s = p.stats()
+    say("rmat16", s)
+    # n / 16 rows at most; they carry >= 30% of the gathers
+    assert 0 < s["hot_rows"] <= g.n // 16 and s["hot_entries"] * 10 >= 3 * s["csr_nnz"], s
+    off = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1).stats()
+    assert off["hot_rows"] == 0 and off["hot_entries"] == 0
+    assert s["device_bytes"] > off["device_bytes"]
+    # a block graph has no hot columns
+    b = graphs.sbm(communities=4096, seed=3, val_seed=3)
+    fb = trspmm.build_format(b.rowptr, b.col, b.val)
+    assert trspmm.Plan.from_format(fb, b.m, b.n).stats()["hot_rows"] == 0
+
+
+@pytest.mark.parametrize("K", [128, 136, 256, 200, 64, 120])
+def test_spmm_staged_equals_unstaged(K):
+    g, f = rmat()
+    hot = trspmm.Plan.from_format(f, g.m, g.n)
+    plain = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1)
+    assert hot.stats()["split_rows"] > 0   # the split part reads staged rows too
+    H = hot.stats()["hot_rows"]
+    partial = plain.workspace_bytes(K)
+    staged = K >= 128 and K % 8 == 0
+    want = ((partial + 255) // 256) * 256 + H * K * 2 if staged else partial
+    assert hot.workspace_bytes(K) == want, (K, hot.workspace_bytes(K), want)
+    Bh = graphs.dense_operand(g.n, K, seed=K)
+    say("hot spmm K", K, "rows", H, "workspace", hot.workspace_bytes(K))
+    C = run_spmm(hot, Bh)
+    assert np.array_equal(C, run_spmm(plain, Bh))
+    e = osp.spmm_error(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m))
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e
+    # a workspace that is not 16-byte aligned runs unstaged with narrower loads: same sums
+    C8 = run_spmm(hot, Bh, ws_pad=8)
+    assert np.max(np.abs(C8 - C)) <= 1e-5 * max(1.0, float(np.max(np.abs(C))))
+
+
+@pytest.mark.parametrize("H", [1, 100, 5000])
+def test_spmm_explicit_hot_rows_with_windows(H):
+    """An explicit row count stages whatever the share; a graph with MFMA windows keeps their B
+    reads on the plain column ids."""
+    g = graphs.sbm(communities=4096, seed=5, val_seed=5)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    p = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=H)
+    s = p.stats()
+    assert s["hot_rows"] == H and s["mfma_windows"] > 0, s
+    Bh = graphs.dense_operand(g.n, 128, seed=7)
+    C = run_spmm(p, Bh)
+    assert np.array_equal(C, run_spmm(trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1), Bh))
+    e = osp.spmm_error(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m))
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e
+
+
+def test_spmm_workspace_too_small_is_refused():
+    g, f = rmat()
+    p = trspmm.Plan.from_format(f, g.m, g.n)
+    K = 128
+    B = torch.from_numpy(graphs.dense_operand(g.n, K, seed=1)).cuda()
+    C = torch.empty((g.m, K), dtype=torch.float32, device="cuda")
+    need = p.workspace_bytes(K)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    rc = nat.lib().trs_spmm_f16(p.handle, B.data_ptr(), K, K, C.data_ptr(), K, ws.data_ptr(), need - 1,
+                                int(torch.cuda.current_stream().cuda_stream))
+    assert rc == 1 and b"workspace" in nat.lib().trs_last_error()
+
+
+def test_noalloc_with_staged_rows():
+    """trs_spmm_f16_noalloc takes the hot buffer from its static array too: equal to the call with
+    a workspace, twice in a row (the second at a smaller width)."""
+    g, f = rmat()
+    p = trspmm.Plan.from_format(f, g.m, g.n)
+    for K in (256, 128):
+        assert p.workspace_bytes(K) <= 128 << 20
+        Bh = graphs.dense_operand(g.n, K, seed=3 + K)
+        B = torch.from_numpy(Bh).cuda()
+        C = torch.full((g.m, K), float("nan"), dtype=torch.float32, device="cuda")
+        nat.check(nat.lib().trs_spmm_f16_noalloc(p.handle, B.data_ptr(), K, K, C.data_ptr(), K,
+                                                 int(torch.cuda.current_stream().cuda_stream)),
+                  "trs_spmm_f16_noalloc")
+        torch.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy(), run_spmm(p, Bh))
+
+
+@pytest.mark.parametrize("K", [128, 256, 200, 64])
+def test_sddmm_staged_equals_unstaged(K):
+    g, f = rmat()
+    hot = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    plain = trspmm.Plan.for_sddmm(f, g.m, g.n, hot_rows=-1)
+    H = hot.stats()["hot_rows"]
+    assert H > 0 and plain.stats()["hot_rows"] == 0
+    assert hot.sddmm_workspace_bytes(K) == (H * K * 2 if K >= 128 and K % 8 == 0 else 0)
+    assert plain.sddmm_workspace_bytes(K) == 0
+    Xh = graphs.dense_operand(g.m, K, seed=30 + K)
+    Yh = graphs.dense_operand(g.n, K, seed=31 + K)
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    say("hot sddmm K", K, "rows", H)
+    S = hot.sddmm(X, Y).cpu().numpy()
+    assert np.array_equal(S, plain.sddmm(X, Y).cpu().numpy())
+    # the entry point without a workspace runs unstaged
+    out = torch.full((hot.stats()["nnz"],), float("nan"), device="cuda")
+    nat.check(nat.lib().trs_sddmm_f16(hot.handle, X.data_ptr(), K, Y.data_ptr(), K, K, out.data_ptr(),
+                                      int(torch.cuda.current_stream().cuda_stream)), "trs_sddmm_f16")
+    torch.cuda.synchronize()
+    assert np.array_equal(S, out.cpu().numpy())
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, float(np.max(np.abs(R))))
+    assert np.max(np.abs(S - R)) <= tol
+
+
+def test_sddmm_workspace_too_small_is_refused():
+    g, f = rmat()
+    p = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    K = 128
+    need = p.sddmm_workspace_bytes(K)
+    X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=1)).cuda()
+    Y = torch.from_numpy(graphs.dense_operand(g.n, K, seed=2)).cuda()
+    out = torch.empty(p.stats()["nnz"], dtype=torch.float32, device="cuda")
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    rc = nat.lib().trs_sddmm_f16_ws(p.handle, X.data_ptr(), K, Y.data_ptr(), K, K, out.data_ptr(), ws.data_ptr(),
+                                    need - 2, int(torch.cuda.current_stream().cuda_stream))
+    assert rc == 1 and b"workspace" in nat.lib().trs_last_error()
+
+
+def test_device_and_host_lowering_choose_the_same_rows():
+    g, f = rmat()
+    d = trspmm.Plan.from_format(f, g.m, g.n).stats()
+    h = trspmm.Plan.from_format(f, g.m, g.n, host_lowering=True).stats()
+    assert d["device_lowered"] == 1 and h["device_lowered"] == 0
+    assert (d["hot_rows"], d["hot_entries"]) == (h["hot_rows"], h["hot_entries"])

@@ -132,6 +132,20 @@ __device__ __forceinline__ uint64_t row_offset(int32_t row, int64_t ld) {
   return (uint64_t)(uint32_t)row * (uint64_t)(uint32_t)ld;
 }
 
+// Fragment address of entry column c: row c of B at Bf (leading dimension ld) or, with HOT and
+// c < 0, staged hot row ~c at Hf (leading dimension hld).  Selects, no branch: the gathers of a
+// batch still issue back to back.
+template <bool HOT>
+__device__ __forceinline__ const uint16_t* gather_addr(const uint16_t* Bf, int64_t ld, const uint16_t* Hf,
+                                                       int32_t hld, int32_t c) {
+  if constexpr (HOT) {
+    const bool h = c < 0;
+    return (h ? Hf : Bf) + row_offset(h ? ~c : c, h ? (int64_t)hld : ld);
+  } else {
+    return Bf + row_offset(c, ld);
+  }
+}
+
 template <bool NT, class T>
 __device__ __forceinline__ T load_stream(const T* p) {
   if constexpr (NT) return __builtin_nontemporal_load(p);
@@ -282,6 +296,12 @@ struct Batch {
 #pragma unroll
     for (int i = 0; i < U; ++i) bb[i].load(Bf + row_offset(cc[i], ldb));
   }
+  // the same with staged hot rows (negative ids) at Hf
+  __device__ __forceinline__ void gather_hot(const uint16_t* __restrict__ Bf, int64_t ldb,
+                                             const uint16_t* __restrict__ Hf, int32_t hld) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) bb[i].load(gather_addr<true>(Bf, ldb, Hf, hld, cc[i]));
+  }
   // after gather(): fetch the next batch's column ids and values into n
   __device__ __forceinline__ void prefetch_next(Batch& n, const int32_t* __restrict__ col,
                                                 const uint16_t* __restrict__ val, int p, int end) const {
@@ -406,7 +426,9 @@ constexpr size_t tasks_static_lds(int lpg, bool ls) {
 
 // PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
 // together with the row pointers, before the barrier.  LS: staged stream (see stage_stream).
-template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
+// HOT: P.col is the hot-renumbered copy and negative ids gather from the staged rows P.hot_b
+// (staged streams only).
+template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
                                                     int K, float* __restrict__ C, int64_t ldc,
                                                     float* __restrict__ partial) {
@@ -419,6 +441,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
   __shared__ __align__(16) uint16_t s_val[LS ? 4 * GPW * kStageSpan : 8];
   static_assert(!(LS && PF), "a staged stream is not pipelined");
+  static_assert(!HOT || LS, "staged hot rows are read by the staged-stream kernel");
   static_assert(sizeof(s_rp) + sizeof(s_col) + sizeof(s_val) == tasks_static_lds(LPG, LS),
                 "tasks_static_lds must describe this kernel's LDS (the occupancy cap depends on it)");
   const int wave = threadIdx.x >> 6;
@@ -448,13 +471,15 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const int f = blockIdx.y * (LPG * VEC) + li * VEC;
   const bool active = f < K;
   const uint16_t* __restrict__ Bf = B + (active ? f : 0);
+  const uint16_t* __restrict__ Hf = HOT ? P.hot_b + (active ? f : 0) : nullptr;
   float acc[VEC];
   zero_acc(acc);
   // one batch: column ids and values (from LDS when staged) and its B gathers
   auto begin_batch = [&](int p, int end) {
     if constexpr (LS) {
       b.load_lds(sc, sv, sbase, p, end);
-      b.gather(Bf, ldb);
+      if constexpr (HOT) b.gather_hot(Bf, ldb, Hf, P.hot_ld);
+      else b.gather(Bf, ldb);
     } else {
       b.template step_begin<PF>(n, col, val, Bf, ldb, p, end);
     }
@@ -781,7 +806,9 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // lines through L2.  SPF: the next batch's column ids are loaded under the current gathers.  NTO:
 // outputs are written with non-temporal stores, so they do not evict gathered Y rows from L2.
 // acc: add to the outputs instead of writing them (a later feature pass of the same entries).
-template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false>
+// HOT: P.col is the hot-renumbered copy and negative ids gather Y rows from the staged rows
+// P.hot_b.
+template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false, bool HOT = false>
 __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
                                                      const uint16_t* __restrict__ Y, int64_t ldy, int K,
                                                      float* __restrict__ out, int acc) {
@@ -873,8 +900,9 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       // distinct row of the chunk; the fragment each entry uses is selected in registers
       BFrag<VEC> x[U], y[U];
       const uint16_t* __restrict__ Yf = Y + (f < K ? f : 0);
+      const uint16_t* __restrict__ Hf = HOT ? P.hot_b + (f < K ? f : 0) : nullptr;
 #pragma unroll
-      for (int i = 0; i < U; ++i) y[i].load(Yf + row_offset(cc[i], ldy));
+      for (int i = 0; i < U; ++i) y[i].load(gather_addr<HOT>(Yf, ldy, Hf, P.hot_ld, cc[i]));
       if constexpr (PFC) {
         if (f0 == 0 && p + U < t.nz_end) load_cols(p + U, cn);
       }
@@ -1034,11 +1062,37 @@ DevicePlan split_view(const DevicePlan& p) {
   return v;
 }
 
-template <int VEC, int LPG, int U, int NT, bool PF, bool LS>
+template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
 void launch_tasks(dim3 grid, int waves, hipStream_t s, const DevicePlan& p, const uint16_t* B, int64_t ldb, int K,
                   float* C, int64_t ldc, float* partial) {
-  hipLaunchKernelGGL((k_spmm_tasks<VEC, LPG, U, NT, PF, LS>), grid, dim3(256),
+  hipLaunchKernelGGL((k_spmm_tasks<VEC, LPG, U, NT, PF, LS, HOT>), grid, dim3(256),
                      occupancy_pad(tasks_static_lds(LPG, LS), waves), s, p, B, ldb, K, C, ldc, partial);
+}
+
+// Staged hot rows: dst[r][0, K) = B[rows[r]][0, K) for r < nhot, 16 bytes per thread (K % 8 == 0,
+// 16-byte aligned rows).
+__global__ __launch_bounds__(256) void k_stage_hot_rows(const uint16_t* __restrict__ B, int64_t ldb, int K,
+                                                        const int32_t* __restrict__ rows, int32_t nhot,
+                                                        uint16_t* __restrict__ dst) {
+  const int chunks = K >> 3;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)nhot * chunks) return;
+  const int r = (int)(t / chunks), c = (int)(t - (int64_t)r * chunks);
+  const int4_t v = *reinterpret_cast<const int4_t*>(B + row_offset(rows[r], ldb) + c * 8);
+  *reinterpret_cast<int4_t*>(dst + (int64_t)r * K + c * 8) = v;
+}
+
+// Copies the plan's hot rows of B (K features) into hot and returns the view whose task kernels
+// read the renumbered columns and the staged rows.
+DevicePlan hot_view(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, uint16_t* hot, hipStream_t s) {
+  const int64_t threads = (int64_t)p.nhot * (K >> 3);
+  hipLaunchKernelGGL(k_stage_hot_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, B, ldb, K,
+                     p.hot_rows, p.nhot, hot);
+  DevicePlan v = p;
+  v.col = p.hot_col;
+  v.hot_b = hot;
+  v.hot_ld = K;
+  return v;
 }
 
 int lanes_for(int K, int vec) {
@@ -1063,7 +1117,7 @@ int fewer_lane_slots(int K, int vec, int lpg) {
 
 template <int VEC>
 hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
-                           float* partial, hipStream_t s, hipEvent_t* ev) {
+                           float* partial, uint16_t* hot, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
   int lpg = lanes_for(K, VEC);
   // a plan may ask for fewer lanes per group: several feature passes, each gathering a narrower
@@ -1084,6 +1138,12 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
   if (p.feature_lanes <= 0 && lpg < 4) lpg = 4;
   const int fpp = lpg * VEC;
   const int passes = (K + fpp - 1) / fpp;
+  // staged hot rows for the staged-stream kernel of 16-lane groups (256-byte gathers); the window
+  // kernel keeps reading B through the plain column ids
+  const bool hot_on = VEC == 8 && lpg == 16 && hot != nullptr && hot_buffer_bytes(p, K) > 0 &&
+                      p.task_max <= kStageMax && p.stage >= 0 &&
+                      (p.x_ntasks == 0 || p.x_task_max <= kStageMax);
+  const DevicePlan tp = hot_on ? hot_view(p, B, ldb, K, hot, s) : p;
   // the main part writes C; the split part (XCD column split) writes sub-row j to partial slot j
   auto run_tasks = [&](const DevicePlan& p, float* C, int64_t ldc) {
     if (p.ntasks <= 0) return;
@@ -1116,12 +1176,12 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // the L2's write combining (same-box A/B on grid+hubs: K=4 0.226 ms plain vs 0.246 streamed,
     // K=1 0.201 vs 0.208; K=8 0.292 plain vs 0.242 streamed, R-MAT K=16 0.341 vs 0.320)
     const int streaming = K >= 8 ? (p.streaming & 3) : (p.streaming & 1);
-#define TRS_TASKS_NT(L, U, PF, LS)                                                                        \
+#define TRS_TASKS_NT(L, U, PF, LS, ...)                                                                   \
     switch (streaming) {                                                                                  \
-      case 0: launch_tasks<VEC, L, U, 0, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      case 1: launch_tasks<VEC, L, U, 1, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      case 2: launch_tasks<VEC, L, U, 2, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      default: launch_tasks<VEC, L, U, 3, PF, LS>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;  \
+      case 0: launch_tasks<VEC, L, U, 0, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      case 1: launch_tasks<VEC, L, U, 1, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      case 2: launch_tasks<VEC, L, U, 2, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
+      default: launch_tasks<VEC, L, U, 3, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;  \
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
@@ -1129,7 +1189,8 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     if constexpr (L <= 8) {                                                                               \
       if (pf) { TRS_TASKS_NT(L, U, true, false) } else { TRS_TASKS_NT(L, U, false, false) }               \
     } else if constexpr (L == 16) {                                                                       \
-      if (ls) { TRS_TASKS_NT(L, U, false, true) } else { TRS_TASKS_NT(L, U, false, false) }               \
+      if (VEC == 8 && p.hot_b != nullptr) { TRS_TASKS_NT(L, U, false, true, VEC == 8) }                   \
+      else if (ls) { TRS_TASKS_NT(L, U, false, true) } else { TRS_TASKS_NT(L, U, false, false) }          \
     } else {                                                                                              \
       TRS_TASKS_NT(L, U, false, false)                                                                    \
     }                                                                                                     \
@@ -1139,8 +1200,8 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 #undef TRS_TASKS
 #undef TRS_TASKS_NT
   };
-  run_tasks(p, C, ldc);
-  if (p.x_ntasks > 0) run_tasks(split_view(p), partial, K);
+  run_tasks(tp, C, ldc);
+  if (p.x_ntasks > 0) run_tasks(split_view(tp), partial, K);
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {
     const int kc16 = ((K + 15) / 16) * 16;
@@ -1168,8 +1229,11 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 
 template <int VEC>
 hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                            int K, float* out, hipStream_t s, hipEvent_t* ev) {
+                            int K, float* out, uint16_t* hot, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
+  // staged hot Y rows (all K features, once per call) for the passes run by 16-lane groups
+  const bool hot_on = VEC == 8 && hot != nullptr && hot_buffer_bytes(p, K) > 0;
+  const DevicePlan hp = hot_on ? hot_view(p, Y, ldy, K, hot, s) : p;
   // feature passes of at most 128 features for 16-byte loads, each over all entries, the later
   // ones adding to the outputs: 256-byte slices of Y rows keep twice as many rows in an XCD's L2
   // as whole 512-byte rows, for one extra read and write of each output per pass (R-MAT 2^20
@@ -1180,6 +1244,7 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     const uint16_t* Xp = X + f0;
     const uint16_t* Yp = Y + f0;
     const int acc = f0 > 0 ? 1 : 0;
+    DevicePlan pp = p;
     int lpg = lanes_for(Kp, VEC);
     // fewer lanes than features: the kernel loops over feature chunks per batch (no second walk
     // of the entries), so narrow loads take the group width with the fewest lane slots (same-box
@@ -1191,6 +1256,10 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // outputs stream; lanes past K add zeros (R-MAT K=4 0.329 -> 0.258 ms, K=2 0.327 -> 0.259,
     // K=1 0.467 -> 0.260)
     if (p.feature_lanes <= 0 && lpg < 8) lpg = 8;
+    if (hot_on && lpg == 16) {
+      pp = hp;
+      pp.hot_b = hot + f0;
+    }
     // the main part, then the split part (XCD column split) through its view
     auto run_tasks = [&](const DevicePlan& p) {
     if (p.ntasks <= 0) return;
@@ -1209,6 +1278,16 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #define TRS_SD_U(L, U)                                                                                     \
     constexpr bool nt_ok = (U < L ? U : L) >= 8;                                                           \
     if constexpr (L == 16) {                                                                               \
+      if (VEC == 8 && p.hot_b != nullptr) {                                                                \
+        if (ls) {                                                                                          \
+          if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, true, false, nt_ok, VEC == 8);                        \
+          else TRS_SD_LAUNCH(VEC, L, U, true, false, false, VEC == 8);                                     \
+        } else {                                                                                           \
+          if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, false, false, nt_ok, VEC == 8);                       \
+          else TRS_SD_LAUNCH(VEC, L, U, false, false, false, VEC == 8);                                    \
+        }                                                                                                  \
+        break;                                                                                             \
+      }                                                                                                    \
       if (ls) {                                                                                            \
         if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, true, false, nt_ok);                                    \
         else TRS_SD_LAUNCH(VEC, L, U, true);                                                               \
@@ -1236,8 +1315,8 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       v.ntasks = p.nfull_tasks;
       run_tasks(v);
     } else {
-      run_tasks(p);
-      if (p.x_ntasks > 0) run_tasks(split_view(p));
+      run_tasks(pp);
+      if (p.x_ntasks > 0) run_tasks(split_view(pp));
     }
   }
   if (ev) (void)hipEventRecord(ev[1], s);
@@ -1337,6 +1416,24 @@ __global__ __launch_bounds__(256) void k_place_entries(const PlaceEntries a) {
   }
 }
 
+// Column histogram for the hot-row choice (global atomics: plan creation only).
+__global__ __launch_bounds__(256) void k_count_columns(const int32_t* __restrict__ col, int64_t total, int32_t n,
+                                                       int32_t* __restrict__ counts) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int32_t c = col[e];
+    if (c >= 0 && c < n) atomicAdd(&counts[c], 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_renumber_hot(const int32_t* __restrict__ col, int64_t total, int32_t n,
+                                                      const int32_t* __restrict__ rank, int32_t* __restrict__ hot_col) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int32_t c = col[e];
+    const int32_t r = c >= 0 && c < n ? rank[c] : -1;
+    hot_col[e] = r >= 0 ? ~r : c;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
 }
@@ -1347,6 +1444,24 @@ hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
   hipLaunchKernelGGL(k_zero_fill, dim3((unsigned)blocks), dim3(256), 0, stream, out, n);
+  return hipGetLastError();
+}
+
+static unsigned stride_grid(int64_t total) {
+  const int64_t b = (total + 255) / 256;
+  return (unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192);
+}
+
+hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream) {
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_count_columns, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, counts);
+  return hipGetLastError();
+}
+
+hipError_t launch_renumber_hot(const int32_t* col, int64_t total, int32_t n, const int32_t* rank, int32_t* hot_col,
+                               hipStream_t stream) {
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_renumber_hot, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, rank, hot_col);
   return hipGetLastError();
 }
 
@@ -1366,7 +1481,7 @@ hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream) {
 }
 
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
-                       float* partial, hipStream_t stream, hipEvent_t* ev) {
+                       float* partial, uint16_t* hot, hipStream_t stream, hipEvent_t* ev) {
   // wide loads only where they leave at least 4 lanes per group (whose column/value loads are
   // shared): with K <= 8 one or two lanes would stream a task alone (R-MAT K=8: 0.545 ms with one
   // 16-byte load per entry, 0.348 with two lanes of 8-byte loads, 0.283 with eight lanes of 2-byte
@@ -1389,14 +1504,16 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
   const bool v2 = (K > 8 || K == 6 || K == 8) && !(v8 || v4) && K % 2 == 0 && ldb % 2 == 0 && ldc % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(B) & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0 &&
                   (partial == nullptr || aligned16(partial));
-  if (v2) return launch_spmm_vec<2>(p, B, ldb, K, C, ldc, partial, stream, ev);
-  return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, stream, ev)
-       : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, stream, ev)
-            : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, stream, ev);
+  // (the staged hot rows need 16-byte aligned rows in the buffer too)
+  if (hot != nullptr && !aligned16(hot)) hot = nullptr;
+  if (v2) return launch_spmm_vec<2>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
+  return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, hot, stream, ev)
+       : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev)
+            : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
 }
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, hipStream_t stream, hipEvent_t* ev) {
+                        int K, float* out, uint16_t* hot, hipStream_t stream, hipEvent_t* ev) {
   // K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms with one lane of
   // 16-byte loads per task, 0.331), and up to K=64 8-byte loads are faster than 16-byte ones
   // (same-box A/B on R-MAT: K=32 0.468 -> 0.430 ms, K=64 0.550 -> 0.503; K=128 1.038 vs 1.080
@@ -1409,10 +1526,11 @@ hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, con
   // serve (K=18 0.743 -> 0.431 ms, K=66 1.866 -> 1.479, K=130 2.350 -> 1.993 with 2-byte loads)
   const bool v2 = K > 8 && (K <= 16 || !(v8 || v4)) && K % 2 == 0 && ldx % 2 == 0 && ldy % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(X) & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 3) == 0;
-  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, stream, ev);
-  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, stream, ev)
-       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, stream, ev)
-            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, stream, ev);
+  if (hot != nullptr && !aligned16(hot)) hot = nullptr;
+  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev);
+  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, hot, stream, ev)
+       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev)
+            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev);
 }
 
 }  // namespace trs

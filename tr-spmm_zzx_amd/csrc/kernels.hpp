@@ -91,7 +91,30 @@ struct DevicePlan {
   int32_t xcd_queues = 0;
   const int32_t* sub_row = nullptr;
   int32_t res_off = 0;   // res_pos[q - res_off] is entry q's output index
+  // Staged hot rows: hot_col is col with every entry of the nhot most used columns renumbered
+  // ~rank (rank 0 = most used), hot_rows[rank] that column.  A call copies those B (Y) rows into a
+  // dense buffer and the task kernels then read hot_col, gathering a negative id ~rank from the
+  // buffer (hot_b, leading dimension hot_ld: set in the launch view only).
+  const int32_t* hot_col = nullptr;
+  const int32_t* hot_rows = nullptr;
+  int32_t nhot = 0;
+  const uint16_t* hot_b = nullptr;
+  int32_t hot_ld = 0;
 };
+
+// Hot-row staging applies to 16-byte gathers of at least this many features (one 16-lane group,
+// 256-byte rows: R-MAT 2^20 K = 128 -6%, K = 256 -5%; K = 32 and 64 unchanged or slower).
+constexpr int kHotMinK = 128;
+// Bytes of the staged-row buffer of plan p at width K (0 when the plan or K does not stage).
+inline int64_t hot_buffer_bytes(const DevicePlan& p, int K) {
+  if (p.nhot <= 0 || K < kHotMinK || K % 8 != 0) return 0;
+  return (int64_t)p.nhot * K * 2;
+}
+// Column histogram of col[0, total) into counts[n] (zeroed by the caller; ids outside [0, n) are
+// skipped), and the renumbering hot_col[e] = rank[col[e]] >= 0 ? ~rank[col[e]] : col[e].
+hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream);
+hipError_t launch_renumber_hot(const int32_t* col, int64_t total, int32_t n, const int32_t* rank, int32_t* hot_col,
+                               hipStream_t stream);
 
 // SDDMM runs a plan's split part from this feature width on (narrower rows measured faster
 // unsplit).
@@ -131,13 +154,16 @@ struct PlaceEntries {
 };
 hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream);
 
-// ev (optional): 4 events recorded before the task kernel and after each of the three kernels.
+// hot: the staged-row buffer (hot_buffer_bytes(p, K) bytes; null = gather every row from B).
+// ev (optional): 4 events recorded before the task kernel (and the hot-row copy) and after each of
+// the three kernels.
 hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
-                       float* partial, hipStream_t stream, hipEvent_t* ev = nullptr);
+                       float* partial, uint16_t* hot, hipStream_t stream, hipEvent_t* ev = nullptr);
 // out[0, n) = 0 with a kernel (not a memset node: callers may capture the stream in a graph).
 hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream);
-// ev (optional): 3 events recorded before the residual kernel and after each of the two kernels.
+// hot: as for launch_spmm, Y rows.  ev (optional): 3 events recorded before the residual kernel
+// (and the hot-row copy) and after each of the two kernels.
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, hipStream_t stream, hipEvent_t* ev = nullptr);
+                        int K, float* out, uint16_t* hot, hipStream_t stream, hipEvent_t* ev = nullptr);
 
 }  // namespace trs

@@ -32,14 +32,14 @@ class PlanOptions(ctypes.Structure):
                 ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
                 ("xcd_run", c_i32), ("sddmm_unroll", c_i32), ("stage", c_i32),
                 ("occupancy", c_i32), ("xcd_split", c_i32), ("host_lowering", c_i32),
-                ("sptc_sparse", c_i32)]
+                ("sptc_sparse", c_i32), ("hot_rows", c_i32)]
 
 
 class PlanStats(ctypes.Structure):
     _fields_ = [("m", c_i64), ("n", c_i64), ("nnz", c_i64), ("mfma_tiles", c_i64), ("mfma_nnz", c_i64),
                 ("csr_nnz", c_i64), ("tasks", c_i64), ("split_rows", c_i64), ("partial_slots", c_i64),
                 ("device_bytes", c_i64), ("mfma_windows", c_i64), ("window_csr_nnz", c_i64),
-                ("device_lowered", c_i64), ("sparse_tiles", c_i64)]
+                ("device_lowered", c_i64), ("sparse_tiles", c_i64), ("hot_rows", c_i64), ("hot_entries", c_i64)]
 
 
 class ReorderParams(ctypes.Structure):
@@ -86,11 +86,14 @@ PROTOTYPES = {
     "trs_spmm_f16": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p]),
     "trs_spmm_f16_noalloc": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p]),
     "trs_sddmm_f16": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p]),
+    "trs_sddmm_workspace_bytes": (c_i64, [c_p, c_i32]),
+    "trs_sddmm_f16_ws": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p, c_i64, c_p]),
     "trs_spmm_f16_timed": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_i32, c_i32,
                                    ctypes.POINTER(c_f32)]),
     "trs_spmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p, c_i32,
                                        ctypes.POINTER(c_f32)]),
-    "trs_sddmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p, c_i32, ctypes.POINTER(c_f32)]),
+    "trs_sddmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p, c_i64, c_p, c_i32,
+                                        ctypes.POINTER(c_f32)]),
     "trs_last_error": (ctypes.c_char_p, []),
 }
 

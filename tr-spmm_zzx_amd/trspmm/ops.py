@@ -233,14 +233,14 @@ class Plan:
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
                     stage: Optional[int] = None, occupancy: Optional[int] = None,
                     xcd_split: Optional[int] = None, host_lowering: bool = False,
-                    sptc_sparse: bool = True) -> "Plan":
+                    sptc_sparse: bool = True, hot_rows: Optional[int] = None) -> "Plan":
         """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default).  host_lowering=True builds the
         residual on the host even when the format holds its input CSR (the plan is the same);
         sptc_sparse=False runs 2:4 tiles on the dense MFMA with zero fill instead of the sparse one."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap,
-                     xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split)
+                     xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split, hot_rows=hot_rows)
         o.host_lowering = int(bool(host_lowering))
         o.sptc_sparse = int(bool(sptc_sparse))
         h = ctypes.c_void_p()
@@ -253,14 +253,14 @@ class Plan:
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
                   streaming: Optional[int] = None, xcd_split: Optional[int] = None,
-                  host_lowering: bool = False) -> "Plan":
+                  host_lowering: bool = False, hot_rows: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
         residual outputs with non-temporal stores.  host_lowering=True builds the residual on the
         host even when the format holds its input CSR (the plan is the same)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
-                     streaming=streaming, xcd_split=xcd_split)
+                     streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows)
         o.host_lowering = int(bool(host_lowering))
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
@@ -271,7 +271,8 @@ class Plan:
     def from_csr(cls, rowptr, col, val_f16, m: int, n: int, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                  feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                  xcd_run: Optional[int] = None, stage: Optional[int] = None,
-                 occupancy: Optional[int] = None, xcd_split: Optional[int] = None) -> "Plan":
+                 occupancy: Optional[int] = None, xcd_split: Optional[int] = None,
+                 hot_rows: Optional[int] = None) -> "Plan":
         rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
         col = np.ascontiguousarray(col, dtype=np.int32)
         val = np.ascontiguousarray(val_f16, dtype=np.float16).view(np.uint16)
@@ -284,7 +285,7 @@ class Plan:
                              f"(got {col.shape[0]} and {val.shape[0]})")
         o = _options(False, False, 1.0, task_nnz, piece_nnz=piece_nnz, feature_lanes=feature_lanes,
                      streaming=streaming, xcd_run=xcd_run, stage=stage, occupancy=occupancy,
-                     xcd_split=xcd_split)
+                     xcd_split=xcd_split, hot_rows=hot_rows)
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_csr(_ptr(rowptr), _ptr(col), _ptr(val), m, n, ctypes.byref(o),
                                                 ctypes.byref(h)), "trs_plan_create_csr")
@@ -332,9 +333,15 @@ class Plan:
                                          ws_ptr, need, _stream_ptr(stream)), "trs_spmm_f16")
         return out
 
-    def sddmm(self, X: torch.Tensor, Y: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    def sddmm_workspace_bytes(self, K: int) -> int:
+        return int(nat.lib().trs_sddmm_workspace_bytes(self._h, K))
+
+    def sddmm(self, X: torch.Tensor, Y: torch.Tensor, out: Optional[torch.Tensor] = None,
+              workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
         """out[e] = X[row_e] . Y[col_e] for every stored entry (CSR order); float32 [nnz].  A given
-        ``out`` must be a contiguous float32 CUDA tensor of at least ``stats()['nnz']`` elements."""
+        ``out`` must be a contiguous float32 CUDA tensor of at least ``stats()['nnz']`` elements.
+        Plans with staged hot rows take a workspace (``sddmm_workspace_bytes(K)``), allocated on the
+        launch stream when not given."""
         st = self.stats()
         for name, t, rows in (("X", X, st["m"]), ("Y", Y, st["n"])):
             if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 2 and t.shape[0] == rows):
@@ -344,15 +351,24 @@ class Plan:
             raise ValueError("X and Y need the same feature width")
         X = X if X.stride(1) == 1 else X.contiguous()
         Y = Y if Y.stride(1) == 1 else Y.contiguous()
-        if out is None:
-            with torch.cuda.stream(_launch_stream(stream)):
+        K = X.shape[1]
+        need = self.sddmm_workspace_bytes(K)
+        with torch.cuda.stream(_launch_stream(stream)):
+            if out is None:
                 out = torch.empty(st["nnz"], dtype=torch.float32, device=X.device)
+            if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+                workspace = torch.empty(need, dtype=torch.uint8, device=X.device)
         if not (isinstance(out, torch.Tensor) and out.is_cuda and out.dtype == torch.float32 and out.is_contiguous()
                 and out.numel() >= st["nnz"]):
             raise ValueError(f"out must be a contiguous CUDA float32 tensor of at least {st['nnz']} elements")
         _on_current_device("out", out)
-        nat.check(nat.lib().trs_sddmm_f16(self._h, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), X.shape[1],
-                                          out.data_ptr(), _stream_ptr(stream)), "trs_sddmm_f16")
+        if need:
+            if not (workspace.is_cuda and workspace.is_contiguous()):
+                raise ValueError("workspace must be a contiguous CUDA tensor")
+            _on_current_device("workspace", workspace)
+        nat.check(nat.lib().trs_sddmm_f16_ws(self._h, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), K,
+                                             out.data_ptr(), workspace.data_ptr() if need else 0, need,
+                                             _stream_ptr(stream)), "trs_sddmm_f16_ws")
         return out
 
 
