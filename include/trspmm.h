@@ -316,7 +316,8 @@ int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, f
 
 /* trs_spmm_f16 without a workspace argument, for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
- * the reference.  The partial slots come from a static device array of TRS_NOALLOC_SCRATCH_BYTES,
+ * the reference.  The workspace (partial slots, staged hot rows) comes from a static device array of
+ * TRS_NOALLOC_SCRATCH_BYTES,
  * which every GPU the library runs on holds until the process ends; the call allocates nothing.
  * Plans whose trs_spmm_workspace_bytes(p, K) exceeds that size are refused with TRS_EINVAL.  All
  * calls on one GPU share its array: calls that overlap on one GPU race (serialise them).  Same

@@ -1,7 +1,8 @@
-// trs_spmm_f16_noalloc: trs_spmm_f16 with its partial-slot workspace taken from a static device
-// array instead of the caller, for callers that cannot allocate device memory (code under HIP graph
-// capture, tight serving loops, harnesses that forbid hipMalloc).  It launches the same kernels
-// with the same arguments, so its output is bitwise equal to trs_spmm_f16's.
+// trs_spmm_f16_noalloc: trs_spmm_f16 with its workspace (partial slots, staged hot rows) taken from
+// a static device array instead of the caller, for callers that cannot allocate device memory
+// (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+// launches the same kernels with the same arguments, so its output is bitwise equal to
+// trs_spmm_f16's.
 //
 // The array `scratch` below is held by every GPU the library runs on, at its own address on each,
 // until the process ends.  Host code never uses the array's name as a device address (in host code
@@ -9,7 +10,8 @@
 // hipGetSymbolAddress looks the address up, and that pointer -- kept per device -- is what the
 // kernels receive.  All calls on one GPU share its array: calls that overlap on one GPU (several
 // streams or threads at once) race and must be serialised by the caller.  Nothing needs clearing
-// between calls: every partial slot a call's fixup kernel reads was written earlier in that call.
+// between calls: every partial slot a call's fixup kernel reads, and every staged row its task
+// kernels read, was written earlier in that call.
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -66,7 +68,7 @@ extern "C" int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_
   if (K < 0) return fail(TRS_EINVAL, "K must be non-negative");
   const int64_t need = trs_spmm_workspace_bytes(p, K);
   if (need > kScratchBytes)
-    return fail(TRS_EINVAL, "trs_spmm_f16_noalloc: the plan's partial slots need " + std::to_string(need) +
+    return fail(TRS_EINVAL, "trs_spmm_f16_noalloc: the plan's workspace needs " + std::to_string(need) +
                                 " bytes at K = " + std::to_string(K) + ", more than the " +
                                 std::to_string(kScratchBytes) +
                                 "-byte scratch array holds; call trs_spmm_f16 with a workspace instead");
