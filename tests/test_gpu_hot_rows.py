@@ -184,3 +184,75 @@ def test_device_and_host_lowering_choose_the_same_rows():
     h = trspmm.Plan.from_format(f, g.m, g.n, host_lowering=True).stats()
     assert d["device_lowered"] == 1 and h["device_lowered"] == 0
     assert (d["hot_rows"], d["hot_entries"]) == (h["hot_rows"], h["hot_entries"])
+
+
+def test_graph_replays_restage_the_rows():
+    """Captured SpMM and SDDMM calls of a staging plan: each replay copies the hot rows again, so a
+    replay after new data is written into B (Y) matches an eager call on that data."""
+    g, f = rmat()
+    K = 128
+    sp = trspmm.Plan.from_format(f, g.m, g.n)
+    dp = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    assert sp.stats()["hot_rows"] > 0 and dp.sddmm_workspace_bytes(K) > 0
+    B = torch.from_numpy(graphs.dense_operand(g.n, K, seed=50)).cuda()
+    X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=51)).cuda()
+    C = torch.empty((g.m, K), device="cuda")
+    S = torch.empty(dp.stats()["nnz"], device="cuda")
+    ws = torch.empty(sp.workspace_bytes(K), dtype=torch.uint8, device="cuda")
+    wd = torch.empty(dp.sddmm_workspace_bytes(K), dtype=torch.uint8, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        sp.spmm(B, out=C, workspace=ws, stream=s)
+        dp.sddmm(X, B, out=S, workspace=wd, stream=s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sp.spmm(B, out=C, workspace=ws, stream=torch.cuda.current_stream())
+        dp.sddmm(X, B, out=S, workspace=wd, stream=torch.cuda.current_stream())
+    for seed in (52, 53, 54):
+        B.copy_(torch.from_numpy(graphs.dense_operand(g.n, K, seed=seed)).cuda())
+        C.fill_(float("nan"))
+        S.fill_(float("nan"))
+        ws.fill_(0xff)                     # stale staged rows would show
+        wd.fill_(0xff)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        say("graph replay", seed)
+        assert torch.equal(C, sp.spmm(B)), seed
+        assert torch.equal(S, dp.sddmm(X, B)), seed
+
+
+def test_threads_share_a_staging_plan():
+    """Staged rows live in each call's workspace: threads on their own streams with their own
+    workspaces get the default-stream result bitwise."""
+    import threading
+    g, f = rmat()
+    K = 128
+    p = trspmm.Plan.from_format(f, g.m, g.n)
+    Bs = [torch.from_numpy(graphs.dense_operand(g.n, K, seed=60 + t)).cuda() for t in range(4)]
+    want = [p.spmm(B) for B in Bs]
+    torch.cuda.synchronize()
+    got, errors = [None] * 4, []
+
+    def work(t):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                ws = torch.empty(p.workspace_bytes(K), dtype=torch.uint8, device="cuda")
+                for _ in range(3):
+                    got[t] = p.spmm(Bs[t], workspace=ws, stream=s)
+            s.synchronize()
+        except Exception as e:   # reported below
+            errors.append(e)
+
+    th = [threading.Thread(target=work, args=(t,)) for t in range(4)]
+    for x in th:
+        x.start()
+    for x in th:
+        x.join()
+    assert not errors, errors
+    for t in range(4):
+        assert torch.equal(got[t], want[t]), t
