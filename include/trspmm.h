@@ -209,7 +209,8 @@ typedef struct trs_plan_options {
                              a second copy of its column ids with those columns renumbered.  Used
                              for K >= 128 (K % 8 == 0) on 16-byte aligned operands.  0 = automatic
                              (16384 rows, at most n / 16, and only when they take >= 30% of the
-                             gathers), > 0 = that many rows, -1 = off */
+                             gathers), > 0 = that many rows, -1 = off.  Never for plans with more
+                             than 4 columns per entry (n > 4 nnz) */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

@@ -256,3 +256,19 @@ def test_threads_share_a_staging_plan():
     assert not errors, errors
     for t in range(4):
         assert torch.equal(got[t], want[t]), t
+
+
+def test_wide_sparse_matrix_stages_nothing():
+    """n far above the entry count: the per-column counts are not taken, even when asked for."""
+    m, n = 64, 1 << 20
+    rng = np.random.default_rng(3)
+    rowptr = np.arange(0, 4 * m + 1, 4, dtype=np.int32)
+    col = np.sort(rng.choice(n, size=(m, 4), replace=False), axis=1).reshape(-1).astype(np.int32)
+    val = rng.uniform(-1, 1, size=col.size).astype(np.float32)
+    f = trspmm.build_format(rowptr, col, val)
+    p = trspmm.Plan.from_format(f, m, n, hot_rows=100)
+    assert p.stats()["hot_rows"] == 0
+    Bh = graphs.dense_operand(n, 128, seed=4)
+    C = run_spmm(p, Bh)
+    e = osp.spmm_error(C, osp.csr_spmm(rowptr, col, val, Bh, m=m))
+    assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e

@@ -88,6 +88,7 @@ constexpr int32_t kWindowRowRatio = 2;
 constexpr int32_t kHotRows = 16384;
 constexpr int32_t kHotColumnShare = 16;
 constexpr int64_t kHotMinShare10 = 3;
+constexpr int64_t kHotMaxColumnsPerEntry = 4;
 
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
@@ -1096,7 +1097,9 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   if (opt.hot_rows < 0 || total <= 0 || d.n <= 0) return Status{};
   const int32_t n = d.n;
   const int32_t want = opt.hot_rows > 0 ? std::min(opt.hot_rows, n) : std::min(kHotRows, n / kHotColumnShare);
-  if (want <= 0) return Status{};
+  // the choice costs O(n) memory (a count per column, here and on the host): not for matrices with
+  // far more columns than entries, whose columns are mostly unused anyway
+  if (want <= 0 || (int64_t)n > kHotMaxColumnsPerEntry * total) return Status{};
   int32_t* counts = nullptr;
   if (hipMalloc(&counts, (size_t)n * 4) != hipSuccess) {
     (void)hipGetLastError();
