@@ -1309,8 +1309,11 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #undef TRS_SD_U
 #undef TRS_SD_LAUNCH
     };
-    if (p.x_ntasks > 0 && K < kSddmmSplitMinK) {   // the unsplit layout of every row
-      DevicePlan v = p;
+    // the unsplit layout of every row below kSddmmSplitMinK, and wherever hot rows are staged (the
+    // split then measured slower: R-MAT 2^20 K = 128 0.777 vs 0.773 ms unsplit, K = 256 1.693
+    // vs 1.570)
+    if (p.x_ntasks > 0 && (K < kSddmmSplitMinK || hot_on)) {
+      DevicePlan v = pp;
       v.tasks = p.full_tasks;
       v.ntasks = p.nfull_tasks;
       run_tasks(v);
