@@ -334,15 +334,18 @@ int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_t ldb, int3
 int trs_sddmm_f16(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                   int32_t K, float* out, void* stream);
 
-/* Bytes of device workspace trs_sddmm_f16_ws uses at feature width K: the plan's staged hot Y rows
- * (plan option hot_rows; 0 when the plan or K stages none).  No reference counterpart. */
+/* Bytes of device workspace trs_sddmm_f16_ws uses at feature width K: from K = 128, an output
+ * buffer for the plan's split part (XCD sub-rows of its long rows, merged into place at the end of
+ * the call) and the plan's staged hot Y rows (plan option hot_rows); 0 when the plan or K uses
+ * neither.  No reference counterpart. */
 int64_t trs_sddmm_workspace_bytes(const trs_plan* p, int32_t K);
 
-/* trs_sddmm_f16 with a workspace of trs_sddmm_workspace_bytes(p, K) bytes (fewer: TRS_EINVAL),
- * into which the call copies the plan's hot Y rows before the dot products gather them there.  The
- * same outputs, bitwise (only where a row is read from changes); trs_sddmm_f16 runs unstaged.  A
- * workspace is the call's own: calls that overlap need separate workspaces.  No reference
- * counterpart. */
+/* trs_sddmm_f16 with a workspace of trs_sddmm_workspace_bytes(p, K) bytes (fewer: TRS_EINVAL):
+ * the call copies the plan's hot Y rows there before the dot products gather them, and its split
+ * part writes its outputs there in its own order before a merge puts them in place.  The same
+ * outputs, bitwise (only where rows are read from and sums written to changes); trs_sddmm_f16
+ * runs without either.  A workspace is the call's own: calls that overlap need separate
+ * workspaces.  No reference counterpart. */
 int trs_sddmm_f16_ws(const trs_plan* p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
                      int32_t K, float* out, void* workspace, int64_t workspace_bytes, void* stream);
 

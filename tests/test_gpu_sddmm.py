@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from oracle import spmm as osp
+from trspmm import _native as nat
 from trspmm import graphs
 import trspmm
 
@@ -261,3 +262,38 @@ def test_sddmm_xcd_column_split_is_bitwise_equal():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
     assert np.max(np.abs(outs[1].cpu().numpy() - R)) <= (1e-5 * np.sqrt(128) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))
+
+
+@pytest.mark.parametrize("K", [128, 136, 200, 256])
+def test_sddmm_split_part_merged_equals_in_place(K):
+    """From K = 128 an SDDMM call with a workspace writes its split part (XCD sub-rows of the long
+    rows) into a buffer of its own and merges the split rows' outputs into place afterwards; the
+    call without a workspace writes them in place.  Same dot products, same outputs bitwise, and
+    against the closed form; both lowerings; feature passes (K > 128) accumulate in the buffer."""
+    print("sddmm merge", K, flush=True)
+    g = graphs.rmat(scale=16, edge_factor=16, seed=21)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    Xh = graphs.dense_operand(g.m, K, seed=70)
+    Yh = graphs.dense_operand(g.n, K, seed=71)
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    first = None
+    for host in (False, True):
+        for hot in (None, -1):
+            plan = trspmm.Plan.for_sddmm(f, g.m, g.n, host_lowering=host, hot_rows=hot)
+            st = plan.stats()
+            assert st["split_rows"] > 0, st
+            need = plan.sddmm_workspace_bytes(K)
+            assert need > 0   # the split part's output buffer (and the staged rows)
+            merged = plan.sddmm(X, Y)
+            inplace = torch.full((st["nnz"],), float("nan"), device="cuda")
+            nat.check(nat.lib().trs_sddmm_f16(plan.handle, X.data_ptr(), K, Y.data_ptr(), K, K, inplace.data_ptr(),
+                                              int(torch.cuda.current_stream().cuda_stream)), "trs_sddmm_f16")
+            torch.cuda.synchronize()
+            assert torch.equal(merged, inplace), (host, hot)
+            if first is None:
+                first = merged
+                got = merged.cpu().numpy()
+                tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, float(np.max(np.abs(R))))
+                assert np.max(np.abs(got - R)) <= tol
+            assert torch.equal(merged, first), (host, hot)

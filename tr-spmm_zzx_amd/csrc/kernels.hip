@@ -933,11 +933,39 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       const int e = b + li / (LPG / UB);
       if (li % (LPG / UB) == 0 && p + e < t.nz_end) {
         const int q = p + e;
-        float* o = &out[P.res_pos ? P.res_pos[q - P.res_off] : q];
+        float* o = &out[P.res_pos ? P.res_pos[q - P.res_off] : q - P.out_off];
         const float v = acc ? sum + *o : sum;
         if constexpr (NTO) __builtin_nontemporal_store(v, o);
         else *o = v;
       }
+    }
+  }
+}
+
+// The split rows' outputs into place (one workgroup per merge task): contiguous stores, reads from
+// the split part's buffer within the row's few runs.
+template <bool NTO>
+__global__ __launch_bounds__(256) void k_sddmm_merge(const MergeTask* __restrict__ tasks,
+                                                     const int32_t* __restrict__ x_src,
+                                                     const float* __restrict__ xbuf, float* __restrict__ out) {
+  // every load of a thread issued before the first store (indices past the task read entry 0)
+  constexpr int PER = kMergeTaskEntries / 256;
+  const MergeTask t = tasks[blockIdx.x];
+  int src[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = t.e_begin + (int)threadIdx.x + i * 256;
+    src[i] = x_src[t.k_begin + (e < t.e_end ? e - t.e_begin : 0)];
+  }
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = xbuf[src[i]];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = t.e_begin + (int)threadIdx.x + i * 256;
+    if (e < t.e_end) {
+      if constexpr (NTO) __builtin_nontemporal_store(v[i], out + e);
+      else out[e] = v[i];
     }
   }
 }
@@ -1229,11 +1257,13 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 
 template <int VEC>
 hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                            int K, float* out, uint16_t* hot, hipStream_t s, hipEvent_t* ev) {
+                            int K, float* out, uint16_t* hot, float* xbuf, hipStream_t s, hipEvent_t* ev) {
   if (ev) (void)hipEventRecord(ev[0], s);
   // staged hot Y rows (all K features, once per call) for the passes run by 16-lane groups
   const bool hot_on = VEC == 8 && hot != nullptr && hot_buffer_bytes(p, K) > 0;
   const DevicePlan hp = hot_on ? hot_view(p, Y, ldy, K, hot, s) : p;
+  // the split part writes its own buffer (then merged) where the workspace holds one
+  const bool merge_on = p.x_ntasks > 0 && xbuf != nullptr && merge_buffer_bytes(p, K) > 0;
   // feature passes of at most 128 features for 16-byte loads, each over all entries, the later
   // ones adding to the outputs: 256-byte slices of Y rows keep twice as many rows in an XCD's L2
   // as whole 512-byte rows, for one extra read and write of each output per pass (R-MAT 2^20
@@ -1261,7 +1291,7 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       pp.hot_b = hot + f0;
     }
     // the main part, then the split part (XCD column split) through its view
-    auto run_tasks = [&](const DevicePlan& p) {
+    auto run_tasks = [&](const DevicePlan& p, float* out) {
     if (p.ntasks <= 0) return;
     dim3 grid(residual_grid(p, 64 / lpg));
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
@@ -1309,18 +1339,29 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #undef TRS_SD_U
 #undef TRS_SD_LAUNCH
     };
-    // the unsplit layout of every row below kSddmmSplitMinK, and wherever hot rows are staged (the
-    // split then measured slower: R-MAT 2^20 K = 128 0.777 vs 0.773 ms unsplit, K = 256 1.693
-    // vs 1.570)
-    if (p.x_ntasks > 0 && (K < kSddmmSplitMinK || hot_on)) {
+    if (merge_on) {
+      // the split part into its own buffer, merged below
+      run_tasks(pp, out);
+      DevicePlan v = split_view(pp);
+      v.res_pos = nullptr;
+      v.out_off = (int32_t)p.nnz_csr;
+      run_tasks(v, xbuf);
+    } else if (p.x_ntasks > 0 && (K < kSddmmSplitMinK || hot_on)) {
+      // written in place, the split part's scattered outputs cost more than it saves below
+      // kSddmmSplitMinK, and wherever hot rows are staged (R-MAT 2^20 K = 128 0.777 vs 0.773 ms
+      // unsplit, K = 256 1.693 vs 1.570): the unsplit layout of every row
       DevicePlan v = pp;
       v.tasks = p.full_tasks;
       v.ntasks = p.nfull_tasks;
-      run_tasks(v);
+      run_tasks(v, out);
     } else {
-      run_tasks(pp);
-      if (p.x_ntasks > 0) run_tasks(split_view(pp));
+      run_tasks(pp, out);
+      if (p.x_ntasks > 0) run_tasks(split_view(pp), out);
     }
+  }
+  if (merge_on) {
+    if (p.streaming & 2) hipLaunchKernelGGL(k_sddmm_merge<true>, dim3(p.nmerge), dim3(256), 0, s, p.merge, p.x_src, xbuf, out);
+    else hipLaunchKernelGGL(k_sddmm_merge<false>, dim3(p.nmerge), dim3(256), 0, s, p.merge, p.x_src, xbuf, out);
   }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.ntiles > 0 && p.tile_pos) {
@@ -1400,6 +1441,7 @@ __global__ __launch_bounds__(256) void k_place_entries(const PlaceEntries a) {
         a.col_out[dst] = c;
         if (a.val_out) a.val_out[dst] = half_bits_of(__builtin_bit_cast(uint32_t, a.val[q]));
         if (a.x_pos) a.x_pos[dst - a.x_base] = q;
+        if (a.x_src) a.x_src[a.merge_off[si] + (q - b)] = (int32_t)(dst - a.x_base);
       }
     }
     if (a.compact) return;
@@ -1516,7 +1558,7 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
 }
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, uint16_t* hot, hipStream_t stream, hipEvent_t* ev) {
+                        int K, float* out, uint16_t* hot, float* xbuf, hipStream_t stream, hipEvent_t* ev) {
   // K <= 8 takes 2-byte loads so that K lanes share a task (R-MAT K=8: 0.747 ms with one lane of
   // 16-byte loads per task, 0.331), and up to K=64 8-byte loads are faster than 16-byte ones
   // (same-box A/B on R-MAT: K=32 0.468 -> 0.430 ms, K=64 0.550 -> 0.503; K=128 1.038 vs 1.080
@@ -1530,10 +1572,10 @@ hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, con
   const bool v2 = K > 8 && (K <= 16 || !(v8 || v4)) && K % 2 == 0 && ldx % 2 == 0 && ldy % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(X) & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 3) == 0;
   if (hot != nullptr && !aligned16(hot)) hot = nullptr;
-  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev);
-  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, hot, stream, ev)
-       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev)
-            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, nullptr, stream, ev);
+  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
+  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, hot, xbuf, stream, ev)
+       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev)
+            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
 }
 
 }  // namespace trs

@@ -26,6 +26,11 @@ constexpr int kXcds = 8;
 // and cold columns evenly over the XCDs.
 __host__ __device__ inline int xcd_of_column(int32_t c) { return (int)(((uint32_t)c * 2654435761u) >> 29); }
 
+// SDDMM split rows, merged: out[e] = xbuf[x_src[k_begin + e - e_begin]] for e in [e_begin, e_end),
+// at most kMergeTaskEntries indices per task (a multiple of 256).
+struct MergeTask { int32_t e_begin, e_end, k_begin, pad; };
+constexpr int32_t kMergeTaskEntries = 4096;
+
 // A window handled by the MFMA window kernel: 16 output rows starting at row0 (rows >= m are
 // dropped), dense 16x16 fp16 tiles [tile_begin, tile_end), plus that window's residual rows.
 struct MfmaWindow { int32_t row0, tile_begin, tile_end, pad; };
@@ -100,11 +105,26 @@ struct DevicePlan {
   int32_t nhot = 0;
   const uint16_t* hot_b = nullptr;
   int32_t hot_ld = 0;
+  // SDDMM split part written in its own order: with a buffer from the workspace, sub-row entry q
+  // (of the x_entries after the main part) writes xbuf[q - nnz_csr], and a merge pass puts the
+  // split rows' outputs in place: merge task i covers output indices [e_begin, e_end), whose
+  // values sit at xbuf[x_src[k]] (k counts the split rows' entries in output order)
+  const int32_t* x_src = nullptr;
+  const MergeTask* merge = nullptr;
+  int32_t nmerge = 0;
+  int64_t x_entries = 0;
+  int32_t out_off = 0;   // set in the view that writes xbuf: entry q writes out[q - out_off]
 };
 
 // Hot-row staging applies to 16-byte gathers of at least this many features (one 16-lane group,
 // 256-byte rows: R-MAT 2^20 K = 128 -6%, K = 256 -5%; K = 32 and 64 unchanged or slower).
 constexpr int kHotMinK = 128;
+// The SDDMM split part writes its own buffer (then merged) from this width on.
+constexpr int kSddmmMergeMinK = 128;
+// Bytes of that buffer for plan p at width K (0: the plan has no split part, or K is narrower).
+inline int64_t merge_buffer_bytes(const DevicePlan& p, int K) {
+  return p.nmerge > 0 && K >= kSddmmMergeMinK ? p.x_entries * 4 : 0;
+}
 // Bytes of the staged-row buffer of plan p at width K (0 when the plan or K does not stage).
 inline int64_t hot_buffer_bytes(const DevicePlan& p, int K) {
   if (p.nhot <= 0 || K < kHotMinK || K % 8 != 0) return 0;
@@ -151,6 +171,9 @@ struct PlaceEntries {
   int32_t* x_pos = nullptr;
   int64_t x_base = 0;
   int32_t compact = 1;
+  // SDDMM: x_src[merge_off[split_index] + offset in the row] = position - x_base (when x_src set)
+  const int32_t* merge_off = nullptr;
+  int32_t* x_src = nullptr;
 };
 hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream);
 
@@ -161,9 +184,12 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
                        float* partial, uint16_t* hot, hipStream_t stream, hipEvent_t* ev = nullptr);
 // out[0, n) = 0 with a kernel (not a memset node: callers may capture the stream in a graph).
 hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream);
-// hot: as for launch_spmm, Y rows.  ev (optional): 3 events recorded before the residual kernel
-// (and the hot-row copy) and after each of the two kernels.
+// hot: as for launch_spmm, Y rows.  xbuf: the split part's own output buffer
+// (merge_buffer_bytes(p, K) bytes; null = the split part writes its outputs in place).  ev
+// (optional): 3 events recorded before the residual kernels (and the hot-row copy) and after them
+// (and the merge), and after the tile kernel.
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
-                        int K, float* out, uint16_t* hot, hipStream_t stream, hipEvent_t* ev = nullptr);
+                        int K, float* out, uint16_t* hot, float* xbuf, hipStream_t stream,
+                        hipEvent_t* ev = nullptr);
 
 }  // namespace trs

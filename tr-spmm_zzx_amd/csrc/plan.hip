@@ -579,11 +579,13 @@ Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, 
 // of P.total entries; x_pos (SDDMM) gets the residual index of each sub-row entry.
 void move_entries(const Placement& P, const std::vector<int32_t>& rowptr, const int32_t* col, const uint16_t* val,
                   int32_t m, std::vector<int32_t>& col_out, std::vector<uint16_t>* val_out,
-                  std::vector<int32_t>* x_pos) {
+                  std::vector<int32_t>* x_pos, std::vector<int32_t>* x_src = nullptr,
+                  const std::vector<int32_t>* merge_off = nullptr) {
   const int64_t nent = rowptr[m];
   col_out.resize((size_t)P.total);
   if (val_out) val_out->resize((size_t)P.total);
   if (x_pos) x_pos->resize((size_t)(P.total - (P.compact ? 0 : nent)));
+  if (x_src) x_src->resize((size_t)(P.total - (P.compact ? 0 : nent)));
   // main part, in row order
   parallel_parts(lowering_threads(), (int64_t)m, 1 << 14, [&](int t) { return (int64_t)m * t / lowering_threads(); },
                  [&](int64_t rb, int64_t re, int) {
@@ -610,6 +612,7 @@ void move_entries(const Placement& P, const std::vector<int32_t>& rowptr, const 
                        col_out[o] = col[q];
                        if (val_out) (*val_out)[o] = val[q];
                        if (x_pos) (*x_pos)[o - xbase] = q;
+                       if (x_src) (*x_src)[(*merge_off)[i] + (q - rowptr[r])] = (int32_t)(o - xbase);
                      }
                    }
                  });
@@ -959,6 +962,8 @@ struct DeviceOut {
   int64_t x_base = 0;             // x_pos[i] belongs to entry x_base + i
   int32_t* tile_pos = nullptr;    // SDDMM with tiles: output index of each stored tile slot, else -1
   bool compact = true;            // SpMM: split rows only in their sub-rows
+  int32_t* x_src = nullptr;       // SDDMM split part: its buffer index of each split-row entry ...
+  const std::vector<int32_t>* merge_off = nullptr;   // ... counted from merge_off[split row index]
 };
 
 // Device half of the device lowering: the input CSR of rows [0, m) goes up once, the kept tiles'
@@ -988,6 +993,7 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   const size_t o_te = tmp.add(te);
   const size_t o_si = tmp.add(split_index);
   const size_t o_cur = tmp.add(PL.cursor);
+  const size_t o_moff = o.x_src ? tmp.add(*o.merge_off) : 0;
   // entry flags as bytes of 32-bit words (the marking kernel sets them with word atomics), then
   // the count of entries marked
   const size_t flag_bytes = ((size_t)cnnz + 3) & ~size_t(3);
@@ -1037,6 +1043,10 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   a.x_pos = o.x_pos;
   a.x_base = o.x_base;
   a.compact = o.compact ? 1 : 0;
+  if (o.x_src) {
+    a.merge_off = reinterpret_cast<const int32_t*>(base + o_moff);
+    a.x_src = o.x_src;
+  }
   if (trs::launch_place_entries(a, nullptr) != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess)
     return done(fail(TRS_EDEVICE, "device lowering: entry placement failed"));
   return done(Status{});
@@ -1493,8 +1503,19 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const Placement PL =
       src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, {}, false, split, reuse)
           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, split, reuse);
-  std::vector<int32_t> col2, x_pos;
-  if (!src) move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos);
+  // the split rows' outputs merged from the split part's own buffer: merge_off[i] = entries of the
+  // split rows before split row i; tasks of at most trs::kMergeTaskEntries output indices
+  std::vector<int32_t> merge_off(PL.split_rows.size() + 1, 0);
+  std::vector<trs::MergeTask> merge;
+  for (size_t i = 0; i < PL.split_rows.size(); ++i) {
+    const int32_t r = PL.split_rows[i];
+    const int32_t b = rowptr[r], e = rowptr[r + 1];
+    merge_off[i + 1] = merge_off[i] + (e - b);
+    for (int32_t q = b; q < e; q += trs::kMergeTaskEntries)
+      merge.push_back({q, std::min(e, q + trs::kMergeTaskEntries), merge_off[i] + (q - b), 0});
+  }
+  std::vector<int32_t> col2, x_pos, x_src;
+  if (!src) move_entries(PL, rowptr, col.data(), nullptr, m, col2, nullptr, &x_pos, &x_src, &merge_off);
   Tasks T = build_tasks(PL, rowptr, m, {}, false, opt);
   if (!T.st.ok()) return T.st;
 
@@ -1506,6 +1527,8 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const size_t o_xtasks = blob.add(T.xtasks);
   const size_t o_xrowptr = blob.add(PL.xrowptr);
   const size_t o_xpos = src ? blob.add_raw(nullptr, n_xpos * 4) : blob.add(x_pos);
+  const size_t o_xsrc = src ? blob.add_raw(nullptr, n_xpos * 4) : blob.add(x_src);
+  const size_t o_merge = blob.add(merge);
   const size_t o_srow = blob.add(PL.sub_row);
   const size_t o_full = blob.add(T.full);
   const size_t o_rpos = src ? blob.add_raw(nullptr, with_pos ? (size_t)nent * 4 : 0) : blob.add(res_pos);
@@ -1525,6 +1548,8 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
     o.res_pos = with_pos ? reinterpret_cast<int32_t*>(base + o_rpos) : nullptr;
     o.x_pos = n_xpos ? reinterpret_cast<int32_t*>(base + o_xpos) : nullptr;
     o.x_base = nent;
+    o.x_src = n_xpos ? reinterpret_cast<int32_t*>(base + o_xsrc) : nullptr;
+    o.merge_off = &merge_off;
     o.tile_pos = with_pos ? reinterpret_cast<int32_t*>(base + o_tpos) : nullptr;
     o.compact = false;
     const Status ds = residual_on_device(*src, m, with_pos ? L.tiles : std::vector<Lowering::Tile>{}, expect_marked, PL, o);
@@ -1546,6 +1571,10 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.x_rowptr = reinterpret_cast<const int32_t*>(base + o_xrowptr);
   d.x_pos = reinterpret_cast<const int32_t*>(base + o_xpos);
   d.x_sub_row = reinterpret_cast<const int32_t*>(base + o_srow);
+  d.x_src = reinterpret_cast<const int32_t*>(base + o_xsrc);
+  d.merge = reinterpret_cast<const trs::MergeTask*>(base + o_merge);
+  d.nmerge = (int32_t)merge.size();
+  d.x_entries = (int64_t)n_xpos;
   d.full_tasks = reinterpret_cast<const trs::Task*>(base + o_full);
   d.nfull_tasks = (int32_t)T.full.size();
   std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
@@ -1572,6 +1601,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   s.mfma_nnz = tile_entries;
   s.nnz = nent + tile_entries;
   s.tasks = (int64_t)(T.tasks.size() + T.xtasks.size());
+  s.split_rows = (int64_t)PL.split_rows.size();
   s.device_bytes = (int64_t)blob.size();
   s.device_lowered = src ? 1 : 0;
   const Status hs = stage_hot_rows(P, PL.total, opt);
@@ -1811,9 +1841,15 @@ int64_t trs_spmm_workspace_bytes(const trs_plan* p, int32_t K) {
   return hot > 0 ? ((partial + 255) & ~int64_t(255)) + hot : partial;
 }
 
+// SDDMM workspace: the split part's output buffer, then (256-byte aligned) the staged hot rows.
+static int64_t merge_region_bytes(const trs_plan* p, int32_t K) {
+  const int64_t b = trs::merge_buffer_bytes(p->dp, K);
+  return trs::hot_buffer_bytes(p->dp, K) > 0 ? (b + 255) & ~int64_t(255) : b;
+}
+
 int64_t trs_sddmm_workspace_bytes(const trs_plan* p, int32_t K) {
   if (!p || K <= 0 || !p->csr_only) return 0;
-  return trs::hot_buffer_bytes(p->dp, K);
+  return merge_region_bytes(p, K) + trs::hot_buffer_bytes(p->dp, K);
 }
 
 static int check_call(const trs_plan* p, int32_t K) {
@@ -1920,8 +1956,12 @@ static int sddmm_impl(const trs_plan* p, const uint16_t* X, int64_t ldx, const u
   const int64_t need = trs_sddmm_workspace_bytes(p, K);
   if (ws && ws_bytes < need)
     return report(fail(TRS_EINVAL, "trs_sddmm_f16_ws: workspace smaller than trs_sddmm_workspace_bytes"));
-  uint16_t* hot = ws && need > 0 ? static_cast<uint16_t*>(ws) : nullptr;
-  const hipError_t e = trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, hot, static_cast<hipStream_t>(stream), ev);
+  float* xbuf = ws && trs::merge_buffer_bytes(p->dp, K) > 0 ? static_cast<float*>(ws) : nullptr;
+  uint16_t* hot = ws && trs::hot_buffer_bytes(p->dp, K) > 0
+                      ? reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(ws) + merge_region_bytes(p, K))
+                      : nullptr;
+  const hipError_t e =
+      trs::launch_sddmm(p->dp, X, ldx, Y, ldy, K, out, hot, xbuf, static_cast<hipStream_t>(stream), ev);
   if (e != hipSuccess) return report(fail(TRS_EDEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e)));
   return TRS_OK;
 }
