@@ -261,7 +261,9 @@ def bench_sddmm(args, workload, g, K):
         nr = st["csr_nnz"]
         bytes_k = 8 * nr + 4 * (M + 1) + 2 * M * K + 2 * N * K
         impl = (4 * nr if st["mfma_tiles"] else 0) + 16 * st["tasks"]   # output index, task descriptors
-        impl += 4 * K * st["hot_rows"] if need else 0                   # staged hot rows: read + write
+        hot_bytes = 2 * K * st["hot_rows"] if need and K >= 128 and K % 8 == 0 else 0
+        impl += 2 * hot_bytes                                           # staged hot rows: read + write
+        impl += 3 * max(0, need - hot_bytes)                            # split-part merge: index, buffer, output (4 B each)
     else:
         bytes_k = 8 * st["mfma_nnz"] + 2 * M * K + 2 * N * K
         impl = st["mfma_tiles"] * (64 + 1024) - 4 * st["mfma_nnz"]      # column ids, dense output slots
