@@ -66,6 +66,9 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.trs_plan_stats_get(None, None) == 1
     assert lib.trs_spmm_f16(None, None, 0, 1, None, 0, None, 0, None) == 1
     assert lib.trs_spmm_workspace_bytes(None, 8) == 0
+    assert lib.trs_sddmm_workspace_bytes(None, 128) == 0
+    assert lib.trs_sddmm_f16(None, None, 0, None, 0, 1, None, None) == 1
+    assert lib.trs_sddmm_f16_ws(None, None, 0, None, 0, 1, None, None, 0, None) == 1
     assert lib.trs_format_slot(None, 0, None, None) == 1
 
 
