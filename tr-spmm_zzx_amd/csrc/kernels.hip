@@ -170,16 +170,22 @@ __device__ __forceinline__ int xcd_remap(int i, int n, int run) {
 // Residual task of lane group `grp` of wave `wave` (GPW lane groups per wave, 4 waves per
 // workgroup).  With per-XCD queues, workgroup i runs on XCD i mod kXcds and takes its tasks, in
 // order, from that XCD's queue; otherwise the tasks form one list spread by xcd_remap.
-__device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int grp, int gpw, bool& valid) {
+// block / nblocks: the workgroup's index among the nblocks that serve this task list (the launch's
+// own index and size, or the part of a fused launch, whose XCD is still block mod kXcds).
+__device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int grp, int gpw, bool& valid,
+                                             int block, int nblocks) {
   if (P.xcd_queues) {
-    const int x = (int)(blockIdx.x % kXcds), k = (int)(blockIdx.x / kXcds);
+    const int x = block % kXcds, k = block / kXcds;
     const int id = P.xq[x] + (k * 4 + wave) * gpw + grp;
     valid = id < P.xq[x + 1];
     return id;
   }
-  const int id = (xcd_remap(blockIdx.x, gridDim.x, P.xcd_run) * 4 + wave) * gpw + grp;
+  const int id = (xcd_remap(block, nblocks, P.xcd_run) * 4 + wave) * gpw + grp;
   valid = id < P.ntasks;
   return id;
+}
+__device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int grp, int gpw, bool& valid) {
+  return residual_task(P, wave, grp, gpw, valid, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Workgroups of 4 waves x gpw lane groups that cover the plan's residual tasks.
@@ -429,9 +435,9 @@ constexpr size_t tasks_static_lds(int lpg, bool ls) {
 // HOT: P.col is the hot-renumbered copy and negative ids gather from the staged rows P.hot_b
 // (staged streams only).
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
-__global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb,
-                                                    int K, float* __restrict__ C, int64_t ldc,
-                                                    float* __restrict__ partial) {
+__device__ __forceinline__ void spmm_tasks_run(const DevicePlan& P, int block, int nblocks,
+                                               const uint16_t* __restrict__ B, int64_t ldb, int K,
+                                               float* __restrict__ C, int64_t ldc, float* __restrict__ partial) {
   constexpr int GPW = 64 / LPG;
   constexpr bool NTL = (NT & kNtLoads) != 0;
   constexpr bool NTS = (NT & kNtStores) != 0;
@@ -449,7 +455,7 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
   const int grp = lane / LPG;
   const int li = lane % LPG;
   bool valid;
-  const int task_id = residual_task(P, wave, grp, GPW, valid);
+  const int task_id = residual_task(P, wave, grp, GPW, valid, block, nblocks);
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   const int32_t* __restrict__ col = P.col;
   const uint16_t* __restrict__ val = P.val;
@@ -519,6 +525,21 @@ __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan P, const uint16_t
     if (active) store_vec<VEC, NTS>(C + (int64_t)(t.row_begin + r) * ldc + f, acc);
     zero_acc(acc);
   }
+}
+
+// One launch for the main part (Pm, the first gm workgroups, into C) and the split part (Px, the
+// rest, sub-row j into partial slot j); gm is a multiple of kXcds, so a split-part workgroup keeps
+// its XCD (block mod kXcds).  One launch instead of two lets the split part start while the main
+// part's last workgroups finish (same-box A/B on R-MAT 2^20: K = 128 0.706 -> 0.689 ms, K = 256
+// 1.464 -> 1.420; the two parts' workgroups interleaved instead: 0.695 / 1.432, split part first
+// 0.695 / 1.443).  Without a split part, Px is unused and gm is the grid.
+template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
+__global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan Pm, DevicePlan Px, int gm,
+                                                    const uint16_t* __restrict__ B, int64_t ldb, int K,
+                                                    float* __restrict__ C, int64_t ldc, float* __restrict__ partial) {
+  const int b = (int)blockIdx.x;
+  if (b < gm) spmm_tasks_run<VEC, LPG, U, NT, PF, LS, HOT>(Pm, b, gm, B, ldb, K, C, ldc, partial);
+  else spmm_tasks_run<VEC, LPG, U, NT, PF, LS, HOT>(Px, b - gm, (int)gridDim.x - gm, B, ldb, K, partial, K, partial);
 }
 
 // C[row] = sum of a split row's partial slots, in slot order (deterministic), 4 slots in flight.
@@ -1091,10 +1112,10 @@ DevicePlan split_view(const DevicePlan& p) {
 }
 
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
-void launch_tasks(dim3 grid, int waves, hipStream_t s, const DevicePlan& p, const uint16_t* B, int64_t ldb, int K,
-                  float* C, int64_t ldc, float* partial) {
+void launch_tasks(dim3 grid, int gm, int waves, hipStream_t s, const DevicePlan& p, const DevicePlan& x,
+                  const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc, float* partial) {
   hipLaunchKernelGGL((k_spmm_tasks<VEC, LPG, U, NT, PF, LS, HOT>), grid, dim3(256),
-                     occupancy_pad(tasks_static_lds(LPG, LS), waves), s, p, B, ldb, K, C, ldc, partial);
+                     occupancy_pad(tasks_static_lds(LPG, LS), waves), s, p, x, gm, B, ldb, K, C, ldc, partial);
 }
 
 // Staged hot rows: dst[r][0, K) = B[rows[r]][0, K) for r < nhot, 16 bytes per thread (K % 8 == 0,
@@ -1172,10 +1193,15 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
                       p.task_max <= kStageMax && p.stage >= 0 &&
                       (p.x_ntasks == 0 || p.x_task_max <= kStageMax);
   const DevicePlan tp = hot_on ? hot_view(p, B, ldb, K, hot, s) : p;
-  // the main part writes C; the split part (XCD column split) writes sub-row j to partial slot j
-  auto run_tasks = [&](const DevicePlan& p, float* C, int64_t ldc) {
-    if (p.ntasks <= 0) return;
-    dim3 grid(residual_grid(p, 64 / lpg), passes);
+  // the main part writes C; the split part (XCD column split) writes sub-row j to partial slot j;
+  // both in one launch (see k_spmm_tasks)
+  const DevicePlan xv = split_view(tp);
+  auto run_tasks = [&](const DevicePlan& p, const DevicePlan& x) {
+    const int gpw = 64 / lpg;
+    const int gx = x.ntasks > 0 ? residual_grid(x, gpw) : 0;   // a multiple of kXcds
+    const int gm = p.ntasks <= 0 ? 0 : gx > 0 ? (residual_grid(p, gpw) + kXcds - 1) / kXcds * kXcds : residual_grid(p, gpw);
+    if (gm + gx == 0) return;
+    dim3 grid(gm + gx, passes);
     // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
     // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
     // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
@@ -1188,7 +1214,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // Its 27 KB of LDS per workgroup hold it at 5 waves per SIMD; that is not where the gain
     // comes from (the unstaged kernel forced to 5 waves takes 1.27 ms), and staging 128 entries
     // at a time to reach 8 waves measured 1.02 ms.
-    const bool ls = p.task_max <= kStageMax && p.stage >= 0;
+    const bool ls = p.task_max <= kStageMax && p.stage >= 0 && (x.ntasks <= 0 || x.task_max <= kStageMax);
     // occupancy: lane groups of <= 8 lanes (K <= 64) run 8 entries per batch and are held to 2 waves
     // per SIMD (same-box A/B at 7/6/5/4/3/2 waves: grid+hubs K=32 0.426 ... 0.395 / 0.389 ms,
     // R-MAT K=32 0.495 -> 0.420, K=64 0.579 -> 0.519, K=16 0.456 -> 0.400); wider groups run 2
@@ -1206,10 +1232,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     const int streaming = K >= 8 ? (p.streaming & 3) : (p.streaming & 1);
 #define TRS_TASKS_NT(L, U, PF, LS, ...)                                                                   \
     switch (streaming) {                                                                                  \
-      case 0: launch_tasks<VEC, L, U, 0, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      case 1: launch_tasks<VEC, L, U, 1, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      case 2: launch_tasks<VEC, L, U, 2, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;   \
-      default: launch_tasks<VEC, L, U, 3, PF, LS, ##__VA_ARGS__>(grid, waves, s, p, B, ldb, K, C, ldc, partial); break;  \
+      case 0: launch_tasks<VEC, L, U, 0, PF, LS, ##__VA_ARGS__>(grid, gm, waves, s, p, x, B, ldb, K, C, ldc, partial); break;   \
+      case 1: launch_tasks<VEC, L, U, 1, PF, LS, ##__VA_ARGS__>(grid, gm, waves, s, p, x, B, ldb, K, C, ldc, partial); break;   \
+      case 2: launch_tasks<VEC, L, U, 2, PF, LS, ##__VA_ARGS__>(grid, gm, waves, s, p, x, B, ldb, K, C, ldc, partial); break;   \
+      default: launch_tasks<VEC, L, U, 3, PF, LS, ##__VA_ARGS__>(grid, gm, waves, s, p, x, B, ldb, K, C, ldc, partial); break;  \
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
@@ -1228,8 +1254,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 #undef TRS_TASKS
 #undef TRS_TASKS_NT
   };
-  run_tasks(tp, C, ldc);
-  if (p.x_ntasks > 0) run_tasks(split_view(tp), partial, K);
+  run_tasks(tp, xv);
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {
     const int kc16 = ((K + 15) / 16) * 16;
