@@ -830,9 +830,10 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // HOT: P.col is the hot-renumbered copy and negative ids gather Y rows from the staged rows
 // P.hot_b.
 template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false, bool HOT = false>
-__global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_t* __restrict__ X, int64_t ldx,
-                                                     const uint16_t* __restrict__ Y, int64_t ldy, int K,
-                                                     float* __restrict__ out, int acc) {
+__device__ __forceinline__ void sddmm_tasks_run(const DevicePlan& P, int block, int nblocks,
+                                                const uint16_t* __restrict__ X, int64_t ldx,
+                                                const uint16_t* __restrict__ Y, int64_t ldy, int K,
+                                                float* __restrict__ out, int acc) {
   constexpr int GPW = 64 / LPG;
   constexpr int FPP = LPG * VEC;               // features per pass
   constexpr int UB = U < LPG ? U : LPG;        // entries per reduce_scatter batch
@@ -843,7 +844,7 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
   const int grp = lane / LPG;
   const int li = lane % LPG;
   bool valid;
-  const int task_id = residual_task(P, wave, grp, GPW, valid);
+  const int task_id = residual_task(P, wave, grp, GPW, valid, block, nblocks);
   const Task t = valid ? P.tasks[task_id] : Task{0, 0, 0, 0};
   const bool piece = t.row_end < 0;
   int* rp = s_rp[wave][grp];
@@ -961,6 +962,18 @@ __global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan P, const uint16_
       }
     }
   }
+}
+
+// Main part (Pm, the first gm workgroups, into out_m) and split part (Px, the rest, into out_x) in
+// one launch, as k_spmm_tasks (gm a multiple of kXcds where a split part follows).
+template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false, bool HOT = false>
+__global__ __launch_bounds__(256) void k_sddmm_tasks(DevicePlan Pm, DevicePlan Px, int gm,
+                                                     const uint16_t* __restrict__ X, int64_t ldx,
+                                                     const uint16_t* __restrict__ Y, int64_t ldy, int K,
+                                                     float* __restrict__ out_m, float* __restrict__ out_x, int acc) {
+  const int b = (int)blockIdx.x;
+  if (b < gm) sddmm_tasks_run<VEC, LPG, U, LS, SPF, NTO, HOT>(Pm, b, gm, X, ldx, Y, ldy, K, out_m, acc);
+  else sddmm_tasks_run<VEC, LPG, U, LS, SPF, NTO, HOT>(Px, b - gm, (int)gridDim.x - gm, X, ldx, Y, ldy, K, out_x, acc);
 }
 
 // The split rows' outputs into place (one workgroup per merge task): contiguous stores, reads from
@@ -1315,10 +1328,13 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       pp = hp;
       pp.hot_b = hot + f0;
     }
-    // the main part, then the split part (XCD column split) through its view
-    auto run_tasks = [&](const DevicePlan& p, float* out) {
-    if (p.ntasks <= 0) return;
-    dim3 grid(residual_grid(p, 64 / lpg));
+    // the main part (into out) and the split part (XCD column split, into xout) in one launch
+    auto run_tasks = [&](const DevicePlan& p, float* out, const DevicePlan& x, float* xout) {
+    const int gpw = 64 / lpg;
+    const int gx = x.ntasks > 0 ? residual_grid(x, gpw) : 0;   // a multiple of kXcds
+    const int gm = p.ntasks <= 0 ? 0 : gx > 0 ? (residual_grid(p, gpw) + kXcds - 1) / kXcds * kXcds : residual_grid(p, gpw);
+    if (gm + gx == 0) return;
+    dim3 grid(gm + gx);
     // column ids staged in LDS for 16-lane groups (K = 65..128; same-box A/B on R-MAT K=128:
     // 1.140 -> 1.112 ms; K=256 +1%, not staged); groups of <= 8 lanes load the next batch's
     // column ids while the current batch's gathers are in flight (K=32 0.429 -> 0.416 ms, K=8
@@ -1326,10 +1342,10 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // the plan asks for plain ones, where a group writes 8 consecutive sums (32 bytes) per store
     // (same-box A/B on R-MAT: K=8 0.329 -> 0.264 ms, K=32 0.423 -> 0.394, K=64 -1.5%, K=128 -1%;
     // 16-byte runs, as 4-lane groups write at K=16, lose: 0.418 -> 0.469)
-    const bool ls = p.task_max <= kStageMax && p.stage >= 0;
+    const bool ls = p.task_max <= kStageMax && p.stage >= 0 && (x.ntasks <= 0 || x.task_max <= kStageMax);
     const bool nto = (p.streaming & 2) != 0;
 #define TRS_SD_LAUNCH(...) \
-  hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, Xp, ldx, Yp, ldy, Kp, out, acc)
+  hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, x, gm, Xp, ldx, Yp, ldy, Kp, out, xout, acc)
 #define TRS_SD_U(L, U)                                                                                     \
     constexpr bool nt_ok = (U < L ? U : L) >= 8;                                                           \
     if constexpr (L == 16) {                                                                               \
@@ -1364,13 +1380,14 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
 #undef TRS_SD_U
 #undef TRS_SD_LAUNCH
     };
+    DevicePlan none = pp;
+    none.ntasks = 0;
     if (merge_on) {
       // the split part into its own buffer, merged below
-      run_tasks(pp, out);
       DevicePlan v = split_view(pp);
       v.res_pos = nullptr;
       v.out_off = (int32_t)p.nnz_csr;
-      run_tasks(v, xbuf);
+      run_tasks(pp, out, v, xbuf);
     } else if (p.x_ntasks > 0 && (K < kSddmmSplitMinK || hot_on)) {
       // written in place, the split part's scattered outputs cost more than it saves below
       // kSddmmSplitMinK, and wherever hot rows are staged (R-MAT 2^20 K = 128 0.777 vs 0.773 ms
@@ -1378,10 +1395,9 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       DevicePlan v = pp;
       v.tasks = p.full_tasks;
       v.ntasks = p.nfull_tasks;
-      run_tasks(v, out);
+      run_tasks(v, out, none, out);
     } else {
-      run_tasks(pp, out);
-      if (p.x_ntasks > 0) run_tasks(split_view(pp), out);
+      run_tasks(pp, out, p.x_ntasks > 0 ? split_view(pp) : none, out);
     }
   }
   if (merge_on) {
