@@ -31,6 +31,13 @@
 #include "half.hpp"
 #include "kernels.hpp"
 
+// This file is compiled once per part (see the Makefile): TRS_KERNEL_PART = 8, 4, 2, 1 builds the
+// SpMM / SDDMM launchers and kernels of that load width, 0 (the default) the plan-lowering kernels
+// and the dispatch between the widths, so the kernel templates build in parallel.
+#ifndef TRS_KERNEL_PART
+#define TRS_KERNEL_PART 0
+#endif
+
 namespace trs {
 namespace {
 
@@ -40,6 +47,12 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half16_t __attribute__((ext_vector_type(16)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+// ------------------------------------------------------------------------------------------------
+// SpMM / SDDMM kernels and their launchers (the width parts only).
+#if TRS_KERNEL_PART > 0
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -183,9 +196,6 @@ __device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int 
   const int id = (xcd_remap(block, nblocks, P.xcd_run) * 4 + wave) * gpw + grp;
   valid = id < P.ntasks;
   return id;
-}
-__device__ __forceinline__ int residual_task(const DevicePlan& P, int wave, int grp, int gpw, bool& valid) {
-  return residual_task(P, wave, grp, gpw, valid, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Workgroups of 4 waves x gpw lane groups that cover the plan's residual tasks.
@@ -1094,7 +1104,6 @@ __global__ __launch_bounds__(256) void k_sddmm_mfma32(DevicePlan P, const uint16
   }
 }
 
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 // LDS of one CU on gfx950.  The residual task kernel can be held to fewer workgroups per CU than
 // its registers allow by giving each workgroup unused dynamic LDS.
@@ -1420,8 +1429,11 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
   return hipGetLastError();
 }
 
+#endif  // TRS_KERNEL_PART > 0
+
 // ------------------------------------------------------------------------------------------------
-// Device-side plan lowering.
+// Device-side plan lowering (part 0 only).
+#if TRS_KERNEL_PART == 0
 
 // One workgroup per tile, one thread per (row, column) slot: binary search of the column in the
 // CSR row (columns ascending) and mark the entry; an entry counts when its flag was clear.
@@ -1523,8 +1535,42 @@ __global__ __launch_bounds__(256) void k_renumber_hot(const int32_t* __restrict_
 __global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
 }
+#endif  // TRS_KERNEL_PART == 0
 
 }  // namespace
+
+// Each load width's launchers -- and so its kernel instantiations -- are compiled in an object of
+// their own (this file with TRS_KERNEL_PART = the width), part 0 holds the rest and calls them.
+template <int VEC>
+hipError_t spmm_width(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
+                      float* partial, uint16_t* hot, hipStream_t s, hipEvent_t* ev);
+template <int VEC>
+hipError_t sddmm_width(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int K,
+                       float* out, uint16_t* hot, float* xbuf, hipStream_t s, hipEvent_t* ev);
+#if TRS_KERNEL_PART > 0
+template <int VEC>
+hipError_t spmm_width(const DevicePlan& p, const uint16_t* B, int64_t ldb, int K, float* C, int64_t ldc,
+                      float* partial, uint16_t* hot, hipStream_t s, hipEvent_t* ev) {
+  return launch_spmm_vec<VEC>(p, B, ldb, K, C, ldc, partial, hot, s, ev);
+}
+template <int VEC>
+hipError_t sddmm_width(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy, int K,
+                       float* out, uint16_t* hot, float* xbuf, hipStream_t s, hipEvent_t* ev) {
+  return launch_sddmm_vec<VEC>(p, X, ldx, Y, ldy, K, out, hot, xbuf, s, ev);
+}
+#endif
+#define TRS_WIDTH_INSTANCES(PREFIX, V)                                                                       \
+  PREFIX template hipError_t spmm_width<V>(const DevicePlan&, const uint16_t*, int64_t, int, float*, int64_t, \
+                                           float*, uint16_t*, hipStream_t, hipEvent_t*);                      \
+  PREFIX template hipError_t sddmm_width<V>(const DevicePlan&, const uint16_t*, int64_t, const uint16_t*,     \
+                                            int64_t, int, float*, uint16_t*, float*, hipStream_t, hipEvent_t*);
+#if TRS_KERNEL_PART > 0
+TRS_WIDTH_INSTANCES(, TRS_KERNEL_PART)
+#else
+TRS_WIDTH_INSTANCES(extern, 8)
+TRS_WIDTH_INSTANCES(extern, 4)
+TRS_WIDTH_INSTANCES(extern, 2)
+TRS_WIDTH_INSTANCES(extern, 1)
 
 hipError_t launch_zero_fill(float* out, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
@@ -1592,10 +1638,10 @@ hipError_t launch_spmm(const DevicePlan& p, const uint16_t* B, int64_t ldb, int 
                   (partial == nullptr || aligned16(partial));
   // (the staged hot rows need 16-byte aligned rows in the buffer too)
   if (hot != nullptr && !aligned16(hot)) hot = nullptr;
-  if (v2) return launch_spmm_vec<2>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
-  return v8 ? launch_spmm_vec<8>(p, B, ldb, K, C, ldc, partial, hot, stream, ev)
-       : v4 ? launch_spmm_vec<4>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev)
-            : launch_spmm_vec<1>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
+  if (v2) return spmm_width<2>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
+  return v8 ? spmm_width<8>(p, B, ldb, K, C, ldc, partial, hot, stream, ev)
+       : v4 ? spmm_width<4>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev)
+            : spmm_width<1>(p, B, ldb, K, C, ldc, partial, nullptr, stream, ev);
 }
 
 hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, const uint16_t* Y, int64_t ldy,
@@ -1613,10 +1659,11 @@ hipError_t launch_sddmm(const DevicePlan& p, const uint16_t* X, int64_t ldx, con
   const bool v2 = K > 8 && (K <= 16 || !(v8 || v4)) && K % 2 == 0 && ldx % 2 == 0 && ldy % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(X) & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 3) == 0;
   if (hot != nullptr && !aligned16(hot)) hot = nullptr;
-  if (v2) return launch_sddmm_vec<2>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
-  return v8 ? launch_sddmm_vec<8>(p, X, ldx, Y, ldy, K, out, hot, xbuf, stream, ev)
-       : v4 ? launch_sddmm_vec<4>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev)
-            : launch_sddmm_vec<1>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
+  if (v2) return sddmm_width<2>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
+  return v8 ? sddmm_width<8>(p, X, ldx, Y, ldy, K, out, hot, xbuf, stream, ev)
+       : v4 ? sddmm_width<4>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev)
+            : sddmm_width<1>(p, X, ldx, Y, ldy, K, out, nullptr, xbuf, stream, ev);
 }
+#endif  // TRS_KERNEL_PART == 0
 
 }  // namespace trs
