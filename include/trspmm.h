@@ -96,14 +96,18 @@ typedef struct trs_reorder_params {
                              for lsh_threshold like the reference's LSH library does */
   float lsh_threshold;    /* Jaccard similarity the LSH banding targets (0.2) */
   int32_t bucket_span;    /* LSH buckets larger than bucket_span + 1 pair each member with the
-                             next bucket_span members only (64) */
+                             next bucket_span members only (64); <= 0: every pair, as the
+                             reference */
   int32_t num_threads;    /* host threads; 0 = OpenMP default */
   int32_t exhaustive;     /* 1: every pair of non-empty sets is a candidate (small inputs, tests) */
   int32_t align_window;   /* 0: the reference's layout.  W > 0 (no reference counterpart): level-1
                              clusters never exceed W rows (thres is ignored) and are packed
                              first-fit decreasing into whole W-row windows per level-2 group, so
                              clusters do not straddle windows */
-  uint64_t seed;          /* MinHash permutation seed (2022) */
+  uint64_t seed;          /* MinHash permutation seed (1, the reference LSH library's default) */
+  int32_t minhash;        /* MinHash family: 1 = the reference's LSH library (datasketch: SHA-1 of
+                             the decimal string, permutations (a x + b) mod 2^61 - 1 drawn by
+                             numpy's legacy RandomState(seed)) (default); 0 = a 64-bit mixing hash */
 } trs_reorder_params;
 
 void trs_reorder_params_default(trs_reorder_params* p);
@@ -112,6 +116,16 @@ void trs_reorder_params_default(trs_reorder_params* p);
  * permutation of [0, rows). */
 int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t ncols,
                     const trs_reorder_params* params, int32_t* order);
+
+/* The reorder's LSH pieces, for tests and diagnostics (no reference counterpart; they expose what
+ * the reference's LSH library computes inside tr_tca_reorder.py:84-90, :121-123).
+ * trs_lsh_bands: the (bands, rows per band) minimising the equally weighted false-positive and
+ * false-negative areas for `threshold` at num_perm permutations.
+ * trs_minhash_signatures: sig[i * count + k] = the k-th MinHash value of set i (elements
+ * elems[off[i] .. off[i + 1]), non-negative; empty sets 0xffffffff) in params' family and seed. */
+int trs_lsh_bands(float threshold, int32_t num_perm, int32_t* bands, int32_t* rows);
+int trs_minhash_signatures(const int64_t* off, const int32_t* elems, int32_t nsets,
+                           const trs_reorder_params* params, int32_t count, uint32_t* sig);
 
 /* ---------------------------------------------------------------------------------------------
  * Statistics-only 2:4 matching ("dual routing").

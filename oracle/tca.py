@@ -8,12 +8,11 @@ Follows spmm/tr_csr_fp16/tr_tca_reorder.py:
     that pair is queued (:145-190, level 2 :282-323)
   * clusters in first-appearance order of their roots, members ascending (:195-205, :325-331)
   * final order: level-2 groups, their level-1 clusters, their rows (:333-340)
-Candidate pairs are every pair of non-empty sets (the LSH library the reference uses is absent
-here, and its candidate sets depend on its SHA-1 hashing); equal similarities pop in pair-key
-order, then by the first end (the reference's queue order for ties is not reproducible: it
-follows Python's per-process string hashing).  Parity of the LSH candidate generation is
-unpinned; the clustering and ordering rules are pinned by hand-derived cases in
-tests/test_reorder.py.
+Candidate pairs are every pair of non-empty sets, or those of the restated LSH library
+(oracle/minhash_lsh.py, lsh=True); equal similarities pop in pair-key order, then by the first end
+(the reference's queue order for ties is not reproducible: it follows Python's per-process string
+hashing).  The clustering and ordering rules are pinned by hand-derived cases in
+tests/test_reorder.py, the LSH restatement by numpy's RandomState and hashlib there.
 """
 from __future__ import annotations
 
@@ -28,21 +27,18 @@ def jaccard(a: frozenset, b: frozenset) -> float:
     return inter / union if union else 0.0
 
 
-def cluster(sets: list, thres: int, capped: bool = False) -> list:
-    """Root of every set after the greedy union-find clustering (exhaustive candidates).
-    capped (the library's window-aligned extension, no reference counterpart): merges that would
-    exceed `thres` members are skipped."""
+def cluster(sets: list, thres: int, capped: bool = False, pairs=None) -> list:
+    """Root of every set after the greedy union-find clustering; candidate pairs (a < b) given,
+    or every pair of non-empty sets.  capped (the library's window-aligned extension, no reference
+    counterpart): merges that would exceed `thres` members are skipped."""
     n = len(sets)
     key = lambda a, b: (min(a, b) * n + max(a, b))   # noqa: E731
     heap, queued = [], set()
-    for a in range(n):
-        if not sets[a]:
-            continue
-        for b in range(a + 1, n):
-            if not sets[b]:
-                continue
-            heapq.heappush(heap, (-jaccard(sets[a], sets[b]), key(a, b), a, b))
-            queued.add(key(a, b))
+    if pairs is None:
+        pairs = [(a, b) for a in range(n) if sets[a] for b in range(a + 1, n) if sets[b]]
+    for a, b in pairs:
+        heapq.heappush(heap, (-jaccard(sets[a], sets[b]), key(a, b), a, b))
+        queued.add(key(a, b))
     cid = list(range(n))
     size = [1] * n
     closed = [False] * n
@@ -120,16 +116,25 @@ def aligned_order(clusters: list, supers: list, W: int) -> list:
     return order
 
 
-def tca_order(rowptr, col, thres: int = 16, cluster_thres: int = 128, align_window: int = 0) -> list:
-    """order[new_row] = old_row, both levels, exhaustive candidates."""
+def tca_order(rowptr, col, thres: int = 16, cluster_thres: int = 128, align_window: int = 0,
+              lsh: bool = False, seed: int = 1) -> list:
+    """order[new_row] = old_row, both levels; candidates exhaustive, or (lsh) the restated LSH
+    library's at the reference's settings (threshold 0.2, 128 permutations, :60-61, :213-214)."""
     rows = len(rowptr) - 1
     sets = [frozenset(int(c) for c in col[rowptr[i]:rowptr[i + 1]]) for i in range(rows)]
+
+    def pairs(ss):
+        if not lsh:
+            return None
+        from oracle import minhash_lsh
+        return minhash_lsh.candidate_pairs(ss, 0.2, 128, seed)
+
     if align_window > 0:
-        clusters = groups(cluster(sets, align_window, capped=True))
+        clusters = groups(cluster(sets, align_window, capped=True, pairs=pairs(sets)))
     else:
-        clusters = groups(cluster(sets, thres))
+        clusters = groups(cluster(sets, thres, pairs=pairs(sets)))
     csets = [frozenset().union(*(sets[r] for r in cl)) for cl in clusters]
-    supers = groups(cluster(csets, cluster_thres))
+    supers = groups(cluster(csets, cluster_thres, pairs=pairs(csets)))
     if align_window > 0:
         return aligned_order(clusters, supers, align_window)
     return [r for grp in supers for c in grp for r in clusters[c]]

@@ -32,7 +32,7 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(nat.BuildParams) == 12 * 4
     assert ctypes.sizeof(nat.PlanOptions) == 16 * 4
     assert ctypes.sizeof(nat.PlanStats) == 16 * 8
-    assert ctypes.sizeof(nat.ReorderParams) == 40
+    assert ctypes.sizeof(nat.ReorderParams) == 48
     assert ctypes.sizeof(nat.MatchStats) == 16 * 8
 
 

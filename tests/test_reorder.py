@@ -157,3 +157,59 @@ def test_aligned_windows_recover_communities():
     val = np.ones(col.shape[0], np.float32)
     tc = lambda o: trspmm.build_format(*reorder.permute_rows(rp, col, o, val)).slot(3).size
     assert tc(aligned) > tc(plain)
+
+
+# ---- the LSH library's MinHash family (oracle/minhash_lsh.py) -------------------------------------
+
+def test_oracle_lsh_primitives_are_the_libraries():
+    """The restatement's two primitives: SHA-1 (hashlib) and numpy's legacy RandomState draws."""
+    from oracle import minhash_lsh as ml
+    assert ml.sha1_hash32(b"abc") == 0x363e99a9           # SHA-1("abc") starts a9 99 3e 36
+    a, b = ml.permutations(2, seed=1)
+    gen = np.random.RandomState(1)
+    want = [int(gen.randint(1, (1 << 61) - 1, dtype=np.uint64)), int(gen.randint(0, (1 << 61) - 1, dtype=np.uint64)),
+            int(gen.randint(1, (1 << 61) - 1, dtype=np.uint64)), int(gen.randint(0, (1 << 61) - 1, dtype=np.uint64))]
+    assert [int(a[0]), int(b[0]), int(a[1]), int(b[1])] == want
+    # a set's MinHash is the elementwise minimum over its elements' permuted hashes
+    v = ml.minhash([7, 11], num_perm=4)
+    assert np.array_equal(v, np.minimum(ml.minhash([7], num_perm=4), ml.minhash([11], num_perm=4)))
+    assert np.array_equal(ml.minhash([], num_perm=4), np.full(4, (1 << 32) - 1, dtype=np.uint64))
+
+
+@pytest.mark.parametrize("seed", [1, 2022])
+def test_native_signatures_equal_the_lsh_library_restatement(seed):
+    from oracle import minhash_lsh as ml
+    rng = np.random.default_rng(seed)
+    sets = [sorted({int(x) for x in rng.integers(0, 5_000_000, size=rng.integers(0, 30))}) for _ in range(40)]
+    sets.append([0, 9, 10, 99, 100, 2_147_483_647])      # decimal strings of every length
+    got = reorder.minhash_signatures(sets, count=128, seed=seed)
+    perms = ml.permutations(128, seed)
+    want = np.stack([ml.minhash(s, 128, seed, perms) for s in sets]).astype(np.uint32)
+    assert np.array_equal(got, want)
+
+
+def test_native_bands_equal_the_lsh_library_optimisation():
+    from oracle import minhash_lsh as ml
+    for t, n in [(0.2, 128), (0.1, 64), (0.3, 128), (0.5, 32), (0.7, 128), (0.9, 64)]:
+        assert reorder.lsh_bands(t, n) == ml.optimal_param(t, n), (t, n)
+
+
+@pytest.mark.parametrize("seed,rows,thres,cthres", [(1, 60, 16, 128), (2, 90, 4, 3), (3, 120, 8, 2),
+                                                    (4, 75, 2, 5), (7, 150, 16, 4)])
+def test_native_matches_oracle_with_lsh_candidates(seed, rows, thres, cthres):
+    """The reference's settings (MinHash family of its LSH library, seed 1, threshold 0.2, 128
+    permutations, every pair of a bucket): the same order as the oracle with the restated
+    library's candidate pairs -- which differs from the exhaustive order on these inputs."""
+    rp, col = random_clustered(rows, seed)
+    got = reorder.tca_order(rp, col, ncols=420, thres=thres, cluster_thres=cthres, bucket_span=0)
+    want = otca.tca_order(rp, col, thres=thres, cluster_thres=cthres, lsh=True)
+    assert got.tolist() == want
+
+
+def test_lsh_candidates_are_a_strict_subset_on_these_inputs():
+    from oracle import minhash_lsh as ml
+    rp, col = random_clustered(120, 3)
+    sets = [frozenset(int(c) for c in col[rp[i]:rp[i + 1]]) for i in range(len(rp) - 1)]
+    lsh = ml.candidate_pairs(sets)
+    every = [(a, b) for a in range(len(sets)) if sets[a] for b in range(a + 1, len(sets)) if sets[b]]
+    assert 0 < len(lsh) < len(every) and set(lsh) < set(every)

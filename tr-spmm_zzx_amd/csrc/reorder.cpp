@@ -13,11 +13,17 @@
 //   order    level-2 groups in order of their first cluster, level-1 clusters inside a group in
 //            index order, rows of a cluster in ascending order (:325-340)
 //
-// Deviations (both forced by scale or by the reference being non-deterministic):
-//   * MinHash values come from a fixed 64-bit mixing hash per permutation instead of the LSH
-//     library's SHA-1 of the decimal string, so candidate sets differ from the reference's;
+// MinHash family (params.minhash): 1 (default) = the reference's LSH library (datasketch, whose
+// MinHash and MinHashLSH the reference calls at :84-90, :121-123, :226-249): element e hashes to
+// the first 4 bytes (little-endian) of SHA-1 of its decimal string, permutation k maps it to
+// ((a_k e + b_k) mod 2^64) mod (2^61 - 1), low 32 bits, with (a_k, b_k) the k-th pair of draws
+// a in [1, 2^61 - 1), b in [0, 2^61 - 1) of numpy's legacy RandomState(seed) -- seed 1 is the
+// library's default -- and a band matches when its r values are equal; 0 = a 64-bit mixing hash
+// (faster, other candidates).
+// Deviations (forced by scale or by the reference being non-deterministic):
 //   * an LSH bucket with more than `bucket_span` + 1 sets pairs each set with the next
 //     `bucket_span` sets of the bucket only (the reference pairs all, O(bucket^2));
+//     bucket_span <= 0 pairs all, as the reference;
 //   * equal similarities pop in (pair key) order; the reference's queue order for ties depends on
 //     Python's per-process string hashing.
 // Extension (align_window = W > 0, no reference counterpart): level-1 merges that would exceed W
@@ -26,6 +32,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <queue>
 #include <vector>
@@ -49,6 +56,100 @@ uint64_t mix64(uint64_t x) {   // splitmix64 finaliser
   x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
   x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
   return x ^ (x >> 31);
+}
+
+// ---- the reference LSH library's MinHash family --------------------------------------------------
+uint32_t rotl32(uint32_t x, int k) { return (x << k) | (x >> (32 - k)); }
+
+// SHA-1 (FIPS 180-4) of a message of fewer than 56 bytes (one block); returns digest bytes 0..3 read
+// little-endian.
+uint32_t sha1_first32(const unsigned char* msg, size_t len) {
+  unsigned char block[64] = {0};
+  std::memcpy(block, msg, len);
+  block[len] = 0x80;
+  const uint64_t bits = (uint64_t)len * 8;
+  for (int i = 0; i < 8; ++i) block[63 - i] = (unsigned char)(bits >> (8 * i));
+  uint32_t w[80];
+  for (int i = 0; i < 16; ++i)
+    w[i] = (uint32_t)block[4 * i] << 24 | (uint32_t)block[4 * i + 1] << 16 | (uint32_t)block[4 * i + 2] << 8 |
+           (uint32_t)block[4 * i + 3];
+  for (int i = 16; i < 80; ++i) w[i] = rotl32(w[i - 3] ^ w[i - 8] ^ w[i - 14] ^ w[i - 16], 1);
+  uint32_t a = 0x67452301u, b = 0xEFCDAB89u, c = 0x98BADCFEu, d = 0x10325476u, e = 0xC3D2E1F0u;
+  for (int i = 0; i < 80; ++i) {
+    uint32_t f, k;
+    if (i < 20) { f = (b & c) | (~b & d); k = 0x5A827999u; }
+    else if (i < 40) { f = b ^ c ^ d; k = 0x6ED9EBA1u; }
+    else if (i < 60) { f = (b & c) | (b & d) | (c & d); k = 0x8F1BBCDCu; }
+    else { f = b ^ c ^ d; k = 0xCA62C1D6u; }
+    const uint32_t t = rotl32(a, 5) + f + e + k + w[i];
+    e = d; d = c; c = rotl32(b, 30); b = a; a = t;
+  }
+  const uint32_t h0 = 0x67452301u + a;   // digest bytes 0..3, big-endian
+  return (h0 >> 24) | ((h0 >> 8) & 0xff00u) | ((h0 << 8) & 0xff0000u) | (h0 << 24);
+}
+
+// Mersenne Twister MT19937 with numpy's legacy RandomState seeding of an integer seed and its
+// bounded 64-bit draws (mask the range, reject values past it; two 32-bit outputs per 64-bit one,
+// the first the high half).
+class Mt19937 {
+ public:
+  explicit Mt19937(uint32_t seed) {
+    mt_[0] = seed;
+    for (int i = 1; i < 624; ++i) mt_[i] = 1812433253u * (mt_[i - 1] ^ (mt_[i - 1] >> 30)) + (uint32_t)i;
+  }
+  uint32_t next32() {
+    if (pos_ >= 624) {
+      for (int i = 0; i < 624; ++i) {
+        const uint32_t y = (mt_[i] & 0x80000000u) | (mt_[(i + 1) % 624] & 0x7fffffffu);
+        mt_[i] = mt_[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+      }
+      pos_ = 0;
+    }
+    uint32_t y = mt_[pos_++];
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+  }
+  // uniform in [low, high)
+  uint64_t bounded(uint64_t low, uint64_t high) {
+    const uint64_t rng = high - low - 1;
+    if (rng == 0) return low;
+    uint64_t mask = rng;
+    for (int s = 1; s < 64; s <<= 1) mask |= mask >> s;
+    uint64_t v;
+    if (rng <= 0xffffffffull) {
+      do v = next32() & mask; while (v > rng);
+    } else {
+      do {
+        const uint64_t hi = next32();
+        v = ((hi << 32) | next32()) & mask;
+      } while (v > rng);
+    }
+    return low + v;
+  }
+
+ private:
+  uint32_t mt_[624];
+  int pos_ = 624;
+};
+
+constexpr uint64_t kMersenne61 = (1ull << 61) - 1;
+uint64_t mod_mersenne61(uint64_t x) {
+  uint64_t r = (x & kMersenne61) + (x >> 61);
+  return r >= kMersenne61 ? r - kMersenne61 : r;
+}
+
+// The first `used` permutations (a_k, b_k) of seed.
+void reference_permutations(uint64_t seed, int used, std::vector<uint64_t>& a, std::vector<uint64_t>& b) {
+  Mt19937 g((uint32_t)seed);
+  a.resize(used);
+  b.resize(used);
+  for (int k = 0; k < used; ++k) {
+    a[k] = g.bounded(1, kMersenne61);
+    b[k] = g.bounded(0, kMersenne61);
+  }
 }
 
 double jaccard(const Sets& S, int32_t a, int32_t b) {
@@ -147,6 +248,67 @@ class KeySet {
   size_t used_ = 0;
 };
 
+// MinHash signatures: sig[i * used + k] = the minimum over set i's elements of hash k (empty sets
+// keep 0xffffffff), in the family params.minhash selects.
+std::vector<uint32_t> signatures(const Sets& S, const trs_reorder_params& prm, int used) {
+  const int32_t n = S.size();
+  std::vector<uint32_t> sig((size_t)n * used, 0xffffffffu);
+  if (prm.minhash == 1) {
+    std::vector<uint64_t> pa, pb;
+    reference_permutations(prm.seed, used, pa, pb);
+    // element hashes, once per distinct element: a table over [0, max] when that is not much
+    // larger than the element count (columns of a matrix), else over the sorted distinct values
+    auto sha = [](int64_t v) {
+      char buf[24];
+      const int len = std::snprintf(buf, sizeof buf, "%lld", (long long)v);
+      return sha1_first32(reinterpret_cast<const unsigned char*>(buf), (size_t)len);
+    };
+    int64_t top = -1;
+    for (int32_t v : S.e) top = std::max<int64_t>(top, v);
+    const bool dense = top + 1 <= std::max<int64_t>((int64_t)S.e.size() * 4, 1 << 20);
+    std::vector<int32_t> distinct;
+    if (!dense) {
+      distinct = S.e;
+      std::sort(distinct.begin(), distinct.end());
+      distinct.erase(std::unique(distinct.begin(), distinct.end()), distinct.end());
+    }
+    const int64_t nh = dense ? top + 1 : (int64_t)distinct.size();
+    std::vector<uint32_t> hv((size_t)nh);
+#pragma omp parallel for schedule(static, 4096)
+    for (int64_t v = 0; v < nh; ++v) hv[v] = sha(dense ? v : distinct[v]);
+    auto hash_of = [&](int32_t e) -> uint64_t {
+      if (dense) return hv[e];
+      return hv[std::lower_bound(distinct.begin(), distinct.end(), e) - distinct.begin()];
+    };
+#pragma omp parallel for schedule(dynamic, 256)
+    for (int32_t i = 0; i < n; ++i) {
+      uint32_t* s = sig.data() + (size_t)i * used;
+      for (int64_t j = S.off[i]; j < S.off[i + 1]; ++j) {
+        const uint64_t h = hash_of(S.e[j]);
+        for (int k = 0; k < used; ++k) {
+          const uint32_t v = (uint32_t)(mod_mersenne61(pa[k] * h + pb[k]) & 0xffffffffu);
+          if (v < s[k]) s[k] = v;
+        }
+      }
+    }
+    return sig;
+  }
+  std::vector<uint64_t> coef(used);
+  for (int k = 0; k < used; ++k) coef[k] = mix64(prm.seed * 0x2545f4914f6cdd1dull + (uint64_t)k + 1);
+#pragma omp parallel for schedule(dynamic, 256)
+  for (int32_t i = 0; i < n; ++i) {
+    uint32_t* s = sig.data() + (size_t)i * used;
+    for (int64_t j = S.off[i]; j < S.off[i + 1]; ++j) {
+      const uint64_t base = mix64((uint64_t)(uint32_t)S.e[j]);
+      for (int k = 0; k < used; ++k) {
+        const uint32_t h = (uint32_t)(mix64(base ^ coef[k]) >> 32);
+        if (h < s[k]) s[k] = h;
+      }
+    }
+  }
+  return sig;
+}
+
 // Candidate pairs (a < b) of non-empty sets: MinHash LSH, or every pair when exhaustive.
 std::vector<std::pair<int32_t, int32_t>> candidates(const Sets& S, const trs_reorder_params& prm) {
   const int32_t n = S.size();
@@ -161,41 +323,32 @@ std::vector<std::pair<int32_t, int32_t>> candidates(const Sets& S, const trs_reo
   int bands, r;
   lsh_bands(prm.lsh_threshold, prm.num_perm, bands, r);
   const int used = bands * r;
-  std::vector<uint64_t> coef(used);
-  for (int k = 0; k < used; ++k) coef[k] = mix64(prm.seed * 0x2545f4914f6cdd1dull + (uint64_t)k + 1);
-  // signatures: per set, the minimum of the k-th hash over its elements
-  std::vector<uint32_t> sig((size_t)n * used, 0xffffffffu);
-#pragma omp parallel for schedule(dynamic, 256)
-  for (int32_t i = 0; i < n; ++i) {
-    uint32_t* s = sig.data() + (size_t)i * used;
-    for (int64_t j = S.off[i]; j < S.off[i + 1]; ++j) {
-      const uint64_t base = mix64((uint64_t)(uint32_t)S.e[j]);
-      for (int k = 0; k < used; ++k) {
-        const uint32_t h = (uint32_t)(mix64(base ^ coef[k]) >> 32);
-        if (h < s[k]) s[k] = h;
-      }
-    }
-  }
-  // per band: (band key, set) sorted; runs of equal keys are buckets
+  const std::vector<uint32_t> sig = signatures(S, prm, used);
+  // per band: sets sorted by their band values; runs of equal values are buckets
   std::vector<std::vector<std::pair<int32_t, int32_t>>> per_band(bands);
-  const int span = std::max(1, prm.bucket_span);
+  const size_t span = prm.bucket_span > 0 ? (size_t)prm.bucket_span : SIZE_MAX;
 #pragma omp parallel for schedule(dynamic, 1)
   for (int t = 0; t < bands; ++t) {
-    std::vector<std::pair<uint64_t, int32_t>> kv;
-    kv.reserve(n);
-    for (int32_t i = 0; i < n; ++i) {
-      if (!S.len(i)) continue;
-      uint64_t h = 0x84222325cbf29ce4ull ^ (uint64_t)t;
-      for (int k = 0; k < r; ++k) h = mix64(h ^ sig[(size_t)i * used + t * r + k]);
-      kv.push_back({h, i});
-    }
-    std::sort(kv.begin(), kv.end());
+    const uint32_t* base = sig.data() + (size_t)t * r;
+    auto band = [&](int32_t i) { return base + (size_t)i * used; };
+    auto less = [&](int32_t x, int32_t y) {
+      const uint32_t *a = band(x), *b = band(y);
+      for (int k = 0; k < r; ++k)
+        if (a[k] != b[k]) return a[k] < b[k];
+      return x < y;
+    };
+    auto same = [&](int32_t x, int32_t y) { return std::equal(band(x), band(x) + r, band(y)); };
+    std::vector<int32_t> ids;
+    ids.reserve(n);
+    for (int32_t i = 0; i < n; ++i)
+      if (S.len(i)) ids.push_back(i);
+    std::sort(ids.begin(), ids.end(), less);
     auto& dst = per_band[t];
-    for (size_t a = 0; a < kv.size();) {
+    for (size_t a = 0; a < ids.size();) {
       size_t e = a;
-      while (e < kv.size() && kv[e].first == kv[a].first) ++e;
+      while (e < ids.size() && same(ids[e], ids[a])) ++e;
       for (size_t x = a; x < e; ++x)
-        for (size_t y = x + 1; y < e && y <= x + (size_t)span; ++y) dst.push_back({kv[x].second, kv[y].second});
+        for (size_t y = x + 1; y < e && y - x <= span; ++y) dst.push_back({ids[x], ids[y]});
       a = e;
     }
   }
@@ -349,7 +502,56 @@ void trs_reorder_params_default(trs_reorder_params* p) {
   p->num_threads = 0;
   p->exhaustive = 0;
   p->align_window = 0;
-  p->seed = 2022;
+  p->seed = 1;
+  p->minhash = 1;
+}
+
+int trs_lsh_bands(float threshold, int32_t num_perm, int32_t* bands, int32_t* rows) {
+  if (!bands || !rows || num_perm < 1 || num_perm > 1024 || !(threshold > 0.0f && threshold < 1.0f)) {
+    trs::set_error("trs_lsh_bands: num_perm in 1..1024, threshold in (0, 1), bands and rows non-NULL");
+    return TRS_EINVAL;
+  }
+  int b = 1, r = 1;
+  lsh_bands(threshold, num_perm, b, r);
+  *bands = b;
+  *rows = r;
+  return TRS_OK;
+}
+
+int trs_minhash_signatures(const int64_t* off, const int32_t* elems, int32_t nsets, const trs_reorder_params* params,
+                           int32_t count, uint32_t* sig) {
+  trs_reorder_params prm;
+  trs_reorder_params_default(&prm);
+  if (params) prm = *params;
+  if (nsets < 0 || count < 1 || count > 1024 || !sig || (nsets > 0 && !off) || (prm.minhash != 0 && prm.minhash != 1)) {
+    trs::set_error("trs_minhash_signatures: bad arguments (count in 1..1024, minhash 0 or 1)");
+    return TRS_EINVAL;
+  }
+  Sets S;
+  S.off.assign(off, off + (size_t)nsets + 1);
+  if (S.off[0] != 0) {
+    trs::set_error("trs_minhash_signatures: off[0] must be 0");
+    return TRS_EINVAL;
+  }
+  for (int32_t i = 0; i < nsets; ++i)
+    if (S.off[i + 1] < S.off[i]) {
+      trs::set_error("trs_minhash_signatures: off must not decrease");
+      return TRS_EINVAL;
+    }
+  if (S.off[nsets] > 0 && !elems) {
+    trs::set_error("trs_minhash_signatures: NULL elements");
+    return TRS_EINVAL;
+  }
+  S.e.assign(elems, elems + S.off[nsets]);
+  for (int32_t v : S.e)
+    if (v < 0) {
+      trs::set_error("trs_minhash_signatures: elements must be non-negative");
+      return TRS_EINVAL;
+    }
+  if (prm.num_threads > 0) omp_set_num_threads(prm.num_threads);
+  const std::vector<uint32_t> out = signatures(S, prm, count);
+  std::copy(out.begin(), out.end(), sig);
+  return TRS_OK;
 }
 
 int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t ncols,
@@ -362,9 +564,10 @@ int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int
     return TRS_EINVAL;
   }
   if (prm.thres < 1 || prm.cluster_thres < 1 || prm.num_perm < 1 || prm.num_perm > 1024 ||
-      !(prm.lsh_threshold > 0.0f && prm.lsh_threshold < 1.0f) || prm.align_window < 0) {
+      !(prm.lsh_threshold > 0.0f && prm.lsh_threshold < 1.0f) || prm.align_window < 0 ||
+      (prm.minhash != 0 && prm.minhash != 1)) {
     trs::set_error("trs_tca_reorder: thres, cluster_thres >= 1, num_perm in 1..1024, lsh_threshold in (0, 1), "
-                   "align_window >= 0");
+                   "align_window >= 0, minhash 0 or 1");
     return TRS_EINVAL;
   }
   if (rows == 0) return TRS_OK;

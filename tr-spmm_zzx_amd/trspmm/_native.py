@@ -45,7 +45,7 @@ class PlanStats(ctypes.Structure):
 class ReorderParams(ctypes.Structure):
     _fields_ = [("thres", c_i32), ("cluster_thres", c_i32), ("num_perm", c_i32), ("lsh_threshold", ctypes.c_float),
                 ("bucket_span", c_i32), ("num_threads", c_i32), ("exhaustive", c_i32), ("align_window", c_i32),
-                ("seed", ctypes.c_uint64)]
+                ("seed", ctypes.c_uint64), ("minhash", c_i32)]
 
 
 class MatchStats(ctypes.Structure):
@@ -69,6 +69,8 @@ PROTOTYPES = {
     "trs_format_write": (c_i32, [c_p, ctypes.c_char_p]),
     "trs_reorder_params_default": (None, [ctypes.POINTER(ReorderParams)]),
     "trs_tca_reorder": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, ctypes.POINTER(ReorderParams), c_p]),
+    "trs_lsh_bands": (c_i32, [ctypes.c_float, c_i32, ctypes.POINTER(c_i32), ctypes.POINTER(c_i32)]),
+    "trs_minhash_signatures": (c_i32, [c_p, c_p, c_i32, ctypes.POINTER(ReorderParams), c_i32, c_p]),
     "trs_format_read": (c_i32, [ctypes.c_char_p, c_pp]),
     "trs_match_2to4": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(MatchStats)]),
     "trs_plan_options_default": (None, [ctypes.POINTER(PlanOptions)]),
