@@ -216,6 +216,40 @@ def test_window_row_cap_option(cap):
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"cap={cap}")
 
 
+def _blocks_with_long_rows(extra, seed):
+    """64 windows of 16 rows, each window a dense 16x16 block on its own 16 columns (TC tiles)
+    plus `extra` random residual entries in every row (uniformly long rows)."""
+    rng = np.random.default_rng(seed)
+    m, n = 1024, 200_000
+    rows = []
+    for r in range(m):
+        w = r // 16
+        cols = set(range(16 * w, 16 * w + 16)) | {int(x) for x in rng.integers(2048, n, size=extra)}
+        rows.append(sorted(cols))
+    rowptr = np.zeros(m + 1, np.int32)
+    rowptr[1:] = np.cumsum([len(c) for c in rows])
+    col = np.concatenate([np.array(c, np.int32) for c in rows])
+    val = rng.uniform(-1, 1, size=len(col)).astype(np.float32)
+    return m, n, rowptr, col, val
+
+
+@pytest.mark.parametrize("extra,kept", [(200, True), (700, False)])
+def test_windows_of_uniformly_long_rows(extra, kept):
+    """A window whose residual rows are all long keeps its tiles up to 4 x window_row_cap (512)
+    entries per row, and hands them back beyond that (the window kernel walks each row with one
+    lane group); with the cap lifted every window keeps them.  Against the oracle either way."""
+    say("long rows", extra)
+    m, n, rowptr, col, val = _blocks_with_long_rows(extra, seed=extra)
+    f = trspmm.build_format(rowptr, col, val)
+    Bh = dense_B(n, 128, seed=3)
+    R = osp.csr_spmm(rowptr, col, val, Bh, m=m)
+    for cap in (0, 1 << 30):
+        plan = trspmm.Plan.from_format(f, m, n, window_row_cap=cap)
+        windows = plan.stats()["mfma_windows"]
+        assert (windows > 0) == (kept or cap > 0), (extra, cap, plan.stats())
+        check(run_plan(plan, Bh), R, f"long rows {extra} cap {cap}")
+
+
 @pytest.mark.parametrize("xcd_run", [1, 3, 16, 64])
 @pytest.mark.parametrize("m", [997, 40000])
 def test_xcd_remap_covers_every_work_item(xcd_run, m):

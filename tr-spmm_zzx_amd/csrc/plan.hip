@@ -79,6 +79,11 @@ constexpr int32_t kSplitMinReuse = 4;
 // (K = 128 / 256) with every window handed back under the length rule alone, 0.796 / 1.473 ms with
 // this one; R-MAT, SBM and grid+hubs plans are unchanged (ratio 4 measured the same as 2).
 constexpr int32_t kWindowRowRatio = 2;
+// ... and whatever its neighbours, when that row is longer than this many times window_row_cap:
+// windows of 16 uniformly long hub rows, which a row reorder (TCA) puts together on power-law
+// graphs, each walked by one lane group (R-MAT 2^20 reordered, K = 128: 5.44 ms with such windows
+// kept; the task kernel cuts those rows into pieces and XCD sub-rows instead).
+constexpr int64_t kWindowRowHardFactor = 4;
 
 // Hot-row staging (option hot_rows = 0): the kHotRows most gathered columns of the task kernels,
 // at most one in kHotColumnShare of all columns, and only when they take at least
@@ -1212,7 +1217,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
         ++rows;
       }
       // only a row much longer than its window's others stalls the workgroup
-      demote[b] = longest > row_cap && longest * rows > (int64_t)kWindowRowRatio * sum;
+      demote[b] = longest > row_cap && (longest * rows > (int64_t)kWindowRowRatio * sum ||
+                                        longest > kWindowRowHardFactor * row_cap);
       any_demote |= demote[b] != 0;
     }
     if (any_demote) {
