@@ -297,3 +297,7 @@ def test_sddmm_split_part_merged_equals_in_place(K):
                 tol = (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, float(np.max(np.abs(R))))
                 assert np.max(np.abs(got - R)) <= tol
             assert torch.equal(merged, first), (host, hot)
+    # the plain-CSR plan (outputs in the given entry order) takes the same path
+    plan = trspmm.Plan.from_csr(g.rowptr[: g.m + 1], g.col, g.val.astype(np.float16), g.m, g.n)
+    assert plan.stats()["split_rows"] > 0
+    assert torch.equal(plan.sddmm(X, Y), first)
