@@ -274,3 +274,22 @@ def test_wide_sparse_matrix_stages_nothing():
     C = run_spmm(p, Bh)
     e = osp.spmm_error(C, osp.csr_spmm(rowptr, col, val, Bh, m=m))
     assert e["elementwise_ok"] and e["max_rel_to_max"] <= 1e-2, e
+
+
+@pytest.mark.parametrize("pad", [16, 8])
+def test_staged_rows_from_strided_operands(pad):
+    """B and Y as column slices of wider arrays (leading dimension K + pad, a multiple of 8): the
+    rows are staged from the strided operand into the dense buffer; bitwise equal to unstaged."""
+    g, f = rmat()
+    K = 128
+    hot = trspmm.Plan.from_format(f, g.m, g.n)
+    plain = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1)
+    Bw = torch.zeros((g.n, K + pad), dtype=torch.float16, device="cuda")
+    Bw[:, :K] = torch.from_numpy(graphs.dense_operand(g.n, K, seed=80)).cuda()
+    B = Bw[:, :K]
+    assert B.stride(0) == K + pad
+    assert torch.equal(hot.spmm(B), plain.spmm(B))
+    sh = trspmm.Plan.for_sddmm(f, g.m, g.n)
+    sp = trspmm.Plan.for_sddmm(f, g.m, g.n, hot_rows=-1)
+    X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=81)).cuda()
+    assert torch.equal(sh.sddmm(X, B), sp.sddmm(X, B))
