@@ -89,6 +89,16 @@ def kernel_ms(plan, B, C, ws, need, iters=10):
     return list(ms)
 
 
+def launched(kms, runs):
+    """Per-kernel event intervals, None for a kernel the plan does not launch: its interval is
+    empty and holds only the cost of the events themselves (~5 us)."""
+    return [v if r else None for v, r in zip(kms, runs)]
+
+
+def dominant(kms) -> int:
+    return max((i for i, v in enumerate(kms) if v is not None), key=lambda i: kms[i])
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -250,10 +260,10 @@ def bench_sddmm(args, workload, g, K):
                                                 out.data_ptr(), ws.data_ptr(), need,
                                                 int(torch.cuda.current_stream().cuda_stream), 10, ms),
               "trs_sddmm_f16_kernel_ms")
-    kms = list(ms)
+    kms = launched(list(ms), [st["tasks"] > 0, st["mfma_tiles"] > 0])
     ms_cold = cold_ms(lambda: plan.sddmm(X, Y, out=out, workspace=ws), max(5, min(args.steps, 10)))
     names = ["sddmm_tasks", "sddmm_mfma"]
-    dom = int(np.argmax(kms))
+    dom = dominant(kms)
     M, N = g.m, g.n
     # compulsory bytes (column id + fp32 output per entry, row pointers, X and Y once) of the share
     # the dominant kernel computes; the layout's extra bytes are reported apart
@@ -307,7 +317,7 @@ def roofline(bytes_k: int, impl: int, ms: float, kernel: str, names, kms, worklo
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
             "alg_bytes": int(bytes_k), "impl_bytes": int(impl), "kernel": kernel, "kernel_ms": round(ms, 4),
-            "kernel_ms_all": {n: round(v, 4) for n, v in zip(names, kms)}}
+            "kernel_ms_all": {n: None if v is None else round(v, 4) for n, v in zip(names, kms)}}
 
 
 def main():
@@ -411,9 +421,9 @@ def main():
     log(f"[bench] {ms_step:.4f} ms/step, {gflops:.1f} GFLOP/s")
 
     # dominant kernel: per-kernel HIP events on the launch stream
-    kms = kernel_ms(plan, B, C, ws, need)
+    kms = launched(kernel_ms(plan, B, C, ws, need), [st["tasks"] > 0, st["mfma_windows"] > 0, st["split_rows"] > 0])
     names = ["spmm_tasks", "spmm_mfma_win", "spmm_fixup"]
-    dom = int(np.argmax(kms))
+    dom = dominant(kms)
     M, N = g.m, g.n
     rows_w = min(M, 16 * st["mfma_windows"])
     nnz_w = st["window_csr_nnz"]
