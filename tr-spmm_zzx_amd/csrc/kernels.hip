@@ -871,17 +871,6 @@ __device__ __forceinline__ void sddmm_tasks_run(const DevicePlan& P, int block, 
   if constexpr (LS) {
     if (valid && t.nz_begin < t.nz_end) stage_cols<LPG>(P.col, t.nz_begin, t.nz_end, li, sc);
   }
-  __syncthreads();
-  if (!valid) return;
-
-  int r = 0;
-  int rend = piece ? t.nz_end : rp[1];
-  // with a single feature pass, the X fragment of the last row used carries over to the next
-  // batch, so X is fetched once per row instead of once per batch
-  const bool carry = K <= FPP;
-  BFrag<VEC> xc;
-  xc.zero();
-  int xrow = -1;
   // column ids of the batch at p (unconditional loads: padded slots repeat the last entry)
   auto load_cols = [&](int p, int (&cc)[U]) {
     if constexpr ((LPG == 2 || LPG == 4) && U % LPG == 0 && !LS) {
@@ -905,10 +894,24 @@ __device__ __forceinline__ void sddmm_tasks_run(const DevicePlan& P, int block, 
       }
     }
   };
-  // PF: the next batch's column ids are loaded while this batch's gathers are in flight
+  // PF: the next batch's column ids are loaded while this batch's gathers are in flight; the
+  // first batch's before the barrier
   constexpr bool PFC = SPF && !LS;
   int cn[U];
-  if constexpr (PFC) load_cols(t.nz_begin, cn);
+  if constexpr (PFC) {
+    if (valid && t.nz_begin < t.nz_end) load_cols(t.nz_begin, cn);
+  }
+  __syncthreads();
+  if (!valid) return;
+
+  int r = 0;
+  int rend = piece ? t.nz_end : rp[1];
+  // with a single feature pass, the X fragment of the last row used carries over to the next
+  // batch, so X is fetched once per row instead of once per batch
+  const bool carry = K <= FPP;
+  BFrag<VEC> xc;
+  xc.zero();
+  int xrow = -1;
   for (int p = t.nz_begin; p < t.nz_end; p += U) {
     int cc[U], rr[U];
     if constexpr (PFC) {
