@@ -700,11 +700,14 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
       }
     }
   }
-  // 2:4 quads on the sparse MFMA (layout in DevicePlan): per 64-feature chunk j, the quad's 64 B
-  // rows are staged row-major ([64][72] fp16, reusing the dense staging space); lane l's B operand
-  // is B[k][16 * wave + l % 16] for k = 8 (l / 16) + s (s < 8) and 32 + 8 (l / 16) + s - 8 (s >= 8)
+  // 2:4 quads on the sparse MFMA (layout in DevicePlan): per chunk j of CW = min(KC, 64) features,
+  // the quad's 64 B rows are staged row-major ([64][CW + 8] fp16, reusing the dense staging space;
+  // only the features the chunk's n-tiles use: SBM K = 16 -1.4%, K = 32 -0.4% against whole
+  // 64-feature rows); lane l's B operand is B[k][16 * wave + l % 16] for k = 8 (l / 16) + s (s < 8)
+  // and 32 + 8 (l / 16) + s - 8 (s >= 8)
   if (P.win_quad) {
-    constexpr int QS = 72;   // staged row stride (fp16)
+    const int CW = KC < 64 ? KC : 64;
+    const int QS = CW + 8;   // staged row stride (fp16)
     const int qb = P.win_quad[wi], qe = P.win_quad[wi + 1];
     for (int q = qb; q < qe; ++q) {
       const half8_t a = reinterpret_cast<const half8_t*>(P.quad_a)[(int64_t)q * 64 + lane];
@@ -712,7 +715,7 @@ void k_spmm_mfma_win(DevicePlan P, const uint16_t* __restrict__ B, int64_t ldb, 
 #pragma unroll
       for (int j = 0; j < NTILE; ++j) {
         __syncthreads();
-        const int per_row = 64 / VEC;
+        const int per_row = CW / VEC;
         for (int i2 = threadIdx.x; i2 < 64 * per_row; i2 += 256) {
           const int k = i2 / per_row;
           const int ff = (i2 % per_row) * VEC;
@@ -1303,8 +1306,9 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // (SBM 1M, K = 256: 0.912 ms with 256 features per workgroup, 0.871 with two of 128)
     const int KC = kc16 < 128 ? kc16 : 128;
     dim3 grid(p.nmwin, (K + KC - 1) / KC);
-    // staging space: 16 dense-tile B rows of KC features, or a quad's 64 rows of 64 (stride 72)
-    const size_t stage = std::max<size_t>((size_t)16 * (KC + 8), p.nquads > 0 ? (size_t)64 * 72 : 0);
+    // staging space: 16 dense-tile B rows of KC features, or a quad's 64 rows of min(KC, 64)
+    const int cw = KC < 64 ? KC : 64;
+    const size_t stage = std::max<size_t>((size_t)16 * (KC + 8), p.nquads > 0 ? (size_t)64 * (cw + 8) : 0);
     const size_t shm = (size_t)16 * (KC + 4) * 4 + stage * 2;
     if (KC <= 64) hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 1>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
     else hipLaunchKernelGGL((k_spmm_mfma_win<VEC, 2>), grid, dim3(256), shm, s, p, B, ldb, K, C, ldc, KC);
