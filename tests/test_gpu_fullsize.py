@@ -44,7 +44,11 @@ def rows_reference(g, rows, B64):
     return out
 
 
-@pytest.mark.parametrize("name,K", [("rmat20", 128), ("sbm1m", 256), ("grid_hubs", 32)])
+# every BASELINE width on R-MAT (K = 256: two feature passes, 8 MB of staged rows), the two ends on
+# SBM (MFMA windows of 32 and 128 features), grid+hubs at its headline width and at K = 128;
+# grouped by graph so that each graph is generated once
+@pytest.mark.parametrize("name,K", [("rmat20", 32), ("rmat20", 64), ("rmat20", 128), ("rmat20", 256),
+                                    ("sbm1m", 32), ("sbm1m", 256), ("grid_hubs", 32), ("grid_hubs", 128)])
 def test_fullsize_spmm_properties(name, K):
     print("fullsize", name, K, flush=True)
     g, f = graph(name)
@@ -86,7 +90,7 @@ def test_fullsize_spmm_properties(name, K):
     assert lin <= 2 * 2.0 ** -10 * rowabs + 1e-3
 
 
-@pytest.mark.parametrize("K", [32, 128])
+@pytest.mark.parametrize("K", [32, 64, 128, 256])
 def test_fullsize_sddmm_sampled(K):
     print("fullsize sddmm", K, flush=True)
     g, f = graph("rmat20")
