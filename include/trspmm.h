@@ -10,11 +10,26 @@
  *               call gets its own output buffer and workspace.
  * Device pointers (B, C, X, Y, out, workspace) are caller-owned HIP device memory; `stream` is a
  * hipStream_t (NULL = the default stream).  fp16 data is passed as uint16_t bit patterns.
+ *
+ * Versioning
+ *   Parameter structs (trs_build_params, trs_reorder_params, trs_plan_options) start with
+ *   `struct_size`, which their *_default initialiser sets to sizeof the struct of this header.
+ *   Every entry point that reads such a struct refuses a struct_size other than the library's
+ *   with TRS_EINVAL, before it reads anything past that first field, so a caller compiled against
+ *   another version of this header (whose struct may be shorter) gets an error, never a read past
+ *   its struct.  Always fill these structs with the *_default function of the header you compile
+ *   against, then change fields.  trs_plan_stats_get takes the size of the caller's stats struct
+ *   and refuses other sizes the same way.  TRSPMM_ABI_VERSION is the version of this header;
+ *   trs_abi_version() returns the library's.
  */
 #ifndef TRSPMM_H
 #define TRSPMM_H
 
 #include <stdint.h>
+
+/* 1: first release; 2: plan options xcd_split .. hot_rows, reorder minhash, wider plan stats;
+ * 3: struct_size fields and the stats size argument. */
+#define TRSPMM_ABI_VERSION 3
 
 #ifdef __cplusplus
 extern "C" {
@@ -36,6 +51,7 @@ typedef enum trs_status {
  * (TR-source/Block/block_online.cpp:545-549 signature, :844-870 return list).
  * ------------------------------------------------------------------------------------------- */
 typedef struct trs_build_params {
+  int32_t struct_size;       /* sizeof(trs_build_params), set by trs_build_params_default */
   int32_t part_size_t;       /* partSize_t: TC sub-blocks per part (32) */
   int32_t part_size_c;       /* partSize_c: residual nnz per long part (32) */
   int32_t short_size;        /* shortSize: residual rows with <= this nnz form short parts (3) */
@@ -90,6 +106,7 @@ int trs_format_read(const char* path, trs_format** out);
  * laid out cluster by cluster.  Deterministic for given parameters and thread-count independent.
  * ------------------------------------------------------------------------------------------- */
 typedef struct trs_reorder_params {
+  int32_t struct_size;    /* sizeof(trs_reorder_params), set by trs_reorder_params_default */
   int32_t thres;          /* rows at which a level-1 cluster closes (16) */
   int32_t cluster_thres;  /* level-1 clusters at which a level-2 group closes (128) */
   int32_t num_perm;       /* MinHash permutations (128); LSH bands x rows per band are chosen
@@ -169,6 +186,7 @@ int trs_match_2to4(const int32_t* rowptr, const int32_t* col, int32_t rows, int6
 typedef struct trs_plan trs_plan;
 
 typedef struct trs_plan_options {
+  int32_t struct_size;    /* sizeof(trs_plan_options), set by trs_plan_options_default */
   int32_t mfma_tc;        /* 1: TC sub-blocks run on MFMA tiles; 0: lowered to the CSR residual */
   int32_t mfma_sptc;      /* 1: 2:4 group tiles whose fill >= sptc_min_fill run on MFMA */
   float sptc_min_fill;    /* fill threshold (nnz / 256 slots of a 16x16 tile) for mfma_sptc */
@@ -313,7 +331,9 @@ typedef struct trs_plan_stats {
   int64_t hot_entries;               /* entries whose B (Y) rows are staged */
 } trs_plan_stats;
 
-int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s);
+/* stats_bytes = sizeof(trs_plan_stats) of the caller's header; any other size: TRS_EINVAL, nothing
+ * written. */
+int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s, int64_t stats_bytes);
 void trs_plan_free(trs_plan* p);
 
 /* ---------------------------------------------------------------------------------------------
@@ -336,7 +356,10 @@ int trs_spmm_f16(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, f
  * which every GPU the library runs on holds until the process ends; the call allocates nothing.
  * Plans whose trs_spmm_workspace_bytes(p, K) exceeds that size are refused with TRS_EINVAL.  All
  * calls on one GPU share its array: calls that overlap on one GPU race (serialise them).  Same
- * kernels and arguments as trs_spmm_f16, so the output is bitwise equal to it. */
+ * kernels and arguments as trs_spmm_f16, so the output is bitwise equal to it.  The first call on
+ * each device looks the array's address up (hipGetSymbolAddress): make that call outside stream
+ * capture.  Later calls only launch kernels and can be captured into a HIP graph; each replay
+ * rewrites the array's contents before reading them. */
 #define TRS_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
 int trs_spmm_f16_noalloc(const trs_plan* p, const uint16_t* B, int64_t ldb, int32_t K, float* C, int64_t ldc,
                          void* stream);
@@ -387,6 +410,9 @@ int trs_sddmm_f16_kernel_ms(const trs_plan* p, const uint16_t* X, int64_t ldx, c
                             void* stream, int32_t iters, float* ms);
 
 const char* trs_last_error(void);
+
+/* TRSPMM_ABI_VERSION of the header the library was built from. */
+int32_t trs_abi_version(void);
 
 #ifdef __cplusplus
 }

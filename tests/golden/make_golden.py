@@ -11,9 +11,16 @@ diagnostics on stdout; they are discarded.
     python tests/golden/make_golden.py digests
 
 writes tests/golden/builder_digests.json instead: for the full-size BASELINE configurations 1
-(Erdos-Renyi 4096) and 3 (SBM, 1M rows, 17.0M entries) and for R-MAT 2^18 (7.6M entries), too large
-to commit as arrays, the SHA-256 of the input CSR and of each of the reference's 29 output arrays
-(dtype, shape and bytes; see `array_digest`).  About two minutes of reference time in all.
+(Erdos-Renyi 4096), 3 (SBM, 1M rows, 17.0M entries) and 5 (2048 x 2048 grid + 64 hub rows of 100k
+columns, 23.2M entries) and for R-MAT 2^18 (7.6M entries), too large to commit as arrays, the
+SHA-256 of the input CSR and of each of the reference's 29 output arrays (dtype, shape and bytes;
+see `array_digest`).  Configurations 1 and 3 and R-MAT 2^18 take about two minutes of reference
+time; configuration 5 takes much longer, because the reference builds the complete unit graph of
+each hub window (about 50k units, O(n^2) memory and time).
+
+    python tests/golden/make_golden.py digests gridhubs4m_config5
+
+(re)computes only the named cases and keeps the other entries of the file.
 """
 from __future__ import annotations
 
@@ -107,13 +114,20 @@ def digest_cases():
     """(name, graph generator) of the full-size cases; the test regenerates the same graphs."""
     return [("er4096_config1", lambda: graphs.erdos_renyi_gcn()),
             ("sbm1m_config3", lambda: graphs.sbm()),
-            ("rmat18", lambda: graphs.rmat(scale=18, edge_factor=16, seed=31))]
+            ("rmat18", lambda: graphs.rmat(scale=18, edge_factor=16, seed=31)),
+            ("gridhubs4m_config5", lambda: graphs.grid_hubs())]
 
 
-def write_digests(mod):
+def write_digests(mod, only=()):
     import time
+    path = os.path.join(HERE, "builder_digests.json")
     out = {}
+    if only and os.path.exists(path):
+        with open(path) as f:
+            out = json.load(f)
     for name, gen in digest_cases():
+        if only and name not in only:
+            continue
         g = gen()
         t0 = time.time()
         arrs = run_reference(mod, g.rowptr, g.col, g.val, DEFAULT)
@@ -121,7 +135,8 @@ def write_digests(mod):
                      "slots": [array_digest(arrs[i]) for i in range(29)],
                      "shapes": [list(arrs[i].shape) for i in range(29)]}
         print(name, "nnz", g.nnz, f"reference {time.time() - t0:.1f}s", flush=True)
-    with open(os.path.join(HERE, "builder_digests.json"), "w") as f:
+        del arrs, g
+    with open(path, "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
 
@@ -130,8 +145,8 @@ def main():
     mod = ob.reference_module()
     if mod is None:
         sys.exit("oracle/_ref is not built (make -C oracle ref, needs /root/reference)")
-    if sys.argv[1:] == ["digests"]:
-        write_digests(mod)
+    if sys.argv[1:2] == ["digests"]:
+        write_digests(mod, tuple(sys.argv[2:]))
         return
     for name, rowptr, col, val, over, env in cases():
         p = dict(DEFAULT, **over)

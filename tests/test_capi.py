@@ -29,11 +29,99 @@ def test_every_declared_symbol_is_exported():
 
 
 def test_struct_layouts_match_header():
-    assert ctypes.sizeof(nat.BuildParams) == 12 * 4
-    assert ctypes.sizeof(nat.PlanOptions) == 16 * 4
+    assert ctypes.sizeof(nat.BuildParams) == 13 * 4
+    assert ctypes.sizeof(nat.PlanOptions) == 17 * 4
     assert ctypes.sizeof(nat.PlanStats) == 16 * 8
-    assert ctypes.sizeof(nat.ReorderParams) == 48
+    assert ctypes.sizeof(nat.ReorderParams) == 56
     assert ctypes.sizeof(nat.MatchStats) == 16 * 8
+
+
+def test_abi_version_and_default_struct_sizes():
+    lib = nat.lib()
+    assert lib.trs_abi_version() == int(re.search(r"#define TRSPMM_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    for cls, fn in ((nat.BuildParams, lib.trs_build_params_default), (nat.PlanOptions, lib.trs_plan_options_default),
+                    (nat.ReorderParams, lib.trs_reorder_params_default)):
+        p = cls()
+        fn(ctypes.byref(p))
+        assert p.struct_size == ctypes.sizeof(cls)
+
+
+class _GuardedBuffer:
+    """`size` caller bytes followed by a canary region: a library that reads or writes past the
+    caller's struct would touch the canary (writes are checked; reads of it would be of 0xA5 bytes,
+    which are no valid struct_size either)."""
+
+    def __init__(self, size: int, fill: bytes):
+        self.size = size
+        self.buf = ctypes.create_string_buffer(fill.ljust(size, b"\0") + b"\xa5" * 256, size + 256)
+
+    def ptr(self):
+        return ctypes.cast(self.buf, ctypes.c_void_p)
+
+    def canary_intact(self) -> bool:
+        return self.buf.raw[self.size:] == b"\xa5" * 256
+
+
+def _round1_plan_options() -> bytes:
+    """The 12-field trs_plan_options of the first header (mfma_tc .. occupancy), defaults."""
+    import struct
+    return struct.pack("<iifiiiiiiiii", 1, 1, 0.25, 0, 0, 0, -1, 0, 0, 0, 0, 0)
+
+
+def _round2_plan_options() -> bytes:
+    """The 16-field trs_plan_options of the second header (no struct_size), defaults."""
+    import struct
+    return struct.pack("<iifiiiiiiiiiiiii", 1, 1, 0.25, 0, 0, 0, -1, 0, 0, 0, 0, 0, 0, 0, 1, 0)
+
+
+@pytest.mark.parametrize("layout", ["round1", "round2"])
+def test_older_plan_options_layouts_are_refused(layout):
+    """A caller compiled against an earlier header passes a shorter options struct without
+    struct_size: every plan constructor refuses it with TRS_EINVAL (its first field, mfma_tc = 1,
+    is no valid size) before reading past that field.  No GPU is touched: the check comes first."""
+    lib = nat.lib()
+    blob = _round1_plan_options() if layout == "round1" else _round2_plan_options()
+    g = _GuardedBuffer(len(blob), blob)
+    rowptr = np.array([0, 1], np.int32)
+    col = np.array([0], np.int32)
+    val = np.zeros(1, np.uint16)
+    h = ctypes.c_void_p()
+    rc = lib.trs_plan_create_csr(rowptr.ctypes.data, col.ctypes.data, val.ctypes.data, 1, 1,
+                                 ctypes.cast(g.ptr(), ctypes.POINTER(nat.PlanOptions)), ctypes.byref(h))
+    assert rc == 1 and not h.value
+    assert b"struct_size" in lib.trs_last_error()
+    assert g.canary_intact()
+
+
+def test_older_build_and_reorder_params_are_refused():
+    import struct
+    lib = nat.lib()
+    old_build = struct.pack("<iiiiiiffiiii", 32, 32, 3, 8, 16, 16, 0.0, 0.5, 12, -1, -1, 0)   # 12 fields
+    g = _GuardedBuffer(len(old_build), old_build)
+    rowptr = np.array([0, 1], np.int32)
+    col = np.array([0], np.int32)
+    val = np.ones(1, np.float32)
+    h = ctypes.c_void_p()
+    rc = lib.trs_build_online(rowptr.ctypes.data, col.ctypes.data, val.ctypes.data, 1, 1,
+                              ctypes.cast(g.ptr(), ctypes.POINTER(nat.BuildParams)), ctypes.byref(h))
+    assert rc == 1 and not h.value and b"struct_size" in lib.trs_last_error() and g.canary_intact()
+    old_reorder = struct.pack("<iiifiiiiQi", 16, 128, 128, 0.2, 64, 0, 0, 0, 1, 1)   # no struct_size
+    g = _GuardedBuffer(len(old_reorder), old_reorder)
+    order = np.zeros(1, np.int32)
+    rc = lib.trs_tca_reorder(rowptr.ctypes.data, col.ctypes.data, 1, 1, 1,
+                             ctypes.cast(g.ptr(), ctypes.POINTER(nat.ReorderParams)), order.ctypes.data)
+    assert rc == 1 and b"struct_size" in lib.trs_last_error() and g.canary_intact()
+
+
+@pytest.mark.parametrize("stats_bytes", [12 * 8, 16 * 8 - 8, 16 * 8 + 8])
+def test_plan_stats_of_another_size_are_refused(stats_bytes):
+    """trs_plan_stats_get checks the caller's stats size (12 fields in the first header) before
+    anything else, so the check is visible without a plan (GPU); with a real plan it is repeated in
+    tests/test_gpu_operators.py."""
+    lib = nat.lib()
+    g = _GuardedBuffer(stats_bytes, b"")
+    rc = lib.trs_plan_stats_get(None, ctypes.cast(g.ptr(), ctypes.POINTER(nat.PlanStats)), stats_bytes)
+    assert rc == 1 and b"stats_bytes" in lib.trs_last_error() and g.canary_intact()
 
 
 def _plan_csr(rowptr, col, val, m, n):
@@ -63,7 +151,7 @@ def test_plan_from_noncanonical_format_is_refused():
 def test_null_arguments_are_errors_not_crashes():
     lib = nat.lib()
     assert lib.trs_build_online(None, None, None, 0, 0, None, None) == 1
-    assert lib.trs_plan_stats_get(None, None) == 1
+    assert lib.trs_plan_stats_get(None, None, 0) == 1
     assert lib.trs_spmm_f16(None, None, 0, 1, None, 0, None, 0, None) == 1
     assert lib.trs_spmm_workspace_bytes(None, 8) == 0
     assert lib.trs_sddmm_workspace_bytes(None, 128) == 0

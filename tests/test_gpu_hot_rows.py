@@ -138,8 +138,10 @@ def test_noalloc_with_staged_rows():
         assert np.array_equal(C.cpu().numpy(), run_spmm(p, Bh))
 
 
-@pytest.mark.parametrize("K", [128, 256, 200, 64])
+@pytest.mark.parametrize("K", [128, 256, 200, 64, 136, 264])
 def test_sddmm_staged_equals_unstaged(K):
+    """K = 136 and 264 end in a feature pass of 8 features (under 16 lanes), which reads the plain
+    column ids while the earlier passes read the staged rows, accumulating into the same outputs."""
     g, f = rmat()
     hot = trspmm.Plan.for_sddmm(f, g.m, g.n)
     plain = trspmm.Plan.for_sddmm(f, g.m, g.n, hot_rows=-1)

@@ -427,3 +427,21 @@ def test_feature_passes_with_split_rows(K):
     C = run_plan(plan, Bh)
     check(C, osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"passes K={K}")
     assert np.array_equal(C, run_plan(plan, Bh))
+
+
+def test_plan_stats_size_is_checked_with_a_real_plan():
+    """trs_plan_stats_get on a device plan: a stats struct of another header's size (12 fields in
+    the first one) gets TRS_EINVAL and nothing is written past it; the right size succeeds."""
+    import ctypes
+    from trspmm import _native as nat
+    say("case stats size")
+    g = graphs.random_csr(64, 64, 0.1, seed=2)
+    plan = trspmm.Plan.from_format(trspmm.build_format(g.rowptr, g.col, g.val), g.m, g.n)
+    lib = nat.lib()
+    for size in (12 * 8, 15 * 8, 17 * 8):
+        buf = ctypes.create_string_buffer(b"\xa5" * (size + 256), size + 256)
+        rc = lib.trs_plan_stats_get(plan.handle, ctypes.cast(buf, ctypes.POINTER(nat.PlanStats)), size)
+        assert rc == 1 and buf.raw == b"\xa5" * (size + 256), size
+    s = nat.PlanStats()
+    assert lib.trs_plan_stats_get(plan.handle, ctypes.byref(s), ctypes.sizeof(s)) == 0
+    assert s.m == g.m and s.nnz == g.nnz

@@ -89,3 +89,38 @@ def test_noalloc_refuses_plans_beyond_the_scratch_array():
     B2 = torch.from_numpy(graphs.dense_operand(g2.n, 96, seed=2)).cuda()
     rc, C2 = _noalloc(plan2, B2)
     assert rc == 0 and torch.equal(C2, _with_workspace(plan2, B2))
+
+
+def test_noalloc_captured_in_a_graph_after_a_warm_up_call():
+    """The header's graph-capture use: after one call outside capture on the device (which looks up
+    the scratch array's address), a noalloc call is captured into a HIP graph and replayed three
+    times, with eager work between replays that overwrites the shared scratch array (a noalloc call
+    of another plan); every replay equals the eager trs_spmm_f16 result bitwise."""
+    print("noalloc: graph capture after warm-up", flush=True)
+    g, plan = _split_plan(128, 4, 8000, 3)
+    g2, plan2 = _split_plan(48, 2, 1500, 5)
+    K = 128
+    B = torch.from_numpy(graphs.dense_operand(g.n, K, seed=11)).cuda()
+    B2 = torch.from_numpy(graphs.dense_operand(g2.n, 64, seed=12)).cuda()
+    ref = _with_workspace(plan, B)
+    rc, _ = _noalloc(plan, B)          # warm-up outside capture
+    assert rc == 0, nat.lib().trs_last_error().decode()
+    C = torch.full((plan.stats()["m"], K), float("nan"), dtype=torch.float32, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = nat.lib().trs_spmm_f16_noalloc(plan.handle, B.data_ptr(), B.stride(0), K, C.data_ptr(), C.stride(0),
+                                                int(side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert rc == 0, nat.lib().trs_last_error().decode()
+    for i in range(3):
+        rc2, _ = _noalloc(plan2, B2)   # eager work that rewrites the scratch array
+        assert rc2 == 0
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(C, ref), f"replay {i}"

@@ -30,6 +30,7 @@
 #include <memory_resource>
 #include <omp.h>
 #include <optional>
+#include <string>
 #include <vector>
 
 #include "format.hpp"
@@ -508,6 +509,7 @@ extern "C" {
 
 void trs_build_params_default(trs_build_params* p) {
   if (!p) return;
+  p->struct_size = (int32_t)sizeof(trs_build_params);
   // spmm/spmm_3090_fp16_test.py:30-40 defaults
   p->part_size_t = 32;
   p->part_size_c = 32;
@@ -528,6 +530,12 @@ int trs_build_online(const int32_t* rowptr, const int32_t* col, const float* val
   if (!out) { trs::set_error("trs_build_online: out is NULL"); return TRS_EINVAL; }
   *out = nullptr;
   if (!prm) { trs::set_error("trs_build_online: params is NULL"); return TRS_EINVAL; }
+  if (prm->struct_size != (int32_t)sizeof(trs_build_params)) {
+    trs::set_error("trs_build_online: trs_build_params.struct_size is " + std::to_string(prm->struct_size) +
+                   ", this library's is " + std::to_string(sizeof(trs_build_params)) +
+                   " (initialise the parameters with trs_build_params_default of the same trspmm.h)");
+    return TRS_EINVAL;
+  }
   // block_online.cpp:551-553
   if (!(prm->window > 0 && prm->window <= 32 && prm->wide > 0 && prm->wide <= 32)) {
     trs::set_error("trs_build_online: requires 0 < window <= 32 and 0 < wide <= 32");

@@ -1546,6 +1546,21 @@ __global__ __launch_bounds__(256) void k_count_columns(const int32_t* __restrict
   }
 }
 
+// Takes the residual entries of MFMA-window rows back out of a column histogram: the window kernel
+// gathers them through the plain column ids, never from the staged rows.  One workgroup per window.
+__global__ __launch_bounds__(256) void k_uncount_windows(const MfmaWindow* __restrict__ mwin, int32_t m,
+                                                         const int32_t* __restrict__ rowptr,
+                                                         const int32_t* __restrict__ col, int32_t n,
+                                                         int32_t* __restrict__ counts) {
+  const MfmaWindow w = mwin[blockIdx.x];
+  const int32_t r1 = min(w.row0 + 16, m);
+  if (w.row0 >= r1) return;
+  for (int32_t e = rowptr[w.row0] + (int32_t)threadIdx.x; e < rowptr[r1]; e += 256) {
+    const int32_t c = col[e];
+    if (c >= 0 && c < n) atomicSub(&counts[c], 1);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_renumber_hot(const int32_t* __restrict__ col, int64_t total, int32_t n,
                                                       const int32_t* __restrict__ rank, int32_t* __restrict__ hot_col) {
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
@@ -1610,6 +1625,13 @@ static unsigned stride_grid(int64_t total) {
 hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream) {
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_count_columns, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, counts);
+  return hipGetLastError();
+}
+
+hipError_t launch_uncount_windows(const MfmaWindow* mwin, int32_t nmwin, int32_t m, const int32_t* rowptr,
+                                  const int32_t* col, int32_t n, int32_t* counts, hipStream_t stream) {
+  if (nmwin <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_uncount_windows, dim3((unsigned)nmwin), dim3(256), 0, stream, mwin, m, rowptr, col, n, counts);
   return hipGetLastError();
 }
 

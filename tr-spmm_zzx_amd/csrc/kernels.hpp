@@ -135,6 +135,10 @@ inline int64_t hot_buffer_bytes(const DevicePlan& p, int K) {
 hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream);
 hipError_t launch_renumber_hot(const int32_t* col, int64_t total, int32_t n, const int32_t* rank, int32_t* hot_col,
                                hipStream_t stream);
+// counts[col[e]] -= 1 for the residual entries e of the nmwin MFMA windows' rows (rowptr [m + 1]):
+// the window kernel reads those through the plain ids, so they do not count towards staging.
+hipError_t launch_uncount_windows(const MfmaWindow* mwin, int32_t nmwin, int32_t m, const int32_t* rowptr,
+                                  const int32_t* col, int32_t n, int32_t* counts, hipStream_t stream);
 
 // SDDMM runs a plan's split part from this feature width on (narrower rows measured faster
 // unsplit).

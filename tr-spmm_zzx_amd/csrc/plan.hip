@@ -1104,9 +1104,11 @@ Status residual_rows(const std::vector<int32_t>& csr_len, const std::vector<Lowe
 }
 
 // Hot-row staging of an uploaded plan whose entry arrays (task kernel column ids) are
-// d.col[0, total): count the gathers of each column on the device, choose the hot columns on the
-// host (most gathered first, ties by column), renumber their entries ~rank into a copy of the
-// column ids (the plain ids stay for the window kernel and for widths that do not stage).
+// d.col[0, total): count the gathers of each column on the device (the residual entries of
+// MFMA-window rows excluded: the window kernel gathers those through the plain ids), choose the hot
+// columns on the host (most gathered first, ties by column), renumber their entries ~rank into a
+// copy of the column ids (the plain ids stay for the window kernel and for widths that do not
+// stage).
 Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   trs::DevicePlan& d = P->dp;
   if (opt.hot_rows < 0 || total <= 0 || d.n <= 0) return Status{};
@@ -1127,8 +1129,11 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   std::vector<int32_t> cnt((size_t)n);
   if (hipMemset(counts, 0, (size_t)n * 4) != hipSuccess ||
       trs::launch_count_columns(d.col, total, n, counts, nullptr) != hipSuccess ||
+      trs::launch_uncount_windows(d.mwin, d.nmwin, d.m, d.rowptr, d.col, n, counts, nullptr) != hipSuccess ||
       hipMemcpy(cnt.data(), counts, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess)
     return done(fail(TRS_EDEVICE, "hot rows: column count failed"));
+  // the task kernels' gathers: every entry but the window rows' residual entries
+  const int64_t task_entries = total - P->stats.window_csr_nnz;
   // a column gathered once gains nothing from a copy
   std::vector<int32_t> hot;
   for (int32_t c = 0; c < n; ++c)
@@ -1141,7 +1146,7 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   std::sort(hot.begin(), hot.end(), before);
   int64_t hot_entries = 0;
   for (int32_t c : hot) hot_entries += cnt[c];
-  if (hot.empty() || (opt.hot_rows == 0 && hot_entries * 10 < total * kHotMinShare10)) return done(Status{});
+  if (hot.empty() || (opt.hot_rows == 0 && hot_entries * 10 < task_entries * kHotMinShare10)) return done(Status{});
   std::vector<int32_t> rank((size_t)n, -1);
   for (size_t i = 0; i < hot.size(); ++i) rank[hot[i]] = (int32_t)i;
   // renumbered ids with the 256-byte tail every entry array has (staged streams read whole
@@ -1645,11 +1650,18 @@ int report(const Status& s) {
   return s.code;
 }
 
-trs_plan_options resolve(const trs_plan_options* o) {
-  trs_plan_options r;
+// The caller's options, or the defaults for NULL.  A struct_size other than this library's means
+// the caller was compiled against another trspmm.h: only that first field is read, and the call
+// fails.
+Status resolve(const trs_plan_options* o, trs_plan_options& r, const char* where) {
   trs_plan_options_default(&r);
-  if (o) r = *o;
-  return r;
+  if (!o) return Status{};
+  if (o->struct_size != (int32_t)sizeof(trs_plan_options))
+    return fail(TRS_EINVAL, std::string(where) + ": trs_plan_options.struct_size is " + std::to_string(o->struct_size) +
+                                ", this library's is " + std::to_string(sizeof(trs_plan_options)) +
+                                " (initialise the options with trs_plan_options_default of the same trspmm.h)");
+  r = *o;
+  return Status{};
 }
 
 bool bad_dims(int32_t m, int32_t n) { return m < 0 || n < 0; }
@@ -1660,6 +1672,7 @@ extern "C" {
 
 void trs_plan_options_default(trs_plan_options* o) {
   if (!o) return;
+  o->struct_size = (int32_t)sizeof(trs_plan_options);
   o->mfma_tc = 1;
   o->mfma_sptc = 1;
   o->sptc_min_fill = 0.25f;
@@ -1680,6 +1693,8 @@ void trs_plan_options_default(trs_plan_options* o) {
 
 const char* trs_last_error(void) { return g_error.c_str(); }
 
+int32_t trs_abi_version(void) { return TRSPMM_ABI_VERSION; }
+
 int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
   if (!f || !out) return report(fail(TRS_EINVAL, "trs_plan_create: NULL argument"));
   *out = nullptr;
@@ -1687,7 +1702,8 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
   if (!f->canonical)
     return report(fail(TRS_ENOTCANON, "trs_plan_create: input rows were not strictly increasing; the format "
                                       "arrays cannot describe duplicate or unsorted entries"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create"); !rs.ok()) return report(rs);
   if (!o.host_lowering && !f->csr_rowptr.empty()) {
     // device lowering: the tiles from the format, the residual from its input CSR
     Lowering D;
@@ -1713,7 +1729,8 @@ int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_p
   if (bad_dims(m, n)) return report(fail(TRS_EINVAL, "trs_plan_create_sddmm: negative m or n"));
   if (!f->canonical)
     return report(fail(TRS_ENOTCANON, "trs_plan_create_sddmm: input rows were not strictly increasing"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create_sddmm"); !rs.ok()) return report(rs);
   if (!o.host_lowering && !f->csr_rowptr.empty()) {
     Lowering D;
     D.m = m;
@@ -1734,7 +1751,8 @@ int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_option
   if (!a || !out) return report(fail(TRS_EINVAL, "trs_plan_create_parallel: NULL argument"));
   *out = nullptr;
   if (bad_dims(a->m, a->n)) return report(fail(TRS_EINVAL, "negative m or n"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create_parallel"); !rs.ok()) return report(rs);
   // structural checks (mGCN_online.cpp:858-932)
   if (a->n_t_row_offset < 1 || a->n_t_row_offset - 1 > a->n_t_window_row || a->n_t_binary < 2 * (a->n_t_block_offset - 1))
     return report(fail(TRS_EINVAL, "TC arrays have inconsistent sizes"));
@@ -1779,7 +1797,8 @@ int trs_plan_create_sptc(const int32_t* s_column, const float* s_value, const in
   if (s_offsets && !s_window)
     for (int64_t w = 0; w + 1 < n_s_offsets; ++w)
       if (s_offsets[w + 1] < s_offsets[w]) return report(fail(TRS_EINVAL, "s_offsets must be non-decreasing"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create_sptc"); !rs.ok()) return report(rs);
   Lowering L;
   L.m = m;
   L.n = n;
@@ -1795,7 +1814,8 @@ int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_p
   *out = nullptr;
   if (bad_dims(m, n) || window <= 0 || window > 16 || n_wto < 2 || !s_window_tile_offset)
     return report(fail(TRS_EINVAL, "trs_plan_create_sptc_packed: bad arguments"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create_sptc_packed"); !rs.ok()) return report(rs);
   Lowering L;
   L.m = m;
   L.n = n;
@@ -1814,7 +1834,8 @@ int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_
     if (rowptr[r + 1] < rowptr[r]) return report(fail(TRS_EINVAL, "rowptr must be non-decreasing"));
   const int64_t nnz = rowptr[m];
   if (nnz > 0 && (!col || !val)) return report(fail(TRS_EINVAL, "trs_plan_create_csr: NULL col/val"));
-  const trs_plan_options o = resolve(opt);
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, "trs_plan_create_csr"); !rs.ok()) return report(rs);
   Lowering L;
   L.m = m;
   L.n = n;
@@ -1827,7 +1848,11 @@ int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_
   return report(finalize_sddmm(L, o, true, out));
 }
 
-int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s) {
+int trs_plan_stats_get(const trs_plan* p, trs_plan_stats* s, int64_t stats_bytes) {
+  if (stats_bytes != (int64_t)sizeof(trs_plan_stats))
+    return report(fail(TRS_EINVAL, "trs_plan_stats_get: stats_bytes is " + std::to_string(stats_bytes) +
+                                       ", this library's trs_plan_stats has " + std::to_string(sizeof(trs_plan_stats)) +
+                                       " bytes"));
   if (!p || !s) return report(fail(TRS_EINVAL, "trs_plan_stats_get: NULL argument"));
   *s = p->stats;
   return TRS_OK;

@@ -35,6 +35,7 @@
 #include <cstdio>
 #include <cstring>
 #include <queue>
+#include <string>
 #include <vector>
 
 #include <omp.h>
@@ -490,10 +491,30 @@ std::vector<std::vector<int32_t>> groups_of(const std::vector<int32_t>& roots) {
 
 }  // namespace
 
+extern "C" void trs_reorder_params_default(trs_reorder_params* p);
+
+namespace {
+// The caller's parameters, or the defaults for NULL.  A struct_size other than this library's
+// means the caller was compiled against another trspmm.h: only that first field is read.
+bool take_params(const trs_reorder_params* params, trs_reorder_params& prm, const char* where) {
+  trs_reorder_params_default(&prm);
+  if (!params) return true;
+  if (params->struct_size != (int32_t)sizeof(trs_reorder_params)) {
+    trs::set_error(std::string(where) + ": trs_reorder_params.struct_size is " + std::to_string(params->struct_size) +
+                   ", this library's is " + std::to_string(sizeof(trs_reorder_params)) +
+                   " (initialise the parameters with trs_reorder_params_default of the same trspmm.h)");
+    return false;
+  }
+  prm = *params;
+  return true;
+}
+}  // namespace
+
 extern "C" {
 
 void trs_reorder_params_default(trs_reorder_params* p) {
   if (!p) return;
+  p->struct_size = (int32_t)sizeof(trs_reorder_params);
   p->thres = 16;
   p->cluster_thres = 128;
   p->num_perm = 128;
@@ -521,8 +542,7 @@ int trs_lsh_bands(float threshold, int32_t num_perm, int32_t* bands, int32_t* ro
 int trs_minhash_signatures(const int64_t* off, const int32_t* elems, int32_t nsets, const trs_reorder_params* params,
                            int32_t count, uint32_t* sig) {
   trs_reorder_params prm;
-  trs_reorder_params_default(&prm);
-  if (params) prm = *params;
+  if (!take_params(params, prm, "trs_minhash_signatures")) return TRS_EINVAL;
   if (nsets < 0 || count < 1 || count > 1024 || !sig || (nsets > 0 && !off) || (prm.minhash != 0 && prm.minhash != 1)) {
     trs::set_error("trs_minhash_signatures: bad arguments (count in 1..1024, minhash 0 or 1)");
     return TRS_EINVAL;
@@ -557,8 +577,7 @@ int trs_minhash_signatures(const int64_t* off, const int32_t* elems, int32_t nse
 int trs_tca_reorder(const int32_t* rowptr, const int32_t* col, int32_t rows, int64_t nnz, int32_t ncols,
                     const trs_reorder_params* params, int32_t* order) {
   trs_reorder_params prm;
-  trs_reorder_params_default(&prm);
-  if (params) prm = *params;
+  if (!take_params(params, prm, "trs_tca_reorder")) return TRS_EINVAL;
   if (rows < 0 || nnz < 0 || ncols < 0 || !order || (rows > 0 && !rowptr) || (nnz > 0 && !col)) {
     trs::set_error("trs_tca_reorder: bad arguments");
     return TRS_EINVAL;

@@ -21,14 +21,14 @@ c_pp = ctypes.POINTER(ctypes.c_void_p)
 
 
 class BuildParams(ctypes.Structure):
-    _fields_ = [("part_size_t", c_i32), ("part_size_c", c_i32), ("short_size", c_i32), ("density", c_i32),
+    _fields_ = [("struct_size", c_i32), ("part_size_t", c_i32), ("part_size_c", c_i32), ("short_size", c_i32), ("density", c_i32),
                 ("window", c_i32), ("wide", c_i32), ("tc_min_util", c_f32), ("sptc_min_util", c_f32),
                 ("sptc_threshold", c_i32), ("skip_tc", c_i32), ("sptc_unit_min_nnz", c_i32),
                 ("num_threads", c_i32)]
 
 
 class PlanOptions(ctypes.Structure):
-    _fields_ = [("mfma_tc", c_i32), ("mfma_sptc", c_i32), ("sptc_min_fill", c_f32), ("task_nnz", c_i32),
+    _fields_ = [("struct_size", c_i32), ("mfma_tc", c_i32), ("mfma_sptc", c_i32), ("sptc_min_fill", c_f32), ("task_nnz", c_i32),
                 ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
                 ("xcd_run", c_i32), ("sddmm_unroll", c_i32), ("stage", c_i32),
                 ("occupancy", c_i32), ("xcd_split", c_i32), ("host_lowering", c_i32),
@@ -43,7 +43,7 @@ class PlanStats(ctypes.Structure):
 
 
 class ReorderParams(ctypes.Structure):
-    _fields_ = [("thres", c_i32), ("cluster_thres", c_i32), ("num_perm", c_i32), ("lsh_threshold", ctypes.c_float),
+    _fields_ = [("struct_size", c_i32), ("thres", c_i32), ("cluster_thres", c_i32), ("num_perm", c_i32), ("lsh_threshold", ctypes.c_float),
                 ("bucket_span", c_i32), ("num_threads", c_i32), ("exhaustive", c_i32), ("align_window", c_i32),
                 ("seed", ctypes.c_uint64), ("minhash", c_i32)]
 
@@ -82,7 +82,7 @@ PROTOTYPES = {
                                             ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_csr": (c_i32, [c_p, c_p, c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_sddmm": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
-    "trs_plan_stats_get": (c_i32, [c_p, ctypes.POINTER(PlanStats)]),
+    "trs_plan_stats_get": (c_i32, [c_p, ctypes.POINTER(PlanStats), c_i64]),
     "trs_plan_free": (None, [c_p]),
     "trs_spmm_workspace_bytes": (c_i64, [c_p, c_i32]),
     "trs_spmm_f16": (c_i32, [c_p, c_p, c_i64, c_i32, c_p, c_i64, c_p, c_i64, c_p]),
@@ -97,6 +97,7 @@ PROTOTYPES = {
     "trs_sddmm_f16_kernel_ms": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_i32, c_p, c_p, c_i64, c_p, c_i32,
                                         ctypes.POINTER(c_f32)]),
     "trs_last_error": (ctypes.c_char_p, []),
+    "trs_abi_version": (c_i32, []),
 }
 
 _lib = None

@@ -297,7 +297,7 @@ class Plan:
 
     def stats(self) -> dict:
         s = nat.PlanStats()
-        nat.check(nat.lib().trs_plan_stats_get(self._h, ctypes.byref(s)), "trs_plan_stats_get")
+        nat.check(nat.lib().trs_plan_stats_get(self._h, ctypes.byref(s), ctypes.sizeof(s)), "trs_plan_stats_get")
         return {k: int(getattr(s, k)) for k, _ in nat.PlanStats._fields_}
 
     def workspace_bytes(self, K: int) -> int:
