@@ -228,7 +228,8 @@ def bench_sddmm(args, workload, g, K):
     torch.cuda.synchronize()
     t1 = time.time()
     plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                 feature_lanes=args.feature_lanes, hot_rows=args.hot_rows)
+                                 feature_lanes=args.feature_lanes, hot_rows=args.hot_rows,
+                                 split_dispatch=int(args.split_dispatch), sddmm_unroll=args.sddmm_unroll)
     st = plan.stats()
     pre = {"build_s": round(fmt.elapsed, 3), "plan_s": round(time.time() - t1, 3),
            "plan_lowering": "device" if st["device_lowered"] else "host"}
@@ -349,6 +350,10 @@ def main():
     ap.add_argument("--hot-rows", type=int, default=None,
                     help="plan option hot_rows (B / Y rows of the most gathered columns staged per call; -1 off; "
                          "default: the library's)")
+    ap.add_argument("--sddmm-unroll", type=int, default=None,
+                    help="plan option sddmm_unroll (SDDMM entries in flight per lane group: 4 or 8)")
+    ap.add_argument("--split-dispatch", action="store_true",
+                    help="plan option split_dispatch: the XCD split part as its own launch (per-part profiles)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -390,7 +395,7 @@ def main():
     t1 = time.time()
     plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
                                    window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes,
-                                   hot_rows=args.hot_rows)
+                                   hot_rows=args.hot_rows, split_dispatch=int(args.split_dispatch))
     pre["plan_s"] = round(time.time() - t1, 3)
     pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
     if "reorder_s" in pre:

@@ -87,6 +87,27 @@ int32_t trs_format_rows(const trs_format* f);
 int32_t trs_format_canonical(const trs_format* f); /* 1 if every row had increasing columns */
 void trs_format_free(trs_format* f);
 
+/* Format builder on the GPU.  No reference counterpart: it builds what
+ * Libra5BlockOnline.block_sptc_2to4_online returns (the reference builds on one CPU thread,
+ * TR-source/Block/block_online.cpp:545-871) from a CSR in device memory (rowptr[rows + 1], col[nnz],
+ * val[nnz] float32, on the current device) into device memory, on `stream` (NULL: the default
+ * stream); the call returns when the format is complete.  The 32 slots are bit-exact with
+ * trs_build_online's on the same input and parameters.  Canonical input only (strictly increasing
+ * columns in every row: TRS_ENOTCANON otherwise) and windows of at most 16 rows (TRS_EINVAL
+ * otherwise); trs_build_online builds every other input.  The result keeps its own copy of the
+ * input CSR, so the caller's buffers may be freed after the call. */
+typedef struct trs_dformat trs_dformat;
+int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const float* val, int32_t rows,
+                            int64_t nnz, const trs_build_params* params, void* stream, trs_dformat** out);
+/* Device pointer and element count of slot 0..31 (element types as for trs_format_slot). */
+int trs_dformat_slot(const trs_dformat* f, int32_t slot, const void** data, int64_t* numel);
+/* A host trs_format with the same 32 slots (and the input CSR, for device plan lowering). */
+int trs_dformat_download(const trs_dformat* f, trs_format** out);
+double trs_dformat_elapsed(const trs_dformat* f);   /* build wall time, s */
+int32_t trs_dformat_rows(const trs_dformat* f);
+int32_t trs_dformat_window(const trs_dformat* f);
+void trs_dformat_free(trs_dformat* f);
+
 /* Format cache.  No counterpart in the reference, which rebuilds the format on every run
  * (spmm/tr_csr_fp16/mdataset2_online.py:100-113); for callers that reuse a graph across runs.
  * One versioned little-endian file holds all 32 slots, rows, window, the canonical flag and the
@@ -243,6 +264,9 @@ typedef struct trs_plan_options {
                              (16384 rows, at most n / 16, and only when they take >= 30% of the
                              gathers), > 0 = that many rows, -1 = off.  Never for plans with more
                              than 4 columns per entry (n > 4 nnz) */
+  int32_t split_dispatch; /* 0: the residual task kernels run the main part and the XCD split part
+                             in one launch (default, faster); 1: as two launches, main part first,
+                             so that a profiler attributes time and counters to each part */
 } trs_plan_options;
 
 void trs_plan_options_default(trs_plan_options* o);

@@ -30,7 +30,7 @@ def test_every_declared_symbol_is_exported():
 
 def test_struct_layouts_match_header():
     assert ctypes.sizeof(nat.BuildParams) == 13 * 4
-    assert ctypes.sizeof(nat.PlanOptions) == 17 * 4
+    assert ctypes.sizeof(nat.PlanOptions) == 18 * 4
     assert ctypes.sizeof(nat.PlanStats) == 16 * 8
     assert ctypes.sizeof(nat.ReorderParams) == 56
     assert ctypes.sizeof(nat.MatchStats) == 16 * 8

@@ -6,7 +6,7 @@ buffer in the workspace and the task kernels gather them there.  Only where a ro
 changes, so the outputs are bitwise equal to the unstaged plan's (same products, same order), and
 both match the float64 oracle.  Covered: the automatic choice (R-MAT stages, a block graph does
 not), widths that stage (128, 136, 256, 200) and ones that do not (64, 120), the split part (XCD
-sub-rows) and MFMA windows beside staged rows, workspace sizes, a workspace too small, the
+sub-rows) and MFMA windows beside staged rows (whose residual entries the choice does not count), workspace sizes, a workspace too small, the
 entry point without workspace (trs_sddmm_f16) and the one that allocates nothing.
 """
 import ctypes
@@ -92,15 +92,48 @@ def test_spmm_staged_equals_unstaged(K):
     assert np.max(np.abs(C8 - C)) <= 1e-5 * max(1.0, float(np.max(np.abs(C))))
 
 
-@pytest.mark.parametrize("H", [1, 100, 5000])
+def sbm_with_plain_rows():
+    """Block graph (every window owns MFMA tiles) followed by 1024 rows of 8 random columns from a
+    pool of 4096: count-1 columns, whose 2:4 tiles are too sparse for MFMA, so those rows run on the
+    task kernel, each pool column gathered about twice there."""
+    if "sbm_plain" not in _cache:
+        g = graphs.sbm(communities=4096, seed=5, val_seed=5)
+        rng = np.random.default_rng(5)
+        extra = np.sort(np.stack([rng.choice(4096, size=8, replace=False) for _ in range(1024)]), axis=1)
+        col = np.concatenate([g.col[: g.rowptr[g.m]], (extra * 7 % g.n).astype(np.int32).ravel()])
+        order = np.concatenate([np.arange(g.rowptr[g.m]),
+                                g.rowptr[g.m] + np.argsort(col[g.rowptr[g.m]:].reshape(1024, 8), axis=1,
+                                                           kind="stable").ravel()
+                                + np.repeat(np.arange(1024) * 8, 8)])
+        col = col[order].astype(np.int32)
+        val = np.concatenate([g.val[: g.rowptr[g.m]],
+                              rng.uniform(0, 1, 8192).astype(np.float16).astype(np.float32)])
+        rowptr = np.concatenate([g.rowptr[: g.m + 1], g.rowptr[g.m] + 8 * np.arange(1, 1025)]).astype(np.int32)
+        _cache["sbm_plain"] = graphs.Graph("sbm4096_plain", g.m + 1024, g.n, rowptr, col, val)
+    return _cache["sbm_plain"]
+
+
+def test_hot_rows_ignore_window_rows():
+    """Staging counts only the task kernels' gathers: on a block graph whose residual entries all
+    sit in MFMA-window rows (read through the plain ids by the window kernel) even an explicit row
+    count stages nothing."""
+    g = graphs.sbm(communities=4096, seed=5, val_seed=5)
+    p = trspmm.Plan.from_format(trspmm.build_format(g.rowptr, g.col, g.val), g.m, g.n, hot_rows=100)
+    s = p.stats()
+    assert s["mfma_windows"] > 0 and s["window_csr_nnz"] == s["csr_nnz"], s   # every residual entry in a window
+    assert s["hot_rows"] == 0 and s["hot_entries"] == 0, s
+
+
+@pytest.mark.parametrize("H", [1, 100, 2000])
 def test_spmm_explicit_hot_rows_with_windows(H):
     """An explicit row count stages whatever the share; a graph with MFMA windows keeps their B
     reads on the plain column ids."""
-    g = graphs.sbm(communities=4096, seed=5, val_seed=5)
+    g = sbm_with_plain_rows()
     f = trspmm.build_format(g.rowptr, g.col, g.val)
     p = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=H)
     s = p.stats()
     assert s["hot_rows"] == H and s["mfma_windows"] > 0, s
+    assert 0 < s["hot_entries"] <= 8192, s
     Bh = graphs.dense_operand(g.n, 128, seed=7)
     C = run_spmm(p, Bh)
     assert np.array_equal(C, run_spmm(trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1), Bh))

@@ -1298,7 +1298,16 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
 #undef TRS_TASKS
 #undef TRS_TASKS_NT
   };
-  run_tasks(tp, xv);
+  if (tp.split_dispatch && tp.ntasks > 0 && xv.ntasks > 0) {
+    // profiling layout: the main part, then the split part, as launches of their own
+    DevicePlan main_only = xv, split_only = tp;
+    main_only.ntasks = 0;
+    split_only.ntasks = 0;
+    run_tasks(tp, main_only);
+    run_tasks(split_only, xv);
+  } else {
+    run_tasks(tp, xv);
+  }
   if (ev) (void)hipEventRecord(ev[1], s);
   if (p.nmwin > 0) {
     const int kc16 = ((K + 15) / 16) * 16;
@@ -1419,7 +1428,15 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       DevicePlan v = split_view(pp);
       v.res_pos = nullptr;
       v.out_off = (int32_t)p.nnz_csr;
-      run_tasks(pp, out, v, xbuf);
+      if (p.split_dispatch && pp.ntasks > 0) {
+        // profiling layout: main part and split part as launches of their own
+        DevicePlan vnone = v;
+        vnone.ntasks = 0;
+        run_tasks(pp, out, vnone, xbuf);
+        run_tasks(none, out, v, xbuf);
+      } else {
+        run_tasks(pp, out, v, xbuf);
+      }
     } else if (p.x_ntasks > 0 && (K < kSddmmSplitMinK || hot_on)) {
       // written in place, the split part's scattered outputs cost more than it saves below
       // kSddmmSplitMinK, and wherever hot rows are staged (R-MAT 2^20 K = 128 0.777 vs 0.773 ms
@@ -1428,6 +1445,11 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
       v.tasks = p.full_tasks;
       v.ntasks = p.nfull_tasks;
       run_tasks(v, out, none, out);
+    } else if (p.split_dispatch && p.x_ntasks > 0 && pp.ntasks > 0) {
+      DevicePlan v = split_view(pp), vnone = split_view(pp);
+      vnone.ntasks = 0;
+      run_tasks(pp, out, vnone, out);
+      run_tasks(none, out, v, out);
     } else {
       run_tasks(pp, out, p.x_ntasks > 0 ? split_view(pp) : none, out);
     }

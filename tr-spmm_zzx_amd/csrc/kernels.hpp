@@ -74,6 +74,7 @@ struct DevicePlan {
   int32_t stage = 0;           // staged task streams: 0 automatic, -1 never
   int32_t occupancy = 0;       // waves per SIMD for the residual task kernel: 2..8, 0 automatic, -1 uncapped
   int32_t sddmm_unroll = 0;    // SDDMM residual entries in flight per lane group (4, 8; 0 automatic)
+  int32_t split_dispatch = 0;  // 1: main part and XCD split part as two launches (profiling)
   int32_t task_nnz = 0;        // entries per packed residual task
   int32_t task_max = 0;        // most entries of any residual task (packed rows or a piece)
   const int32_t* slot_list = nullptr;   // partial slots of the split rows, in summation order

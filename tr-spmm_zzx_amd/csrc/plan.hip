@@ -1380,6 +1380,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     d.nquads = Q.count;
   }
   d.feature_lanes = opt.feature_lanes;
+  d.split_dispatch = opt.split_dispatch != 0;
   // default: non-temporal C stores only (measured +3%); non-temporal A loads cost ~60% because
   // consecutive iterations re-read the same col/val cache lines
   d.task_nnz = T.task_nnz;
@@ -1596,6 +1597,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.tile_pos = with_pos ? reinterpret_cast<const int32_t*>(base + o_tpos) : nullptr;
   d.ntiles = with_pos ? (int32_t)L.tiles.size() : 0;
   d.feature_lanes = opt.feature_lanes;
+  d.split_dispatch = opt.split_dispatch != 0;
   d.streaming = opt.streaming < 0 ? 2 : (opt.streaming & 2);
   d.xcd_run = opt.xcd_run > 0 ? opt.xcd_run : 16;
   d.sddmm_unroll = opt.sddmm_unroll == 4 || opt.sddmm_unroll == 8 ? opt.sddmm_unroll : 0;
@@ -1689,6 +1691,7 @@ void trs_plan_options_default(trs_plan_options* o) {
   o->host_lowering = 0;
   o->sptc_sparse = 1;
   o->hot_rows = 0;
+  o->split_dispatch = 0;
 }
 
 const char* trs_last_error(void) { return g_error.c_str(); }

@@ -32,7 +32,7 @@ class PlanOptions(ctypes.Structure):
                 ("piece_nnz", c_i32), ("feature_lanes", c_i32), ("streaming", c_i32), ("window_row_cap", c_i32),
                 ("xcd_run", c_i32), ("sddmm_unroll", c_i32), ("stage", c_i32),
                 ("occupancy", c_i32), ("xcd_split", c_i32), ("host_lowering", c_i32),
-                ("sptc_sparse", c_i32), ("hot_rows", c_i32)]
+                ("sptc_sparse", c_i32), ("hot_rows", c_i32), ("split_dispatch", c_i32)]
 
 
 class PlanStats(ctypes.Structure):
@@ -72,6 +72,13 @@ PROTOTYPES = {
     "trs_lsh_bands": (c_i32, [ctypes.c_float, c_i32, ctypes.POINTER(c_i32), ctypes.POINTER(c_i32)]),
     "trs_minhash_signatures": (c_i32, [c_p, c_p, c_i32, ctypes.POINTER(ReorderParams), c_i32, c_p]),
     "trs_format_read": (c_i32, [ctypes.c_char_p, c_pp]),
+    "trs_build_online_device": (c_i32, [c_p, c_p, c_p, c_i32, c_i64, ctypes.POINTER(BuildParams), c_p, c_pp]),
+    "trs_dformat_slot": (c_i32, [c_p, c_i32, c_pp, ctypes.POINTER(c_i64)]),
+    "trs_dformat_download": (c_i32, [c_p, c_pp]),
+    "trs_dformat_elapsed": (c_f64, [c_p]),
+    "trs_dformat_rows": (c_i32, [c_p]),
+    "trs_dformat_window": (c_i32, [c_p]),
+    "trs_dformat_free": (None, [c_p]),
     "trs_match_2to4": (c_i32, [c_p, c_p, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(MatchStats)]),
     "trs_plan_options_default": (None, [ctypes.POINTER(PlanOptions)]),
     "trs_plan_create": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),

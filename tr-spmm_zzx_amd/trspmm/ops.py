@@ -142,6 +142,77 @@ def build_format(rowptr, col, val, part_t: int = 32, part_c: int = 32, short_siz
     return Format(h.value)
 
 
+class DeviceFormat:
+    """Output of the GPU format builder (owns a C ``trs_dformat``): the same 32 slots as
+    :class:`Format`, in device memory.  :meth:`download` returns the host :class:`Format`."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            try:
+                nat.lib().trs_dformat_free(h)
+            except (TypeError, AttributeError):
+                pass
+            self._h = ctypes.c_void_p(0)
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    @property
+    def elapsed(self) -> float:
+        return float(nat.lib().trs_dformat_elapsed(self._h))
+
+    @property
+    def rows(self) -> int:
+        return int(nat.lib().trs_dformat_rows(self._h))
+
+    @property
+    def window(self) -> int:
+        return int(nat.lib().trs_dformat_window(self._h))
+
+    def slot_info(self, i: int) -> tuple:
+        """(device pointer, element count) of slot i."""
+        data = ctypes.c_void_p()
+        n = ctypes.c_int64()
+        nat.check(nat.lib().trs_dformat_slot(self._h, i, ctypes.byref(data), ctypes.byref(n)), "trs_dformat_slot")
+        return data.value or 0, n.value
+
+    def download(self) -> Format:
+        h = ctypes.c_void_p()
+        nat.check(nat.lib().trs_dformat_download(self._h, ctypes.byref(h)), "trs_dformat_download")
+        return Format(h.value)
+
+
+def build_format_device(rowptr: torch.Tensor, col: torch.Tensor, val: torch.Tensor, part_t: int = 32,
+                        part_c: int = 32, short_size: int = 3, density: int = 8, window: int = 16,
+                        wide: int = 16, tc_min_util: float = 0.0, skip_tc: Optional[bool] = None,
+                        unit_min_nnz: Optional[int] = None, stream=None) -> DeviceFormat:
+    """The format builder on the GPU (trs_build_online_device): int32 rowptr / col and float32 val
+    on the current device, canonical rows, window <= 16.  Bit-exact with :func:`build_format`."""
+    for name, t, dt in (("rowptr", rowptr, torch.int32), ("col", col, torch.int32), ("val", val, torch.float32)):
+        if not (t.is_cuda and t.dtype == dt and t.dim() == 1 and t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous 1-D {dt} tensor on the GPU")
+        _on_current_device(name, t)
+    if col.shape[0] != val.shape[0]:
+        raise ValueError("col and val must have the same length")
+    p = nat.BuildParams()
+    nat.lib().trs_build_params_default(ctypes.byref(p))
+    p.part_size_t, p.part_size_c, p.short_size, p.density = part_t, part_c, short_size, density
+    p.window, p.wide, p.tc_min_util = window, wide, tc_min_util
+    p.skip_tc = -1 if skip_tc is None else int(bool(skip_tc))
+    p.sptc_unit_min_nnz = -1 if unit_min_nnz is None else int(unit_min_nnz)
+    h = ctypes.c_void_p()
+    nat.check(nat.lib().trs_build_online_device(rowptr.data_ptr(), col.data_ptr() if col.numel() else None,
+                                                val.data_ptr() if val.numel() else None, rowptr.shape[0] - 1,
+                                                col.shape[0], ctypes.byref(p), _stream_ptr(stream),
+                                                ctypes.byref(h)), "trs_build_online_device")
+    return DeviceFormat(h.value)
+
+
 def _env_setting(name: str) -> str:
     v = os.environ.get(name)
     return "unset" if v is None else v
@@ -233,14 +304,16 @@ class Plan:
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
                     stage: Optional[int] = None, occupancy: Optional[int] = None,
                     xcd_split: Optional[int] = None, host_lowering: bool = False,
-                    sptc_sparse: bool = True, hot_rows: Optional[int] = None) -> "Plan":
+                    sptc_sparse: bool = True, hot_rows: Optional[int] = None,
+                    split_dispatch: Optional[int] = None) -> "Plan":
         """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default).  host_lowering=True builds the
         residual on the host even when the format holds its input CSR (the plan is the same);
         sptc_sparse=False runs 2:4 tiles on the dense MFMA with zero fill instead of the sparse one."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, streaming=streaming, window_row_cap=window_row_cap,
-                     xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split, hot_rows=hot_rows)
+                     xcd_run=xcd_run, stage=stage, occupancy=occupancy, xcd_split=xcd_split, hot_rows=hot_rows,
+                     split_dispatch=split_dispatch)
         o.host_lowering = int(bool(host_lowering))
         o.sptc_sparse = int(bool(sptc_sparse))
         h = ctypes.c_void_p()
@@ -253,14 +326,15 @@ class Plan:
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
                   streaming: Optional[int] = None, xcd_split: Optional[int] = None,
-                  host_lowering: bool = False, hot_rows: Optional[int] = None) -> "Plan":
+                  host_lowering: bool = False, hot_rows: Optional[int] = None,
+                  split_dispatch: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
         residual outputs with non-temporal stores.  host_lowering=True builds the residual on the
         host even when the format holds its input CSR (the plan is the same)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
-                     streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows)
+                     streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows, split_dispatch=split_dispatch)
         o.host_lowering = int(bool(host_lowering))
         h = ctypes.c_void_p()
         nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
