@@ -215,4 +215,48 @@ int64_t check_batched_sort(const int64_t* sizes, int32_t nsizes, int32_t alphabe
   return bad;
 }
 
+// tied_final_offset against the restated loop on ranges of equal elements (every comparison
+// false), for lengths 0..Lmax and depth limits from the least that lasts to 3 more; returns the
+// number of (L, d) that differ, or -1 if tied_depth_ok disagrees with the loop reaching a heap sort.
+int64_t check_tied(int64_t Lmax) {
+  struct Never {
+    bool operator()(int32_t, int32_t) const { return false; }
+  };
+  int64_t bad = 0;
+  for (int64_t L = 0; L <= Lmax; L += (L < 3000 ? 1 : 997)) {
+    int dmin = 0;
+    while (!trs::isort::tied_depth_ok(L, dmin)) ++dmin;
+    for (int d = (dmin > 0 ? dmin - 1 : 0); d <= dmin + 3; ++d) {
+      std::vector<int32_t> a((size_t)L);
+      std::iota(a.begin(), a.end(), 0);
+      Never cmp;
+      // does the loop heap-sort at depth d? walk its ranges as killer_reaches_heap_sort does
+      bool heap = false;
+      {
+        struct Range { int64_t f, l; int d; };
+        std::vector<Range> st{{0, L, d}};
+        std::vector<int32_t> b = a;
+        while (!st.empty() && !heap) {
+          Range r = st.back();
+          st.pop_back();
+          while (r.l - r.f > trs::isort::kThreshold) {
+            if (r.d == 0) { heap = true; break; }
+            --r.d;
+            int32_t* cut = trs::isort::partition_pivot(b.data() + r.f, b.data() + r.l, cmp);
+            st.push_back({cut - b.data(), r.l, r.d});
+            r.l = cut - b.data();
+          }
+        }
+      }
+      if (heap == trs::isort::tied_depth_ok(L, d)) return -1;
+      if (heap) continue;
+      if (L > 0) trs::isort::introsort_loop(a.data(), a.data() + L, d, cmp);
+      if (L > 0) trs::isort::final_insertion_sort(a.data(), a.data() + L, cmp);
+      for (int64_t o = 0; o < L; ++o)
+        if (a[(size_t)trs::isort::tied_final_offset(L, o)] != o) { ++bad; break; }
+    }
+  }
+  return bad;
+}
+
 }  // extern "C"

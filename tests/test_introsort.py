@@ -4,7 +4,8 @@ sorted by a key with heavy ties (the builder's nnz-descending unit order, block_
 up to n = 100k; McIlroy-adversary inputs that push it into the heap-sort fallback; and the
 list form of the partition step and its batched form (the one a wave runs, a batch of stops per
 lane) against the scanning form, and whole sorts built on the batched step (leaves finished by a
-stable insertion sort, as the final insertion sort leaves them) against std::sort.  No GPU:
+stable insertion sort, as the final insertion sort leaves them) against std::sort, and the closed
+form for ranges of equal keys against the loop.  No GPU:
 tests/native/introsort_check.cpp is compiled with g++ for the host."""
 import ctypes
 import os
@@ -40,6 +41,8 @@ def chk(tmp_path_factory):
     lib.check_batched_sort.argtypes = [i64p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint64,
                                        ctypes.c_int32]
     lib.check_batched_sort.restype = ctypes.c_int64
+    lib.check_tied.argtypes = [ctypes.c_int64]
+    lib.check_tied.restype = ctypes.c_int64
     return lib
 
 
@@ -96,3 +99,11 @@ def test_sort_on_batched_partitions_equals_std_sort(chk, lanes, alphabet):
     assert chk.check_batched_sort(p, k, alphabet, 20, 21 + alphabet + lanes, lanes) == 0
     keep, p, k = _sizes(4096, 20000, 70000)
     assert chk.check_batched_sort(p, k, alphabet, 2, 23 + alphabet + lanes, lanes) == 0
+
+
+def test_tied_range_closed_form(chk):
+    """The device builder's shortcut for ranges of equal keys (isort::tied_final_offset: each
+    element's final offset from its own, no partition passes) against the restated loop and final
+    insertion sort, for every length up to 3000 and sampled ones to 100k, at depth limits from one
+    too few (the heap-sort case, which tied_depth_ok must recognise) to three more than needed."""
+    assert chk.check_tied(100000) == 0

@@ -63,11 +63,12 @@ namespace {
 
 using u64 = unsigned long long;
 
-constexpr int kSmallU = 2048;       // windows with more distinct columns take the workgroup kernel
+constexpr int kSmallU = 8192;       // windows with more distinct columns take the workgroup kernel
 constexpr int kBlockWaves = 8;      // waves of that kernel
 constexpr int kLdsUnits = 65536;    // most units whose order it keeps in LDS (16-bit indices; the
                                     // device's LDS per workgroup may allow fewer)
 constexpr int kMaxKey = 32;         // unit nnz <= 2 * window
+constexpr int kGreedySpan = 1024;   // indices ahead of the matching's low end one round looks at
 
 // ---- wave helpers --------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
@@ -355,16 +356,24 @@ __device__ int count_sort(const uint32_t* umask, int U, Sel sel, int32_t* out, W
   const int l = lane_id(), w = (int)(threadIdx.x >> 6);
   const int chunks = (U + 63) >> 6;
   const int c0 = (int)((int64_t)chunks * w / NW), c1 = (int)((int64_t)chunks * (w + 1) / NW);
-  int myhist = 0;   // lane v: this wave's columns of count v
-  for (int ch = c0; ch < c1; ++ch) {
+  // the count of this lane's column in chunk ch (0: not selected); four chunks' loads in flight
+  auto count_of = [&](int ch) {
     const int u = ch * 64 + l;
-    const int c = u < U && sel(u) ? popc32(umask[u]) : 0;
-    u64 rem = ballot(c != 0);
-    while (rem) {
-      const int v = rdlane(c, __builtin_ctzll(rem));
-      const u64 b = ballot(c == v);
-      if (l == v) myhist += __popcll(b);
-      rem &= ~b;
+    return ch < c1 && u < U && sel(u) ? popc32(umask[u]) : 0;
+  };
+  int myhist = 0;   // lane v: this wave's columns of count v
+  for (int ch0 = c0; ch0 < c1; ch0 += 4) {
+    int cs[4];
+    for (int i = 0; i < 4; ++i) cs[i] = count_of(ch0 + i);
+    for (int i = 0; i < 4; ++i) {
+      const int c = cs[i];
+      u64 rem = ballot(c != 0);
+      while (rem) {
+        const int v = rdlane(c, __builtin_ctzll(rem));
+        const u64 b = ballot(c == v);
+        if (l == v) myhist += __popcll(b);
+        rem &= ~b;
+      }
     }
   }
   if (l <= 16) sh.hist[w][l] = myhist;
@@ -379,17 +388,21 @@ __device__ int count_sort(const uint32_t* umask, int U, Sel sel, int32_t* out, W
   }
   for (int v = 1; v <= 16; ++v)
     for (int q = 0; q < NW; ++q) total += sh.hist[q][v];
-  for (int ch = c0; ch < c1; ++ch) {
-    const int u = ch * 64 + l;
-    const int c = u < U && sel(u) ? popc32(umask[u]) : 0;
-    u64 rem = ballot(c != 0);
-    while (rem) {
-      const int v = rdlane(c, __builtin_ctzll(rem));
-      const u64 b = ballot(c == v);
-      const int base = rdlane(run, v);
-      if (c == v) out[base + mbcnt(b)] = u;
-      if (l == v) run += __popcll(b);
-      rem &= ~b;
+  for (int ch0 = c0; ch0 < c1; ch0 += 4) {
+    int cs[4];
+    for (int i = 0; i < 4; ++i) cs[i] = count_of(ch0 + i);
+    for (int i = 0; i < 4; ++i) {
+      const int c = cs[i];
+      const int u = (ch0 + i) * 64 + l;
+      u64 rem = ballot(c != 0);
+      while (rem) {
+        const int v = rdlane(c, __builtin_ctzll(rem));
+        const u64 b = ballot(c == v);
+        const int base = rdlane(run, v);
+        if (c == v) out[base + mbcnt(b)] = u;
+        if (l == v) run += __popcll(b);
+        rem &= ~b;
+      }
     }
   }
   __syncthreads();
@@ -401,7 +414,7 @@ __device__ int count_sort(const uint32_t* umask, int U, Sel sel, int32_t* out, W
 // start_of[key] and "key(x) >= pivot key" is x < end_of[key].  Returns the cut.
 template <class P>
 __device__ int wave_partition(P* perm, int s, int e, const uint8_t* unnz, const WinShared& sh, int* Lbuf, int* Rbuf,
-                              uint32_t* err) {
+                              uint32_t* err, int* pivot_key) {
   const int l = lane_id();
   const int mid = s + (e - s) / 2;
   const int ia = s + 1, ib = mid, ic = e - 1;
@@ -417,6 +430,7 @@ __device__ int wave_partition(P* perm, int s, int e, const uint8_t* unnz, const 
   }
   wave_sync();
   const int pk = unnz[vt];
+  *pivot_key = pk;
   const int lo = sh.start_of[pk], hi = sh.end_of[pk];
   int aL = s + 1, aR = e - 1, nL = 0, nR = 0, rprev = e;
   for (int guard = 0; guard <= (e - s) / 64 + 2; ++guard) {
@@ -485,52 +499,91 @@ __device__ void lane0_heap_sort(P* perm, int s, int e, const uint8_t* unnz) {
   wave_sync();
 }
 
-// Leaves (ranges the loop left at <= 16 elements) each get the stable insertion sort the final
-// insertion sort amounts to there (isort::final_insertion_sort never moves an element across a
-// partition cut); threads [t0, t0 + nt) of the window share the positions.
+// A range whose units all have one nnz, finished by one wave: every unit goes to the offset
+// isort::tied_final_offset gives (the loop's steps on equal elements), through tmp.
+template <class P>
+__device__ void wave_tied(P* perm, int s, int L, int32_t* tmp) {
+  const int l = lane_id();
+  for (int o = l; o < L; o += 64) tmp[s + (int)trs::isort::tied_final_offset(L, o)] = (int32_t)perm[s + o];
+  __threadfence_block();
+  wave_sync();
+  for (int o = l; o < L; o += 64) perm[s + o] = (P)tmp[s + o];
+  __threadfence_block();
+  wave_sync();
+}
+
+// Depth limit and the range's key bounds in one int: keys are at most kMaxKey (6 bits).
+__device__ __forceinline__ int pack_range(int d, int kmin, int kmax) { return d | (kmin << 8) | (kmax << 16); }
+
+// Leaves (ranges the loop left at <= 16 elements) each get the stable sort the final insertion
+// sort amounts to there (isort::final_insertion_sort never moves an element across a partition
+// cut): a leaf's units and keys are loaded into registers at once and sorted by odd-even
+// transposition, which swaps only strictly inverted neighbours (so equal keys keep their order).
+// Threads [t0, t0 + nt) of the window share the positions.
 template <class P>
 __device__ void sort_leaves(P* perm, int n, const uint8_t* leaf, const uint8_t* unnz, int t0, int nt) {
   for (int i = (int)threadIdx.x - t0; i < n; i += nt) {
     const int len = leaf[i];
     if (len < 2) continue;
-    for (int j = i + 1; j < i + len; ++j) {
-      const P v = perm[j];
-      const int kv = unnz[v];
-      int k = j;
-      while (k > i && kv > (int)unnz[perm[k - 1]]) {
-        perm[k] = perm[k - 1];
-        --k;
+    int v[16], k[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = j < len ? (int)perm[i + j] : 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) k[j] = j < len ? (int)unnz[v[j]] : -1;   // -1: past the leaf, stays last
+#pragma unroll
+    for (int round = 0; round < 16; ++round) {
+#pragma unroll
+      for (int j = round & 1; j + 1 < 16; j += 2) {
+        if (k[j + 1] > k[j]) {   // descending keys
+          const int tv = v[j], tk = k[j];
+          v[j] = v[j + 1];
+          k[j] = k[j + 1];
+          v[j + 1] = tv;
+          k[j + 1] = tk;
+        }
       }
-      perm[k] = v;
     }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < len) perm[i + j] = (P)v[j];
   }
 }
 
-// std::sort's loop over perm[0, n) by one wave, ranges on a stack held one per lane.
+// std::sort's loop over perm[0, n) by one wave, ranges on a stack held one per lane.  Each range
+// carries bounds on its keys (the left part of a partition holds keys >= the pivot's, the right
+// part keys <= it); a range whose bounds meet is finished by the closed form for equal keys.
 template <class P>
 __device__ void wave_introsort(P* perm, int n, const uint8_t* unnz, uint8_t* leaf, const WinShared& sh, int* Lbuf,
-                               int* Rbuf, uint32_t* err) {
+                               int* Rbuf, int32_t* tmp, uint32_t* err) {
   const int l = lane_id();
   int sf = 0, sl = 0, sd = 0, top = 0;
   if (l == 0) {
     sf = 0;
     sl = n;
-    sd = 2 * trs::isort::lg(n);
+    sd = pack_range(2 * trs::isort::lg(n), unnz[n - 1], unnz[0]);
   }
   top = 1;
   while (top > 0) {
     --top;
     const int f = rdlane(sf, top);
-    int last = rdlane(sl, top), d = rdlane(sd, top);
-    bool heap = false;
+    int last = rdlane(sl, top);
+    const int packed = rdlane(sd, top);
+    int d = packed & 0xff, kmin = (packed >> 8) & 0xff, kmax = packed >> 16;
+    bool done = false;
     while (last - f > 16) {
+      if (kmin == kmax && trs::isort::tied_depth_ok(last - f, d)) {
+        wave_tied(perm, f, last - f, tmp);
+        done = true;
+        break;
+      }
       if (d == 0) {
         lane0_heap_sort(perm, f, last, unnz);
-        heap = true;
+        done = true;
         break;
       }
       --d;
-      const int cut = wave_partition(perm, f, last, unnz, sh, Lbuf, Rbuf, err);
+      int pk = 0;
+      const int cut = wave_partition(perm, f, last, unnz, sh, Lbuf, Rbuf, err, &pk);
       if (top >= 63) {   // the stack never holds more than the depth limit (<= 2 log2 n) ranges
         atomicOr(err, kErrInternal);
         return;
@@ -538,65 +591,122 @@ __device__ void wave_introsort(P* perm, int n, const uint8_t* unnz, uint8_t* lea
       if (l == top) {
         sf = cut;
         sl = last;
-        sd = d;
+        sd = pack_range(d, kmin, pk);
       }
       ++top;
       last = cut;
+      kmin = pk;
     }
-    if (!heap && l == 0) leaf[f] = (uint8_t)(last - f);
+    if (!done && l == 0) leaf[f] = (uint8_t)(last - f);
     wave_sync();
   }
 }
 
 // Greedy matching over the sorted order (one wave): the next unit of the order not yet taken
-// pairs with the lowest-index unit not yet taken.  perm / pos are the order and its inverse; the
-// pairs go to px[k], py[k]; returns their number, *left = the unit left unmatched (-1: none).
-template <class P, class Q>
-__device__ int wave_greedy(const P* perm, const Q* pos, int n, int32_t* px, int32_t* py, int* left) {
+// pairs with the lowest-index unit not yet taken.  Two walks: the order's (a position in perm) and
+// the low end's (an index b); `taken` (n bits, zeroed by the caller) records the units the order's
+// walk took, which the low end skips, and the order skips units below b (the low end took them).
+//
+// 64 steps at a time: the order's next 64 candidates (positions >= a whose unit is >= b) and the
+// low end's next 64 (untaken indices in [b, b + kGreedySpan)) are paired lane by lane, as if neither
+// walk took a candidate of the other.  Step j is exact until one of them did: the order's
+// candidate x_j is not above the low end's previous pick y_{j-1} (the low end took it first), or
+// the low end's y_j is some x_i, i <= j (the order took it first).  Steps before the first such j
+// are committed together; a first step that fails is taken on its own, exactly.  Pairs go to
+// px[k], py[k]; returns their number, *left = the unit left unmatched (-1: none).  buf: 512 ints
+// of LDS for this wave.
+template <class P>
+__device__ int wave_greedy(const P* perm, uint32_t* taken, int n, int32_t* px, int32_t* py, int* left, int* buf) {
   const int l = lane_id();
+  int* Ab = buf;          // order candidates: positions
+  int* Bb = buf + 128;    // low-end candidates: indices
+  // for index b + d (d < kGreedySpan): the step whose order candidate it is (64: none)
+  uint8_t* stepA = reinterpret_cast<uint8_t*>(buf + 256);
   int a = 0, b = 0, np = 0, lf = -1;
-  int ca_base = -128, cb_base = -128, ca = 0, cb = 0;
-  int hx = 0, hy = 0;
-  while (true) {
-    // units the order reaches after the low end took them (index < b) are skipped
-    while (a < n) {
-      if (a >= ca_base + 64) {
-        ca_base = a & ~63;
-        ca = ca_base + l < n ? (int)perm[ca_base + l] : 0x7fffffff;
-      }
-      if (rdlane(ca, a - ca_base) >= b) break;
-      ++a;
+  for (int guard = 0; guard <= 2 * n + 2; ++guard) {
+    int nA = 0, aEnd = a;
+    for (; nA < 64 && aEnd < n; aEnd += 64) {
+      const int p = aEnd + l;
+      const bool f = p < n && (int)perm[p] >= b;
+      const u64 m = ballot(f);
+      const int r = nA + mbcnt(m);
+      if (f && r < 64) Ab[r] = p;
+      nA += __popcll(m);
     }
-    if (a >= n) break;
-    const int x = rdlane(ca, a - ca_base);
-    ++a;
-    // units the order already took (position < a) are skipped at the low end
-    while (b < n) {
-      if (b >= cb_base + 64) {
-        cb_base = b & ~63;
-        cb = cb_base + l < n ? (int)pos[cb_base + l] : 0x7fffffff;
-      }
-      if (rdlane(cb, b - cb_base) >= a) break;
-      ++b;
+    if (nA == 0) break;   // no unit left for the order
+    // positions the scan passed without a candidate stay passed (b only grows): after the
+    // committed steps the walk resumes at the next collected candidate, or where the scan ended
+    const bool scan_whole = nA <= 64;
+    if (nA > 64) nA = 64;
+    // the low end's candidates: the next 64 untaken indices from b, below b + kGreedySpan
+    const int lim = min(n, b + kGreedySpan);
+    int nB = 0, bEnd = b;
+    for (; nB < 64 && bEnd < lim; bEnd += 64) {
+      const int q = bEnd + l;
+      const bool f = q < lim && !((taken[q >> 5] >> (q & 31)) & 1u);
+      const u64 m = ballot(f);
+      const int r = nB + mbcnt(m);
+      if (f && r < 64) Bb[r] = q;
+      nB += __popcll(m);
     }
-    if (b >= n) {
-      lf = x;
+    if (nB > 64) nB = 64;
+    for (int i = l; i < kGreedySpan / 4; i += 64) reinterpret_cast<uint32_t*>(stepA)[i] = 0x40404040u;
+    wave_sync();
+    const int pj = l < nA ? Ab[l] : 0;
+    const int xj = l < nA ? (int)perm[pj] : 0x7fffffff;
+    const int yj = l < nB ? Bb[l] : 0x7fffffff;
+    if (l < nA && xj - b < kGreedySpan) stepA[xj - b] = (uint8_t)l;
+    wave_sync();
+    // y_j taken by the order at step i <= j
+    const bool hit = l < nB && (int)stepA[yj - b] <= l;
+    int yprev = __shfl_up(yj, 1);
+    if (l == 0) yprev = b - 1;
+    const bool stop = l >= nA || l >= nB || xj <= yprev || hit;
+    const u64 sm = ballot(stop);
+    const int js = sm ? (int)__builtin_ctzll(sm) : 64;
+    if (js > 0) {
+      if (l < js) {
+        px[np + l] = xj;
+        py[np + l] = yj;
+        atomicOr(&taken[xj >> 5], 1u << (xj & 31));
+      }
+      np += js;
+      a = js < nA ? rdlane(pj, js) : scan_whole ? min(aEnd, n) : rdlane(pj, js - 1) + 1;
+      // indices the low end's scan passed were taken: it resumes at its next candidate
+      b = js < nB ? rdlane(yj, js) : rdlane(yj, js - 1) + 1;
+      wave_sync();
+      continue;
+    }
+    if (nB == 0 && lim < n) {   // every index in [b, lim) is taken: the low end passes them
+      b = lim;
+      continue;
+    }
+    // one exact step: the order takes x_0; the low end takes the first untaken index after it
+    const int x0 = rdlane(xj, 0);
+    a = rdlane(pj, 0) + 1;
+    if (l == 0) atomicOr(&taken[x0 >> 5], 1u << (x0 & 31));
+    wave_sync();
+    int y = -1;
+    for (int q0 = b; q0 < n; q0 += 64) {
+      const int q = q0 + l;
+      const bool f = q < n && !((taken[q >> 5] >> (q & 31)) & 1u);
+      const u64 m = ballot(f);
+      if (m) {
+        y = q0 + (int)__builtin_ctzll(m);
+        break;
+      }
+    }
+    if (y < 0) {
+      lf = x0;
       break;
     }
-    const int y = b++;
-    if (l == (np & 63)) {
-      hx = x;
-      hy = y;
+    if (l == 0) {
+      px[np] = x0;
+      py[np] = y;
     }
     ++np;
-    if ((np & 63) == 0) {
-      px[np - 64 + l] = hx;
-      py[np - 64 + l] = hy;
-    }
-  }
-  if (l < (np & 63)) {
-    px[(np & ~63) + l] = hx;
-    py[(np & ~63) + l] = hy;
+    b = y + 1;
+    wave_sync();
   }
   *left = lf;
   return np;
@@ -617,9 +727,9 @@ __device__ __forceinline__ void sort4(int32_t* m) {   // ascending, -1 entries l
 
 // Stage B for window w with NW waves.  Small windows keep the unit order in LDS (P = uint16_t,
 // arrays given), large ones in LDS too up to kLdsUnits units, else in global memory.
-template <int NW, class P, class Q>
-__device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t* unnz_w, uint8_t* leaf_w,
-                            int32_t* px, int32_t* py, WinShared& sh, int* LRbuf) {
+template <int NW, class P>
+__device__ void plan_window(const Build& B, int32_t w, P* perm, uint32_t* taken, uint8_t* unnz_w, uint8_t* leaf_w,
+                            int32_t* px, int32_t* py, WinShared& sh, int* LRbuf, int* gbuf, int32_t* tmp) {
   const int tid = threadIdx.x, l = lane_id(), wv = tid >> 6;
   constexpr int NT = NW * 64;
   const int32_t ub = B.ubase[w], U = B.ubase[w + 1] - ub;
@@ -706,7 +816,7 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
   int* Rbuf = Lbuf + 128;
   if (n > 16) {
     if constexpr (NW == 1) {
-      wave_introsort(perm, n, unnz_w, leaf_w, sh, Lbuf, Rbuf, B.err);
+      wave_introsort(perm, n, unnz_w, leaf_w, sh, Lbuf, Rbuf, tmp, B.err);
     } else {
       // level by level: each wave takes ranges of the current list, children go to the next
       int* lists = B.ranges + ub;   // two lists of (first, last, depth), (U / 2) ints each
@@ -715,7 +825,7 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
       if (tid == 0) {
         lists[0] = 0;
         lists[1] = n;
-        lists[2] = 2 * trs::isort::lg(n);
+        lists[2] = pack_range(2 * trs::isort::lg(n), unnz_w[n - 1], unnz_w[0]);
         sh.cnt[0] = 1;
         sh.cnt[1] = 0;
       }
@@ -726,14 +836,21 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
         int* lc = lists + cur * (U / 2);
         int* ln = lists + (cur ^ 1) * (U / 2);
         for (int r = wv; r < ncur; r += NW) {
-          const int f = lc[3 * r], last = lc[3 * r + 1], d = lc[3 * r + 2];
+          const int f = lc[3 * r], last = lc[3 * r + 1], packed = lc[3 * r + 2];
+          const int d = packed & 0xff, kmin = (packed >> 8) & 0xff, kmax = packed >> 16;
+          if (kmin == kmax && trs::isort::tied_depth_ok(last - f, d)) {
+            wave_tied(perm, f, last - f, tmp);
+            continue;
+          }
           if (d == 0) {
             lane0_heap_sort(perm, f, last, unnz_w);
             continue;
           }
-          const int cut = wave_partition(perm, f, last, unnz_w, sh, Lbuf, Rbuf, B.err);
+          int pk = 0;
+          const int cut = wave_partition(perm, f, last, unnz_w, sh, Lbuf, Rbuf, B.err, &pk);
           if (l == 0) {
             const int cf[2] = {f, cut}, cl[2] = {cut, last};
+            const int cp[2] = {pack_range(d - 1, pk, kmax), pack_range(d - 1, kmin, pk)};
             for (int h = 0; h < 2; ++h) {
               const int len = cl[h] - cf[h];
               if (len > 16) {
@@ -741,7 +858,7 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
                 if (at < cap) {
                   ln[3 * at] = cf[h];
                   ln[3 * at + 1] = cl[h];
-                  ln[3 * at + 2] = d - 1;
+                  ln[3 * at + 2] = cp[h];
                 } else {
                   atomicOr(B.err, kErrInternal);
                 }
@@ -764,13 +881,13 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
     sort_leaves(perm, n, leaf_w, unnz_w, 0, NT);
     __syncthreads();
   }
-  for (int i = tid; i < n; i += NT) pos[perm[i]] = (Q)i;
+  for (int i = tid; i < n / 32 + 2; i += NT) taken[i] = 0u;
   __syncthreads();
 
   // greedy matching (block_online.cpp:365-391)
   if (wv == 0) {
     int left = -1;
-    const int np = wave_greedy(perm, pos, n, px, py, &left);
+    const int np = wave_greedy(perm, taken, n, px, py, &left, gbuf);
     if (l == 0) {
       sh.misc[2] = np;
       sh.misc[3] = left;
@@ -817,28 +934,32 @@ __device__ void plan_window(const Build& B, int32_t w, P* perm, Q* pos, uint8_t*
   }
 }
 
-// Windows of at most kSmallU distinct columns, one wave each (workgroups of one wave).
+// Windows of at most kSmallU distinct columns, one wave each (workgroups of one wave); matched
+// pairs go to the window's part of B.pairs.
 __global__ __launch_bounds__(64) void k_plan_small(Build B) {
   const int32_t w = blockIdx.x;
-  const int32_t U = B.ubase[w + 1] - B.ubase[w];
+  const int32_t ub = B.ubase[w], U = B.ubase[w + 1] - ub;
   if (U > kSmallU) return;
   __shared__ uint16_t perm[kSmallU / 2 + 1];
-  __shared__ uint16_t pos[kSmallU / 2 + 1];
   __shared__ uint8_t unnz[kSmallU / 2 + 1];
   __shared__ uint8_t leaf[kSmallU / 2 + 1];
-  __shared__ int32_t px[kSmallU / 4 + 1];
-  __shared__ int32_t py[kSmallU / 4 + 1];
+  __shared__ uint32_t taken[kSmallU / 64 + 2];
   __shared__ int LR[256];
+  __shared__ int GB[512];
   __shared__ WinShared sh;
-  plan_window<1>(B, w, perm, pos, unnz, leaf, px, py, sh, LR);
+  int32_t* px = B.pairs + ub;
+  int32_t* py = px + (U + 3) / 4 + 1;
+  plan_window<1>(B, w, perm, taken, unnz, leaf, px, py, sh, LR, GB, B.gperm + ub);
 }
 
-// The other windows, a workgroup of kBlockWaves waves each (window list `big`): unit order in LDS
-// (16-bit indices) for windows of at most kLdsUnits units ...
+// The other windows, a workgroup of kBlockWaves waves each, largest first (window list `big`):
+// unit order (16-bit indices) and taken bits in LDS for windows of at most B.lds_units units ...
 __global__ __launch_bounds__(kBlockWaves * 64) void k_plan_large(Build B, const int32_t* big, int32_t nbig) {
-  extern __shared__ uint16_t lds_perm[];   // kLdsUnits entries
+  extern __shared__ uint16_t lds_perm[];   // B.lds_units entries, then the taken bits
   __shared__ int LR[kBlockWaves * 256];
+  __shared__ int GB[512];
   __shared__ WinShared sh;
+  uint32_t* taken = reinterpret_cast<uint32_t*>(lds_perm + ((B.lds_units + 1) & ~1));
   for (int32_t i = blockIdx.x; i < nbig; i += gridDim.x) {
     const int32_t w = big[i];
     const int32_t ub = B.ubase[w];
@@ -846,7 +967,7 @@ __global__ __launch_bounds__(kBlockWaves * 64) void k_plan_large(Build B, const 
     // units <= ceil(U / 2); the global arrays are sized by U at the window's offset
     int32_t* px = B.pairs + ub;
     int32_t* py = px + (U + 3) / 4 + 1;
-    plan_window<kBlockWaves>(B, w, lds_perm, B.gpos + ub, B.unnz + ub, B.leaf + ub, px, py, sh, LR);
+    plan_window<kBlockWaves>(B, w, lds_perm, taken, B.unnz + ub, B.leaf + ub, px, py, sh, LR, GB, B.gperm + ub);
     __syncthreads();
   }
 }
@@ -854,6 +975,7 @@ __global__ __launch_bounds__(kBlockWaves * 64) void k_plan_large(Build B, const 
 // ... and in global memory for larger ones.
 __global__ __launch_bounds__(kBlockWaves * 64) void k_plan_huge(Build B, const int32_t* big, int32_t nbig) {
   __shared__ int LR[kBlockWaves * 256];
+  __shared__ int GB[512];
   __shared__ WinShared sh;
   for (int32_t i = blockIdx.x; i < nbig; i += gridDim.x) {
     const int32_t w = big[i];
@@ -861,20 +983,22 @@ __global__ __launch_bounds__(kBlockWaves * 64) void k_plan_huge(Build B, const i
     const int32_t U = B.ubase[w + 1] - ub;
     int32_t* px = B.pairs + ub;
     int32_t* py = px + (U + 3) / 4 + 1;
-    plan_window<kBlockWaves>(B, w, B.gperm + ub, B.gpos + ub, B.unnz + ub, B.leaf + ub, px, py, sh, LR);
+    plan_window<kBlockWaves>(B, w, B.gperm + ub, reinterpret_cast<uint32_t*>(B.gpos + ub), B.unnz + ub,
+                             B.leaf + ub, px, py, sh, LR, GB, B.gpos + ub);
     __syncthreads();
   }
 }
 
-// Windows for the workgroup kernels: big[0, nbig[0]) for k_plan_large, from the end of `big`
-// backwards nbig[1] windows for k_plan_huge.
+// Windows for the workgroup kernels: (distinct columns, window) of each, big[0, nbig) (the host
+// orders them, largest first, and splits them between the two kernels).
 __global__ __launch_bounds__(256) void k_list_large(Build B, int32_t* big, int32_t* nbig) {
   const int32_t w = (int32_t)(blockIdx.x * 256 + threadIdx.x);
   if (w >= B.nwin) return;
   const int32_t U = B.ubase[w + 1] - B.ubase[w];
   if (U <= kSmallU) return;
-  if ((U + 1) / 2 <= B.lds_units) big[atomicAdd(&nbig[0], 1)] = w;
-  else big[B.nwin - 1 - atomicAdd(&nbig[1], 1)] = w;
+  const int32_t i = atomicAdd(nbig, 1);
+  big[2 * i] = U;
+  big[2 * i + 1] = w;
 }
 
 // ---- stage C: counts -----------------------------------------------------------------------
@@ -934,117 +1058,130 @@ __global__ __launch_bounds__(256) void k_row_counts(Build B) {
 }
 
 // ---- stage D: the arrays -------------------------------------------------------------------
-// TC sub-blocks and parts of one window per wave (block_online.cpp:444-540, :736-776).
-__global__ __launch_bounds__(64) void k_fill_tc(Build B, Out O) {
-  const int32_t w = blockIdx.x;
-  const int l = lane_id();
-  const WinOut o = B.win[w];
-  const int32_t pb = B.wparts[w], sb = B.wsubs[w];
-  if (l == 0 && w == 0) {
+// The window holding item i of a per-window numbering with exclusive bases base[0..nwin]
+// (base[nwin] = the total; i below it).
+__device__ __forceinline__ int32_t window_of(const int32_t* base, int32_t nwin, int32_t i) {
+  int32_t lo = 0, hi = nwin;   // base[lo] <= i < base[hi]
+  while (hi - lo > 1) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (base[mid] <= i) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Per window: TC parts (block_online.cpp:502-537), group and tile offsets (:736-776, :840).
+__global__ __launch_bounds__(256) void k_fill_windows(Build B, Out O) {
+  const int32_t w = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (w == 0) {
     O.t_rowoff[0] = 0;
-    O.t_blockoff[0] = 0;
+    O.s_offsets[B.nwin] = B.wgroups[B.nwin];
+    O.win_tile_off[B.nwin] = B.wtiles[B.nwin];
   }
+  if (w >= B.nwin) return;
+  O.s_offsets[w] = B.wgroups[w];
+  O.win_tile_off[w] = B.wtiles[w];
+  const WinOut o = B.win[w];
   if (o.nsub == 0) return;
+  const int32_t pb = B.wparts[w], sb = B.wsubs[w];
   const int32_t nparts = B.wparts[w + 1] - pb;
-  for (int q = l; q < nparts; q += 64) {
+  for (int q = 0; q < nparts; ++q) {
     O.t_rowoff[pb + q + 1] = sb + min((q + 1) * B.part_t, o.nsub);
-    O.t_winrow[pb + q] = w * 16;   // block_online.cpp:494
+    O.t_winrow[pb + q] = w * 16;   // block_online.cpp:494 (window id * 16 for every window size)
     O.t_atomic[pb + q] = nparts == 1 ? (o.nres > 0 ? 1 : 0) : 1;
-  }
-  const int32_t ub = B.ubase[w];
-  const int32_t* tcl = B.tcl + ub + 8 * w;
-  int32_t vrun = B.wtvals[w];
-  for (int s0 = 0; s0 < o.nsub; s0 += 64) {
-    const int s = s0 + l;
-    uint64_t lo = 0, hi = 0;
-    if (s < o.nsub) {
-      for (int k = 0; k < 8; ++k) {
-        const int32_t u = tcl[s * 8 + k];
-        O.t_col[(int64_t)(sb + s) * 8 + k] = u >= 0 ? B.ucol[ub + u] : -1;
-        if (u < 0) continue;
-        uint32_t m = B.umask[ub + u];
-        while (m) {
-          const int lr = __builtin_ctz(m);
-          m &= m - 1;
-          if (lr < 8) lo |= 1ull << (lr * 8 + k);
-          else hi |= 1ull << ((lr - 8) * 8 + k);
-        }
-      }
-      O.t_bin[2 * (int64_t)(sb + s)] = (int64_t)lo;
-      O.t_bin[2 * (int64_t)(sb + s) + 1] = (int64_t)hi;
-    }
-    const int cnt = __popcll(lo) + __popcll(hi);
-    int x = cnt;   // inclusive prefix over the lanes
-    for (int d = 1; d < 64; d <<= 1) {
-      const int y = __shfl_up(x, d);
-      if (l >= d) x += y;
-    }
-    const int32_t vb = vrun + x - cnt;
-    if (s < o.nsub) {
-      O.t_blockoff[sb + s + 1] = vb + cnt;
-      // values in ascending bit order: rows 0-7 (lo), then rows 8-15 (hi); row-major, columns
-      // ascending -- the CSR order of block_online.cpp:474-492
-      int idx = 0;
-      for (int half = 0; half < 2; ++half) {
-        uint64_t bits = half ? hi : lo;
-        while (bits) {
-          const int b = __builtin_ctzll(bits);
-          bits &= bits - 1;
-          const int lr = half * 8 + b / 8, k = b % 8;
-          O.t_val[vb + idx++] = B.val[entry_of(B, ub + tcl[s * 8 + k], lr)];
-        }
-      }
-    }
-    vrun += rdlane(x, 63);
   }
 }
 
-// 2:4 groups of one window per wave: columns, masks, the first two values of each row, spill
-// flags for the rest (block_online.cpp:629-703).
-__global__ __launch_bounds__(64) void k_fill_groups(Build B, Out O) {
-  const int32_t w = blockIdx.x;
-  const int l = lane_id();
-  const int ws = B.ws;
-  const int32_t gb = B.wgroups[w], G = B.wgroups[w + 1] - gb;
-  if (l == 0) O.s_offsets[w] = gb;
-  if (l == 0 && w == B.nwin - 1) O.s_offsets[B.nwin] = B.wgroups[B.nwin];
+// Values per TC sub-block (their prefix sums are t_blockNew_offset).
+__global__ __launch_bounds__(256) void k_tc_counts(Build B, int32_t nsubs, int32_t* __restrict__ cnt) {
+  const int32_t s = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (s >= nsubs) return;
+  const int32_t w = window_of(B.wsubs, B.nwin, s);
   const int32_t ub = B.ubase[w];
-  const int32_t* gl = B.gl + ub + 4 * w;
-  for (int g = l; g < G; g += 64) {
-    const int64_t gg = gb + g;
-    int32_t m[4];
-    uint32_t mk[4];
-    for (int q = 0; q < 4; ++q) {
-      m[q] = gl[4 * g + q];
-      O.s_col[gg * 4 + q] = m[q] >= 0 ? B.ucol[ub + m[q]] : -1;
-      mk[q] = m[q] >= 0 ? B.umask[ub + m[q]] : 0u;
-    }
-    O.s_win[gg] = w;
-    for (int lr = 0; lr < ws; ++lr) {
-      const int64_t mi = gg * ws + lr;
-      uint32_t present = 0;
-      int kept = 0;
-      float v[2] = {0.f, 0.f};
-      int p[2] = {-1, -1};
-      for (int q = 0; q < 4; ++q) {
-        if (!((mk[q] >> lr) & 1u)) continue;
-        present |= 1u << q;
-        const int32_t e = entry_of(B, ub + m[q], lr);
-        if (kept < 2) {
-          v[kept] = B.val[e];
-          p[kept] = q;
-        } else {
-          B.spill[e] = 1;
-        }
-        ++kept;
-      }
-      O.s_mask[mi] = (uint8_t)present;
-      O.s_val[mi * 2] = v[0];
-      O.s_val[mi * 2 + 1] = v[1];
-      O.s_pos[mi * 2] = (int8_t)p[0];
-      O.s_pos[mi * 2 + 1] = (int8_t)p[1];
+  const int32_t* tcl = B.tcl + ub + 8 * w + (int64_t)(s - B.wsubs[w]) * 8;
+  int c = 0;
+  for (int k = 0; k < 8; ++k)
+    if (tcl[k] >= 0) c += popc32(B.umask[ub + tcl[k]]);
+  cnt[s] = c;
+}
+
+// TC sub-block s: columns, row bits and values (block_online.cpp:444-540): bit (row % 8) * 8 + k
+// of t_binary[2s] (rows 0-7) or [2s + 1] (rows 8-15); values in ascending bit order, which is the
+// rows' CSR order.
+__global__ __launch_bounds__(256) void k_fill_tc(Build B, Out O, int32_t nsubs) {
+  const int32_t s = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (s >= nsubs) return;
+  const int32_t w = window_of(B.wsubs, B.nwin, s);
+  const int32_t ub = B.ubase[w];
+  const int32_t* tcl = B.tcl + ub + 8 * w + (int64_t)(s - B.wsubs[w]) * 8;
+  uint64_t lo = 0, hi = 0;
+  int32_t u[8];
+  for (int k = 0; k < 8; ++k) {
+    u[k] = tcl[k];
+    O.t_col[(int64_t)s * 8 + k] = u[k] >= 0 ? B.ucol[ub + u[k]] : -1;
+    if (u[k] < 0) continue;
+    uint32_t m = B.umask[ub + u[k]];
+    while (m) {
+      const int lr = __builtin_ctz(m);
+      m &= m - 1;
+      if (lr < 8) lo |= 1ull << (lr * 8 + k);
+      else hi |= 1ull << ((lr - 8) * 8 + k);
     }
   }
+  O.t_bin[2 * (int64_t)s] = (int64_t)lo;
+  O.t_bin[2 * (int64_t)s + 1] = (int64_t)hi;
+  int32_t vi = O.t_blockoff[s];
+  for (int half = 0; half < 2; ++half) {
+    uint64_t bits = half ? hi : lo;
+    while (bits) {
+      const int b = __builtin_ctzll(bits);
+      bits &= bits - 1;
+      const int lr = half * 8 + b / 8, k = b % 8;
+      O.t_val[vi++] = B.val[entry_of(B, ub + u[k], lr)];
+    }
+  }
+}
+
+// Window of each 2:4 group (s_window, block_online.cpp:664).
+__global__ __launch_bounds__(256) void k_group_windows(Build B, Out O, int32_t ngroups) {
+  const int32_t g = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (g < ngroups) O.s_win[g] = window_of(B.wgroups, B.nwin, g);
+}
+
+// Group g, local row lr: columns (lr = 0), the row's mask, its first two values and their
+// positions; the row's further values are spilled (block_online.cpp:629-703).
+__global__ __launch_bounds__(256) void k_fill_groups(Build B, Out O, int64_t items) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= items) return;
+  const int ws = B.ws;
+  const int32_t g = (int32_t)(t / ws);
+  const int lr = (int)(t - (int64_t)g * ws);
+  const int32_t w = O.s_win[g];
+  const int32_t ub = B.ubase[w];
+  const int32_t* gl = B.gl + ub + 4 * w + (int64_t)(g - B.wgroups[w]) * 4;
+  uint32_t present = 0;
+  int kept = 0;
+  float v[2] = {0.f, 0.f};
+  int p[2] = {-1, -1};
+  for (int q = 0; q < 4; ++q) {
+    const int32_t m = gl[q];
+    if (lr == 0) O.s_col[(int64_t)g * 4 + q] = m >= 0 ? B.ucol[ub + m] : -1;
+    if (m < 0 || !((B.umask[ub + m] >> lr) & 1u)) continue;
+    present |= 1u << q;
+    const int32_t e = entry_of(B, ub + m, lr);
+    if (kept < 2) {
+      v[kept] = B.val[e];
+      p[kept] = q;
+    } else {
+      B.spill[e] = 1;
+    }
+    ++kept;
+  }
+  O.s_mask[t] = (uint8_t)present;
+  O.s_val[2 * t] = v[0];
+  O.s_val[2 * t + 1] = v[1];
+  O.s_pos[2 * t] = (int8_t)p[0];
+  O.s_pos[2 * t + 1] = (int8_t)p[1];
 }
 
 // block_online.cpp:190-210 (g window-local, gend the window's group count)
@@ -1078,38 +1215,34 @@ __device__ __forceinline__ void load_chunk(const Out& O, int64_t gb, int g, int 
 
 __device__ __forceinline__ uint16_t f16_bits(float f) { return trs::half_bits_of(__float_as_uint(f)); }
 
-// Tiles of 4 groups (block_online.cpp:796-841), one window per wave, a tile per lane.
-__global__ __launch_bounds__(64) void k_fill_tiles(Build B, Out O) {
-  const int32_t w = blockIdx.x;
-  const int l = lane_id();
+// Tile t: 4 groups of its window (block_online.cpp:796-841).
+__global__ __launch_bounds__(256) void k_fill_tiles(Build B, Out O, int32_t ntiles) {
+  const int32_t t = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (t >= ntiles) return;
   const int ws = B.ws;
+  const int32_t w = window_of(B.wtiles, B.nwin, t);
   const int32_t gb = B.wgroups[w], G = B.wgroups[w + 1] - gb;
-  const int32_t tb = B.wtiles[w], T = B.wtiles[w + 1] - tb;
-  if (l == 0) O.win_tile_off[w] = tb;
-  if (l == 0 && w == B.nwin - 1) O.win_tile_off[B.nwin] = B.wtiles[B.nwin];
-  for (int ti = l; ti < T; ti += 64) {
-    const int64_t t = tb + ti;
-    const int base = ti * 4;
-    O.tile_win[t] = w;
-    O.tile_group[t] = gb + base;
-    for (int k = 0; k < 16; ++k) {
-      const int g = base + k / 4;
-      O.tile_cols[t * 16 + k] = g < G ? O.s_col[(gb + g) * 4 + k % 4] : -1;
+  const int base = (t - B.wtiles[w]) * 4;
+  O.tile_win[t] = w;
+  O.tile_group[t] = gb + base;
+  for (int k = 0; k < 16; ++k) {
+    const int g = base + k / 4;
+    O.tile_cols[(int64_t)t * 16 + k] = g < G ? O.s_col[((int64_t)gb + g) * 4 + k % 4] : -1;
+  }
+  for (int rg = 0; rg < 8; ++rg) {
+    float a[16];
+    uint32_t meta = 0;
+    for (int c = 0; c < 4; ++c) {
+      int p0, p1;
+      load_chunk(O, gb, base + c, G, rg, ws, a[4 * c], a[4 * c + 1], p0, p1);
+      meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (4 * c);
+      load_chunk(O, gb, base + c, G, rg + 8, ws, a[4 * c + 2], a[4 * c + 3], p0, p1);
+      meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (16 + 4 * c);
     }
-    for (int rg = 0; rg < 8; ++rg) {
-      float a[16];
-      uint32_t meta = 0;
-      for (int c = 0; c < 4; ++c) {
-        int p0, p1;
-        load_chunk(O, gb, base + c, G, rg, ws, a[4 * c], a[4 * c + 1], p0, p1);
-        meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (4 * c);
-        load_chunk(O, gb, base + c, G, rg + 8, ws, a[4 * c + 2], a[4 * c + 3], p0, p1);
-        meta |= ((uint32_t)(p0 & 3) | ((uint32_t)(p1 & 3) << 2)) << (16 + 4 * c);
-      }
-      O.packed_meta[t * 8 + rg] = (int32_t)meta;
-      for (int j = 0; j < 8; ++j)
-        O.packed_a[(t * 8 + rg) * 8 + j] = (int32_t)((uint32_t)f16_bits(a[2 * j]) | ((uint32_t)f16_bits(a[2 * j + 1]) << 16));
-    }
+    O.packed_meta[(int64_t)t * 8 + rg] = (int32_t)meta;
+    for (int j = 0; j < 8; ++j)
+      O.packed_a[((int64_t)t * 8 + rg) * 8 + j] =
+          (int32_t)((uint32_t)f16_bits(a[2 * j]) | ((uint32_t)f16_bits(a[2 * j + 1]) << 16));
   }
 }
 
@@ -1256,7 +1389,9 @@ int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const flo
     return fail(TRS_EDEVICE, "trs_build_online_device: device attributes unavailable");
   }
   Build B;
-  B.lds_units = (int32_t)std::min<int64_t>(kLdsUnits, std::max<int64_t>(0, ((int64_t)max_lds - (int64_t)fa.sharedSizeBytes - 512) / 2));
+  // 2 bytes of order and 1 taken bit per unit
+  B.lds_units = (int32_t)std::min<int64_t>(
+      kLdsUnits, std::max<int64_t>(0, ((int64_t)max_lds - (int64_t)fa.sharedSizeBytes - 1024) * 8 / 17));
   B.rows = rows;
   B.ws = prm->window;
   B.nwin = (rows + B.ws - 1) / B.ws;
@@ -1323,7 +1458,7 @@ int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const flo
   const size_t need2 = bytes_of<int32_t>(U) * 3 + bytes_of<uint32_t>(U) + bytes_of<int32_t>(U + 1) +
                        bytes_of<int32_t>(Ue) * 2 + bytes_of<uint8_t>(U) * 2 + bytes_of<int32_t>(U) * 4 +
                        bytes_of<WinOut>(W) + bytes_of<int32_t>(W + 1) * 5 + bytes_of<int32_t>(rows + 1) * 4 +
-                       bytes_of<uint8_t>(nnz) + bytes_of<int32_t>(nnz + 1) + bytes_of<int32_t>(W + 1) +
+                       bytes_of<uint8_t>(nnz) + bytes_of<int32_t>(nnz + 1) + bytes_of<int32_t>(2 * (int64_t)W + 2) +
                        bytes_of<int32_t>(scan_scratch_ints(std::max<int64_t>(nnz, rows)) + 64);
   if (hipMalloc(&s2.p, need2) != hipSuccess) {
     (void)hipGetLastError();
@@ -1355,7 +1490,7 @@ int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const flo
   B.rse = A2.take<int32_t>(rows + 1);
   B.spill = A2.take<uint8_t>(nnz);
   B.spill_at = A2.take<int32_t>(nnz + 1);
-  int32_t* big = A2.take<int32_t>(W + 1);
+  int32_t* big = A2.take<int32_t>(2 * (int64_t)W + 2);
   int32_t* bsum2 = A2.take<int32_t>(scan_scratch_ints(std::max<int64_t>(nnz, rows)) + 64);
   int32_t* nbig_d = bsum2 + scan_scratch_ints(std::max<int64_t>(nnz, rows)) + 32;
   if (nnz > 0) hipLaunchKernelGGL(k_distinct, dim3(grid_of(nnz)), dim3(256), 0, s, B);
@@ -1364,20 +1499,38 @@ int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const flo
   if (W > 0) {
     hipLaunchKernelGGL(k_list_large, dim3(grid_of(W)), dim3(256), 0, s, B, big, nbig_d);
     hipLaunchKernelGGL(k_plan_small, dim3(W), dim3(64), 0, s, B);
-    int32_t nbig[2] = {0, 0};
-    if (hipMemcpyAsync(nbig, nbig_d, 8, hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+    int32_t nbig = 0;
+    if (hipMemcpyAsync(&nbig, nbig_d, 4, hipMemcpyDeviceToHost, s) != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
       return fail(TRS_EDEVICE, std::string("trs_build_online_device: ") + hipGetErrorString(hipGetLastError()));
-    if (nbig[0] > 0) {
-      const size_t lds = (size_t)B.lds_units * sizeof(uint16_t);
-      if (hipFuncSetAttribute((const void*)k_plan_large, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
-          hipSuccess)
-        return fail(TRS_EDEVICE, "trs_build_online_device: the window kernel cannot get its LDS");
-      hipLaunchKernelGGL(k_plan_large, dim3((unsigned)std::min(nbig[0], 1024)), dim3(kBlockWaves * 64), lds, s, B, big,
-                         nbig[0]);
+    if (nbig > 0) {
+      // largest windows first (they take longest), split between the LDS and the global-memory
+      // kernel by unit count
+      std::vector<int32_t> lst(2 * (size_t)nbig);
+      if (hipMemcpy(lst.data(), big, lst.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(TRS_EDEVICE, "trs_build_online_device: window list copy failed");
+      std::vector<std::pair<int32_t, int32_t>> order((size_t)nbig);
+      for (int32_t i = 0; i < nbig; ++i) order[i] = {lst[2 * i], lst[2 * i + 1]};
+      std::sort(order.begin(), order.end(), [](const auto& x, const auto& y) {
+        return x.first != y.first ? x.first > y.first : x.second < y.second;
+      });
+      std::vector<int32_t> in_lds, in_global;
+      for (const auto& o : order) ((o.first + 1) / 2 <= B.lds_units ? in_lds : in_global).push_back(o.second);
+      std::vector<int32_t> ids(in_lds);
+      ids.insert(ids.end(), in_global.begin(), in_global.end());
+      if (hipMemcpy(big, ids.data(), ids.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(TRS_EDEVICE, "trs_build_online_device: window list copy failed");
+      if (!in_lds.empty()) {
+        const size_t lds = (size_t)((B.lds_units + 1) & ~1) * sizeof(uint16_t) + ((size_t)B.lds_units / 32 + 2) * 4;
+        if (hipFuncSetAttribute((const void*)k_plan_large, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+            hipSuccess)
+          return fail(TRS_EDEVICE, "trs_build_online_device: the window kernel cannot get its LDS");
+        hipLaunchKernelGGL(k_plan_large, dim3((unsigned)std::min<size_t>(in_lds.size(), 1024)), dim3(kBlockWaves * 64),
+                           lds, s, B, big, (int32_t)in_lds.size());
+      }
+      if (!in_global.empty())
+        hipLaunchKernelGGL(k_plan_huge, dim3((unsigned)std::min<size_t>(in_global.size(), 1024)),
+                           dim3(kBlockWaves * 64), 0, s, B, big + in_lds.size(), (int32_t)in_global.size());
     }
-    if (nbig[1] > 0)
-      hipLaunchKernelGGL(k_plan_huge, dim3((unsigned)std::min(nbig[1], 1024)), dim3(kBlockWaves * 64), 0, s, B,
-                         big + (W - nbig[1]), nbig[1]);
     hipLaunchKernelGGL(k_window_counts, dim3(grid_of(W)), dim3(256), 0, s, B);
   }
   if (rows > 0) hipLaunchKernelGGL(k_row_counts, dim3(grid_of(rows)), dim3(256), 0, s, B);
@@ -1470,16 +1623,17 @@ int trs_build_online_device(const int32_t* rowptr, const int32_t* col, const flo
       (nnz > 0 && (hipMemcpyAsync(F->csr_col, col, (size_t)nnz * 4, hipMemcpyDeviceToDevice, s) != hipSuccess ||
                    hipMemcpyAsync(F->csr_val, val, (size_t)nnz * 4, hipMemcpyDeviceToDevice, s) != hipSuccess)))
     return fail_f(TRS_EDEVICE, "trs_build_online_device: copy of the input CSR failed");
-  if (W > 0) {
-    hipLaunchKernelGGL(k_fill_tc, dim3(W), dim3(64), 0, s, B, O);
-    hipLaunchKernelGGL(k_fill_groups, dim3(W), dim3(64), 0, s, B, O);
-    hipLaunchKernelGGL(k_fill_tiles, dim3(W), dim3(64), 0, s, B, O);
-  } else {
-    // no window: the offset arrays still hold their leading zero
-    if (hipMemsetAsync(O.t_rowoff, 0, 4, s) != hipSuccess || hipMemsetAsync(O.t_blockoff, 0, 4, s) != hipSuccess ||
-        hipMemsetAsync(O.s_offsets, 0, 4, s) != hipSuccess || hipMemsetAsync(O.win_tile_off, 0, 4, s) != hipSuccess)
-      return fail_f(TRS_EDEVICE, "hipMemsetAsync failed");
+  hipLaunchKernelGGL(k_fill_windows, dim3(grid_of((int64_t)W + 1)), dim3(256), 0, s, B, O);
+  // t_blockNew_offset: prefix sums of the sub-blocks' value counts (B.ord is free after stage B
+  // and holds U >= S_t ints)
+  if (S_t > 0) hipLaunchKernelGGL(k_tc_counts, dim3(grid_of(S_t)), dim3(256), 0, s, B, (int32_t)S_t, B.ord);
+  if (scan(B.ord, S_t, O.t_blockoff, bsum2, s) != hipSuccess) return fail_f(TRS_EDEVICE, "scan failed");
+  if (S_t > 0) hipLaunchKernelGGL(k_fill_tc, dim3(grid_of(S_t)), dim3(256), 0, s, B, O, (int32_t)S_t);
+  if (G > 0) {
+    hipLaunchKernelGGL(k_group_windows, dim3(grid_of(G)), dim3(256), 0, s, B, O, (int32_t)G);
+    hipLaunchKernelGGL(k_fill_groups, dim3(grid_of(G * ws)), dim3(256), 0, s, B, O, G * ws);
   }
+  if (T > 0) hipLaunchKernelGGL(k_fill_tiles, dim3(grid_of(T)), dim3(256), 0, s, B, O, (int32_t)T);
   hipLaunchKernelGGL(k_fill_residual, dim3(grid_of(std::max(rows, 1))), dim3(256), 0, s, B, O);
   if (scan(B.spill, nnz, B.spill_at, bsum2, s) != hipSuccess) return fail_f(TRS_EDEVICE, "scan failed");
   int32_t nsp = 0;

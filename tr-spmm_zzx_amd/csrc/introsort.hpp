@@ -254,6 +254,42 @@ TRS_HD int64_t partition_by_lists(T* a, int64_t first, int64_t last, Cmp& comp, 
   return cut;
 }
 
+// A range of L elements that all compare equal, entered with depth limit d: introsort_loop's
+// steps do not depend on the elements, so each one's final offset follows from its own.  Per
+// step: move_median_to_first swaps offsets 0 and L / 2 (every comparison is false); the scans stop
+// at every position, so the pairs (1 + k, L - 1 - k), k < (L - 1) / 2, swap; the cut is
+// (L + 1) / 2; then the part holding the element continues, one depth lower, until at most 16
+// remain (the final insertion sort moves no equal elements).  tied_depth_ok(L, d): the depth limit
+// lasts (no part of more than 16 elements reaches depth 0, where the loop would heap-sort).
+TRS_HD inline bool tied_depth_ok(int64_t L, int d) {
+  while (L > kThreshold) {
+    if (d == 0) return false;
+    --d;
+    L = (L + 1) / 2;   // the larger part
+  }
+  return true;
+}
+
+TRS_HD inline int64_t tied_final_offset(int64_t L, int64_t o) {
+  int64_t base = 0;
+  while (L > kThreshold) {
+    const int64_t mid = L / 2;
+    if (o == 0) o = mid;
+    else if (o == mid) o = 0;
+    const int64_t ks = (L - 1) / 2;
+    if ((o >= 1 && o <= ks) || o >= L - ks) o = L - o;
+    const int64_t c = (L + 1) / 2;
+    if (o >= c) {
+      base += c;
+      o -= c;
+      L -= c;
+    } else {
+      L = c;
+    }
+  }
+  return base + o;
+}
+
 // The same step in batches of `lanes` pairs, as a wave runs it (one lane per pair), restated
 // sequentially for the host tests.  The two lists are filled by scans of `lanes` positions at a
 // time, which may read positions that an earlier batch has already swapped; such a read lies at
