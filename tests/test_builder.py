@@ -217,7 +217,8 @@ def _digest_case_ids():
 @pytest.mark.parametrize("name", _digest_case_ids())
 def test_product_matches_reference_digests_at_full_size(name, golden_env):
     """All 29 arrays bit-exact with the reference builder at BASELINE sizes: config 1 (ER 4096),
-    config 3 (SBM, 1M rows, 17.0M entries) and R-MAT 2^18 (7.6M entries).  The reference's
+    config 3 (SBM, 1M rows, 17.0M entries), config 5 (grid + hubs, 4M rows, 23.2M entries; the
+    reference took 50 minutes on it) and R-MAT 2^18 (7.6M entries).  The reference's
     outputs are committed as SHA-256 digests (tests/golden/make_golden.py digests), since the
     arrays themselves run to gigabytes; the regenerated input is checked against its digest
     first, so a changed generator cannot pass silently."""
