@@ -216,6 +216,35 @@ def calibration_copy(mib: int) -> None:
     del src, dst
 
 
+def build_and_plan(args, g, sddmm, **opts):
+    """The format (host builder, or the device builder from a CSR uploaded first) and the plan on
+    it, with their wall times: upload_s (CSR to HBM), build_s, plan_s."""
+    import numpy as np
+    import torch
+    import trspmm
+    torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of the timings
+    torch.cuda.synchronize()
+    pre = {"builder": args.builder}
+    if args.builder == "device":
+        t0 = time.time()
+        csr = [torch.from_numpy(np.ascontiguousarray(a, dtype=dt)).cuda()
+               for a, dt in ((g.rowptr, np.int32), (g.col, np.int32), (g.val, np.float32))]
+        torch.cuda.synchronize()
+        pre["upload_s"] = round(time.time() - t0, 4)
+        fmt = trspmm.build_format_device(*csr)
+        del csr
+    else:
+        fmt = trspmm.build_format(g.rowptr, g.col, g.val)
+    pre["build_s"] = round(fmt.elapsed, 4)
+    log(f"[bench] format built ({args.builder}) in {fmt.elapsed:.4f}s")
+    t1 = time.time()
+    plan = (trspmm.Plan.for_sddmm if sddmm else trspmm.Plan.from_format)(fmt, g.m, g.n, **opts)
+    pre["plan_s"] = round(time.time() - t1, 4)
+    pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
+    del fmt
+    return plan, pre
+
+
 def bench_sddmm(args, workload, g, K):
     """Config 4: SDDMM out[e] = X[row_e] . Y[col_e] on the R-MAT pattern (hybrid tiling)."""
     import numpy as np
@@ -223,17 +252,10 @@ def bench_sddmm(args, workload, g, K):
     import trspmm
     from trspmm import _native as nat, graphs
     t0 = time.time()
-    fmt = trspmm.build_format(g.rowptr, g.col, g.val)
-    torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of plan_s
-    torch.cuda.synchronize()
-    t1 = time.time()
-    plan = trspmm.Plan.for_sddmm(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                 feature_lanes=args.feature_lanes, hot_rows=args.hot_rows,
-                                 split_dispatch=int(args.split_dispatch), sddmm_unroll=args.sddmm_unroll)
+    plan, pre = build_and_plan(args, g, True, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
+                               feature_lanes=args.feature_lanes, hot_rows=args.hot_rows,
+                               split_dispatch=int(args.split_dispatch), sddmm_unroll=args.sddmm_unroll)
     st = plan.stats()
-    pre = {"build_s": round(fmt.elapsed, 3), "plan_s": round(time.time() - t1, 3),
-           "plan_lowering": "device" if st["device_lowered"] else "host"}
-    del fmt
     log(f"[bench] sddmm plan {st} ({time.time() - t0:.1f}s)")
     Xh = graphs.dense_operand(g.m, K, seed=4)
     Yh = graphs.dense_operand(g.n, K, seed=5)
@@ -337,6 +359,9 @@ def main():
     ap.add_argument("--reorder", choices=["none", "tca", "tca-aligned"], default="none",
                     help="TCA row reorder before the builder (timed, reported under 'preprocess'); "
                          "tca-aligned keeps clusters inside 16-row windows")
+    ap.add_argument("--builder", choices=["device", "host"], default="device",
+                    help="format builder: on the GPU from the CSR uploaded to HBM (default), or the host "
+                         "builder (the reference's CPU algorithm); both give the same format and plan")
     ap.add_argument("--host-lowering", action="store_true",
                     help="build the plan's residual on the host (default: on the device from the input CSR)")
     ap.add_argument("--feature-lanes", type=int, default=None,
@@ -387,21 +412,13 @@ def main():
         bench_sddmm(args, workload, g, K)
         return
     t0 = time.time()
-    fmt = trspmm.build_format(g.rowptr, g.col, g.val)
-    log(f"[bench] format built in {fmt.elapsed:.2f}s")
-    pre["build_s"] = round(fmt.elapsed, 3)
-    torch.zeros(1, device="cuda")   # HIP runtime start-up stays out of plan_s
-    torch.cuda.synchronize()
-    t1 = time.time()
-    plan = trspmm.Plan.from_format(fmt, g.m, g.n, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
-                                   window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes,
-                                   hot_rows=args.hot_rows, split_dispatch=int(args.split_dispatch))
-    pre["plan_s"] = round(time.time() - t1, 3)
-    pre["plan_lowering"] = "device" if plan.stats()["device_lowered"] else "host"
+    plan, built = build_and_plan(args, g, False, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
+                                 window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes,
+                                 hot_rows=args.hot_rows, split_dispatch=int(args.split_dispatch))
+    pre.update(built)
     if "reorder_s" in pre:
         pre["reorder_s"] = round(pre["reorder_s"], 3)
     st = plan.stats()
-    del fmt
     log(f"[bench] plan {st} ({time.time() - t0:.1f}s)")
     Bh = graphs.dense_operand(g.n, K, seed=bseed)
     B = torch.from_numpy(Bh).cuda()

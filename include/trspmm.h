@@ -336,6 +336,18 @@ int trs_plan_create_sptc_packed(const int32_t* s_tile_column, const int32_t* s_p
 int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_plan_options* opt,
                           trs_plan** out);
 
+/* trs_plan_create / trs_plan_create_sddmm from a device-resident format (trs_build_online_device),
+ * on the device that holds it (TRS_EINVAL when another device is current).  No reference
+ * counterpart (the reference hands its 29 arrays from the host, spmm/tr_csr_fp16/
+ * mdataset2_online.py:100-113).  The format does not come to the host: its row pointers, the TC
+ * arrays (slots 0-4, 6) and the 2:4 group tiles that pass the fill rule do; the residual is
+ * placed from the format's device copy of the input CSR.  The plan equals the one
+ * trs_plan_create(_sddmm) makes from trs_dformat_download's format, with the same options. */
+int trs_plan_create_dformat(const trs_dformat* f, int32_t m, int32_t n, const trs_plan_options* opt,
+                            trs_plan** out);
+int trs_plan_create_sddmm_dformat(const trs_dformat* f, int32_t m, int32_t n, const trs_plan_options* opt,
+                                  trs_plan** out);
+
 /* Plain CSR SDDMM plan (fp16 values kept for the caller's reference only; SDDMM does not scale by
  * them): outputs in the given entry order.  No reference counterpart. */
 int trs_plan_create_csr(const int32_t* rowptr, const int32_t* col, const uint16_t* val,

@@ -158,9 +158,10 @@ def test_device_lowering_exercises_tiles_and_split_rows():
     assert s1["device_lowered"] == 1 and s1["mfma_tiles"] == 0 and s1["tasks"] > s0["tasks"]
 
 
-@pytest.mark.parametrize("extra", [-7, 5])
+@pytest.mark.parametrize("extra", [-100, -7, 5])
 def test_device_lowering_with_other_row_counts(extra):
-    """m below the input's rows drops the rows beyond it; m above adds empty rows."""
+    """m below the input's rows drops the rows beyond it (-100: whole windows of tiles past m,
+    which the plan leaves out); m above adds empty rows."""
     g, f = graph("sbm2k", GRAPHS[2][1])
     m = g.m + extra
     say("device lowering m =", m)

@@ -1592,6 +1592,93 @@ __global__ __launch_bounds__(256) void k_renumber_hot(const int32_t* __restrict_
   }
 }
 
+__global__ __launch_bounds__(256) void k_check_columns(const int32_t* __restrict__ col, int64_t total, int32_t n,
+                                                       unsigned long long* __restrict__ first_bad) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int32_t c = col[e];
+    if (c < 0 || c >= n) atomicMin(first_bad, (unsigned long long)e);
+  }
+}
+
+// one wave per candidate row
+__global__ __launch_bounds__(256) void k_split_stats(const int32_t* __restrict__ col, const int32_t* __restrict__ start,
+                                                     const int32_t* __restrict__ len, int32_t rows,
+                                                     int32_t* __restrict__ cnt, uint32_t* __restrict__ seen) {
+  const int32_t i = (int32_t)(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (i >= rows) return;
+  const int l = threadIdx.x & 63;
+  const int32_t* c = col + start[i];
+  const int32_t n = len[i];
+  int32_t k[kXcds] = {};
+  for (int32_t q = l; q < n; q += 64) {
+    const int32_t v = c[q];
+    const int x = xcd_of_column(v);
+#pragma unroll
+    for (int y = 0; y < kXcds; ++y) k[y] += x == y;
+    if (seen) atomicOr(&seen[(uint32_t)v >> 5], 1u << (v & 31));
+  }
+#pragma unroll
+  for (int y = 0; y < kXcds; ++y) {
+    int32_t v = k[y];
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
+    if (l == 0) cnt[(int64_t)i * kXcds + y] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_popcount(const uint32_t* __restrict__ words, int64_t nwords,
+                                                  unsigned long long* __restrict__ out) {
+  unsigned long long s = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nwords; i += (int64_t)gridDim.x * 256)
+    s += __popc(words[i]);
+  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d);
+  if ((threadIdx.x & 63) == 0 && s) atomicAdd(out, s);
+}
+
+__global__ __launch_bounds__(256) void k_group_tile_fill(const int32_t* __restrict__ tile_win,
+                                                         const int32_t* __restrict__ tile_group,
+                                                         const int32_t* __restrict__ s_offsets,
+                                                         const int8_t* __restrict__ s_pos, int32_t ntiles,
+                                                         float min_fill, uint8_t* __restrict__ pass) {
+  const int32_t t = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (t >= ntiles) return;
+  const int32_t g0 = tile_group[t];
+  const int32_t g1 = min(g0 + 4, s_offsets[tile_win[t] + 1]);
+  int kept = 0;
+  for (int32_t g = g0; g < g1; ++g) {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(s_pos + (int64_t)g * 32);
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = p[i];   // four int8 positions, -1 = none
+      kept += ((w & 0x80u) == 0) + ((w & 0x8000u) == 0) + ((w & 0x800000u) == 0) + ((w & 0x80000000u) == 0);
+    }
+  }
+  pass[t] = (float)kept < min_fill * 256.f ? 0 : 1;
+}
+
+__global__ __launch_bounds__(256) void k_gather_group_tiles(const int32_t* __restrict__ ids, int32_t nids,
+                                                            const int32_t* __restrict__ tile_win,
+                                                            const int32_t* __restrict__ tile_group,
+                                                            const int32_t* __restrict__ s_offsets,
+                                                            const int32_t* __restrict__ s_col,
+                                                            const float* __restrict__ s_val,
+                                                            const int8_t* __restrict__ s_pos,
+                                                            GroupTile* __restrict__ out) {
+  const int32_t i = (int32_t)(blockIdx.x * 256 + threadIdx.x);
+  if (i >= nids) return;
+  const int32_t t = ids[i];
+  const int32_t w = tile_win[t], g0 = tile_group[t];
+  const int32_t ng = min(4, s_offsets[w + 1] - g0);
+  GroupTile& o = out[i];
+  o.row0 = w * 16;
+  o.ngroups = ng;
+  for (int g = 0; g < 4; ++g) {
+    for (int p = 0; p < 4; ++p) o.cols[g * 4 + p] = g < ng ? s_col[(int64_t)(g0 + g) * 4 + p] : -1;
+    for (int j = 0; j < 32; ++j) {
+      o.val[g][j] = g < ng ? s_val[(int64_t)(g0 + g) * 32 + j] : 0.f;
+      o.pos[g][j] = g < ng ? s_pos[(int64_t)(g0 + g) * 32 + j] : (int8_t)-1;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_zero_fill(float* __restrict__ out, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) out[i] = 0.f;
 }
@@ -1661,6 +1748,45 @@ hipError_t launch_renumber_hot(const int32_t* col, int64_t total, int32_t n, con
                                hipStream_t stream) {
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_renumber_hot, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, rank, hot_col);
+  return hipGetLastError();
+}
+
+hipError_t launch_check_columns(const int32_t* col, int64_t total, int32_t n, unsigned long long* first_bad,
+                                hipStream_t stream) {
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_check_columns, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, first_bad);
+  return hipGetLastError();
+}
+
+hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, int32_t rows, int32_t* cnt,
+                              uint32_t* seen, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_split_stats, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, col, start, len, rows, cnt,
+                     seen);
+  return hipGetLastError();
+}
+
+hipError_t launch_popcount(const uint32_t* words, int64_t nwords, unsigned long long* out, hipStream_t stream) {
+  if (nwords <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_popcount, dim3(stride_grid(nwords)), dim3(256), 0, stream, words, nwords, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_group_tile_fill(const int32_t* tile_win, const int32_t* tile_group, const int32_t* s_offsets,
+                                  const int8_t* s_pos, int32_t ntiles, float min_fill, uint8_t* pass,
+                                  hipStream_t stream) {
+  if (ntiles <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_group_tile_fill, dim3((unsigned)((ntiles + 255) / 256)), dim3(256), 0, stream, tile_win,
+                     tile_group, s_offsets, s_pos, ntiles, min_fill, pass);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_group_tiles(const int32_t* ids, int32_t nids, const int32_t* tile_win,
+                                     const int32_t* tile_group, const int32_t* s_offsets, const int32_t* s_col,
+                                     const float* s_val, const int8_t* s_pos, GroupTile* out, hipStream_t stream) {
+  if (nids <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gather_group_tiles, dim3((unsigned)((nids + 255) / 256)), dim3(256), 0, stream, ids, nids,
+                     tile_win, tile_group, s_offsets, s_col, s_val, s_pos, out);
   return hipGetLastError();
 }
 

@@ -182,6 +182,31 @@ struct PlaceEntries {
 };
 hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream);
 
+// Plans from a device-resident format (trs_dformat): what the host lowering reads of the input
+// CSR's columns, computed where they are.
+// *first_bad (the caller sets it to ~0ull) = the lowest index e with col[e] outside [0, n).
+hipError_t launch_check_columns(const int32_t* col, int64_t total, int32_t n, unsigned long long* first_bad,
+                                hipStream_t stream);
+// For split-row candidate i (entries col[start[i] .. start[i] + len[i])): cnt[i * kXcds + x] =
+// its entries of XCD class x (xcd_of_column); with seen (n bits, zeroed by the caller) also the
+// candidates' columns marked in it.
+hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, int32_t rows,
+                              int32_t* cnt, uint32_t* seen, hipStream_t stream);
+// *out += set bits of words[0, nwords) (*out zeroed by the caller).
+hipError_t launch_popcount(const uint32_t* words, int64_t nwords, unsigned long long* out, hipStream_t stream);
+// 2:4 group tiles of a window-16 format (tiles of four groups per window, block_online.cpp:796-841):
+// pass[t] = 1 when the stored values of tile t's groups (s_pos >= 0, 32 per group) are at least
+// min_fill * 256, the fill rule of the host lowering.
+hipError_t launch_group_tile_fill(const int32_t* tile_win, const int32_t* tile_group, const int32_t* s_offsets,
+                                  const int8_t* s_pos, int32_t ntiles, float min_fill, uint8_t* pass,
+                                  hipStream_t stream);
+// The groups of the listed tiles, packed: GroupTile i holds tile ids[i]'s window row, group count,
+// s_columns, s_values and s_pos (window 16).
+struct GroupTile { int32_t row0, ngroups; int32_t cols[16]; float val[4][32]; int8_t pos[4][32]; };
+hipError_t launch_gather_group_tiles(const int32_t* ids, int32_t nids, const int32_t* tile_win,
+                                     const int32_t* tile_group, const int32_t* s_offsets, const int32_t* s_col,
+                                     const float* s_val, const int8_t* s_pos, GroupTile* out, hipStream_t stream);
+
 // hot: the staged-row buffer (hot_buffer_bytes(p, K) bytes; null = gather every row from B).
 // ev (optional): 4 events recorded before the task kernel (and the hot-row copy) and after each of
 // the three kernels.

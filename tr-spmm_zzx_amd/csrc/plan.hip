@@ -24,6 +24,7 @@
 #include <thread>
 #include <vector>
 
+#include "dformat.hpp"
 #include "format.hpp"
 #include "kernels.hpp"
 
@@ -58,6 +59,11 @@ struct Status {
 };
 
 Status fail(int code, const std::string& m) { return Status{code, m}; }
+
+// Internal status of the device lowering: the format's tiles and its input CSR disagree (a tile
+// entry the CSR does not hold, or two tiles holding one entry) or its temporaries could not be
+// allocated; the caller then lowers on the host.
+constexpr int kLowerOnHost = -100;
 
 // Default XCD column split thresholds (rows with at least this many residual entries).  SpMM, R-MAT
 // 2^20 step at K = 32 / 64 / 128 / 256: -16% / -6% / -18% / -19% against no split (128 and 512
@@ -476,6 +482,26 @@ struct Blob {
 // row lengths and the split rows' columns alone), move_entries puts them there (on the host here;
 // the device lowering does it with kernels), build_tasks cuts the placed rows into tasks.
 
+// The input CSR a device lowering reads: row pointers on the host; columns and values on the host
+// (a trs_format built in this process), in device memory (a trs_dformat), or both.
+struct CsrSource {
+  int32_t rows = 0;
+  const int32_t* rowptr = nullptr;   // host, rows + 1
+  const int32_t* col = nullptr;      // host (null: device only)
+  const float* val = nullptr;
+  const int32_t* d_col = nullptr;    // device (null: uploaded from the host arrays when needed)
+  const float* d_val = nullptr;
+};
+
+CsrSource csr_of(const trs_format& f) {
+  CsrSource c;
+  c.rows = f.rows;
+  c.rowptr = f.csr_rowptr.data();
+  c.col = f.csr_col.data();
+  c.val = f.csr_val.data();
+  return c;
+}
+
 // Where the residual entries go in the plan's entry arrays.
 struct Placement {
   bool compact = false;               // SpMM: split rows leave the main part (else they stay, SDDMM)
@@ -490,6 +516,11 @@ struct Placement {
   int32_t J() const { return (int32_t)sub_row.size(); }
 };
 
+// Split-row statistics from device-resident columns (defined with the device lowering below).
+Status split_stats_device(const int32_t* d_col, const int32_t* col_rowptr, const std::vector<int32_t>& rowptr,
+                          const std::vector<int32_t>& split_rows, int32_t n, bool need_distinct, int64_t& total,
+                          int64_t& distinct, std::vector<int32_t>& cnt);
+
 // rowptr: the residual CSR's row pointers; owned: per 16-row block (empty = none).  The columns of
 // a split row r are col[col_rowptr[r] ..] (col_rowptr = rowptr for the residual CSR itself; the
 // input CSR's row pointers when the residual is built on the device, where split rows -- owned by
@@ -499,9 +530,11 @@ struct Placement {
 // min_reuse times their distinct columns.  The split buys L2 reuse of B rows; columns the long rows
 // read once or twice each (uniformly random hub rows) have none to buy, and the split's extra
 // launch and partial slots then cost time.
+// d_col (device lowering of a device-resident CSR; col is then unused): the candidates' statistics
+// are counted on the device instead.
 Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, const int32_t* col_rowptr, int32_t m,
                         int32_t n, const std::vector<uint8_t>& owned, bool compact, int32_t split_min,
-                        int32_t min_reuse = 0) {
+                        int32_t min_reuse = 0, const int32_t* d_col = nullptr, Status* st = nullptr) {
   Placement P;
   P.compact = compact;
   const int64_t nent = rowptr[m];
@@ -512,7 +545,21 @@ Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, 
         P.split[r] = 1;
         P.split_rows.push_back(r);
       }
-  if (min_reuse > 0 && !P.split_rows.empty()) {
+  std::vector<int32_t> dev_cnt;
+  if (d_col && !P.split_rows.empty()) {
+    int64_t total = 0, distinct = 0;
+    const Status ds = split_stats_device(d_col, col_rowptr, rowptr, P.split_rows, n, min_reuse > 0, total, distinct,
+                                         dev_cnt);
+    if (!ds.ok()) {
+      if (st) *st = ds;
+      return P;
+    }
+    if (min_reuse > 0 && total < (int64_t)min_reuse * distinct) {
+      for (int32_t r : P.split_rows) P.split[r] = 0;
+      P.split_rows.clear();
+      dev_cnt.clear();
+    }
+  } else if (min_reuse > 0 && !P.split_rows.empty()) {
     // distinct columns of the candidate rows: per-thread bitmaps, OR-ed
     const int T = lowering_threads();
     const size_t ns = P.split_rows.size();
@@ -546,7 +593,8 @@ Placement place_entries(const std::vector<int32_t>& rowptr, const int32_t* col, 
   const size_t ns = P.split_rows.size();
   // entries per (split row, XCD), counted by the column hash on a few threads
   std::vector<int32_t> cnt(ns * trs::kXcds, 0);
-  parallel_parts(lowering_threads(), (int64_t)ns, 256, [&](int t) { return (int64_t)ns * t / lowering_threads(); },
+  if (d_col) cnt.swap(dev_cnt);
+  else parallel_parts(lowering_threads(), (int64_t)ns, 256, [&](int t) { return (int64_t)ns * t / lowering_threads(); },
                  [&](int64_t b, int64_t e, int) {
                    for (int64_t i = b; i < e; ++i) {
                      const int32_t r = P.split_rows[i];
@@ -838,6 +886,55 @@ bool copy_pieces(const Blob& blob, void* dmem) {
   return true;
 }
 
+// Entries per (split candidate, XCD class) -- cnt, as place_entries counts them -- and, with
+// need_distinct, the candidates' distinct columns, counted on the device from the input columns
+// d_col (candidate i = split_rows[i] holds d_col[col_rowptr[r] ..] of length rowptr[r + 1] - rowptr[r]).
+Status split_stats_device(const int32_t* d_col, const int32_t* col_rowptr, const std::vector<int32_t>& rowptr,
+                          const std::vector<int32_t>& split_rows, int32_t n, bool need_distinct, int64_t& total,
+                          int64_t& distinct, std::vector<int32_t>& cnt) {
+  const size_t ns = split_rows.size();
+  std::vector<int32_t> start(ns), len(ns);
+  total = 0;
+  for (size_t i = 0; i < ns; ++i) {
+    const int32_t r = split_rows[i];
+    start[i] = col_rowptr[r];
+    len[i] = rowptr[r + 1] - rowptr[r];
+    total += len[i];
+  }
+  const size_t words = need_distinct ? ((size_t)n + 31) / 32 : 0;
+  Blob tmp;
+  const size_t o_start = tmp.add(start);
+  const size_t o_len = tmp.add(len);
+  const size_t o_cnt = tmp.add_raw(nullptr, ns * trs::kXcds * 4);
+  const size_t o_pop = tmp.add_raw(nullptr, 8 + words * 4);   // the count, then the bitmap
+  void* dmem = nullptr;
+  if (hipMalloc(&dmem, tmp.size()) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(kLowerOnHost, "device lowering temporaries: hipMalloc failed");
+  }
+  unsigned char* base = static_cast<unsigned char*>(dmem);
+  auto done = [&](Status st) {
+    (void)hipFree(dmem);
+    return st;
+  };
+  unsigned long long* d_pop = reinterpret_cast<unsigned long long*>(base + o_pop);
+  uint32_t* d_seen = need_distinct ? reinterpret_cast<uint32_t*>(base + o_pop + 8) : nullptr;
+  int32_t* d_cnt = reinterpret_cast<int32_t*>(base + o_cnt);
+  if (!copy_pieces(tmp, dmem) || hipMemset(base + o_pop, 0, 8 + words * 4) != hipSuccess ||
+      trs::launch_split_stats(d_col, reinterpret_cast<const int32_t*>(base + o_start),
+                              reinterpret_cast<const int32_t*>(base + o_len), (int32_t)ns, d_cnt, d_seen,
+                              nullptr) != hipSuccess ||
+      (need_distinct && trs::launch_popcount(d_seen, (int64_t)words, d_pop, nullptr) != hipSuccess))
+    return done(fail(TRS_EDEVICE, "device lowering: split statistics launch failed"));
+  cnt.resize(ns * trs::kXcds);
+  unsigned long long pop = 0;
+  if (hipMemcpy(cnt.data(), d_cnt, cnt.size() * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(&pop, d_pop, 8, hipMemcpyDeviceToHost) != hipSuccess)
+    return done(fail(TRS_EDEVICE, "device lowering: split statistics failed"));
+  distinct = (int64_t)pop;
+  return done(Status{});
+}
+
 // One hipMalloc holding the whole plan, filled array by array.
 Status upload(const Blob& blob, trs_plan*& P) {
   P = new trs_plan();
@@ -940,11 +1037,6 @@ void add_quad(Quads& Q, const std::vector<Lowering::Tile>& tiles, size_t b, size
   }
 }
 
-// Internal status of the device lowering: the format's tiles and its input CSR disagree (a tile
-// entry the CSR does not hold, or two tiles holding one entry) or its temporaries could not be
-// allocated; the caller then lowers on the host.
-constexpr int kLowerOnHost = -100;
-
 // Entries stored by tile t, rows < m: the present bits (tile_add sets each once per entry).
 int64_t tile_present(const Lowering::Tile& t) {
   int64_t c = 0;
@@ -976,12 +1068,12 @@ struct DeviceOut {
 // their flagged entries, split rows scattered into their XCD sub-rows.  Outputs follow the input
 // CSR order, so an entry's output index is its CSR index.  Temporaries live in one allocation
 // freed before returning.
-Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowering::Tile>& tiles,
+Status residual_on_device(const CsrSource& f, int32_t m, const std::vector<Lowering::Tile>& tiles,
                           int64_t expect_marked, const Placement& PL, const DeviceOut& o) {
   const int32_t rows = std::min(m, f.rows);
-  const int64_t cnnz = f.csr_rowptr[rows];
+  const int64_t cnnz = f.rowptr[rows];
   std::vector<int32_t> rp((size_t)m + 1, (int32_t)cnnz);
-  std::copy(f.csr_rowptr.begin(), f.csr_rowptr.begin() + rows + 1, rp.begin());
+  std::copy(f.rowptr, f.rowptr + rows + 1, rp.begin());
   std::vector<trs::TileEntries> te(tiles.size());
   for (size_t i = 0; i < tiles.size(); ++i) {
     te[i] = trs::TileEntries{};
@@ -993,8 +1085,10 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   for (size_t i = 0; i < PL.split_rows.size(); ++i) split_index[PL.split_rows[i]] = (int32_t)i;
   Blob tmp;
   const size_t o_rp = tmp.add(rp);
-  const size_t o_col = tmp.add_raw(f.csr_col.data(), (size_t)cnnz * 4);
-  const size_t o_val = tmp.add_raw(o.val ? f.csr_val.data() : nullptr, o.val ? (size_t)cnnz * 4 : 0);
+  // columns and values go up unless they are on the device already
+  const size_t o_col = tmp.add_raw(f.d_col ? nullptr : f.col, f.d_col ? 0 : (size_t)cnnz * 4);
+  const bool up_val = o.val && !f.d_val;
+  const size_t o_val = tmp.add_raw(up_val ? f.val : nullptr, up_val ? (size_t)cnnz * 4 : 0);
   const size_t o_te = tmp.add(te);
   const size_t o_si = tmp.add(split_index);
   const size_t o_cur = tmp.add(PL.cursor);
@@ -1016,7 +1110,7 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   if (!copy_pieces(tmp, dmem) || hipMemset(base + o_flag, 0, flag_bytes + 256) != hipSuccess)
     return done(fail(TRS_EDEVICE, "device lowering: upload failed"));
   const int32_t* d_rp = reinterpret_cast<const int32_t*>(base + o_rp);
-  const int32_t* d_col = reinterpret_cast<const int32_t*>(base + o_col);
+  const int32_t* d_col = f.d_col ? f.d_col : reinterpret_cast<const int32_t*>(base + o_col);
   uint32_t* d_flag = reinterpret_cast<uint32_t*>(base + o_flag);
   uint32_t* d_marked = reinterpret_cast<uint32_t*>(base + o_flag + flag_bytes);
   if (!tiles.empty()) {
@@ -1037,7 +1131,7 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
   a.m = m;
   a.rowptr = d_rp;
   a.col = d_col;
-  a.val = o.val ? reinterpret_cast<const float*>(base + o_val) : nullptr;
+  a.val = !o.val ? nullptr : f.d_val ? f.d_val : reinterpret_cast<const float*>(base + o_val);
   a.flag = tiles.empty() ? nullptr : reinterpret_cast<const uint8_t*>(d_flag);
   a.main_rowptr = o.main_rowptr;
   a.split_index = reinterpret_cast<const int32_t*>(base + o_si);
@@ -1060,24 +1154,43 @@ Status residual_on_device(const trs_format& f, int32_t m, const std::vector<Lowe
 // Device lowering, host side: the column range check the host lowering makes (a residual or tile
 // column outside [0, n) is TRS_ERANGE) over the input CSR's rows [0, m), and their lengths (rows
 // beyond the input's are empty).
-Status input_rows(const trs_format& src, Lowering& L, std::vector<int32_t>& csr_len) {
+Status input_rows(const CsrSource& src, Lowering& L, std::vector<int32_t>& csr_len) {
   const int32_t m = L.m;
   const int32_t rows = std::min(m, src.rows);
-  const int64_t cnnz = src.csr_rowptr[rows];
-  const int T = lowering_threads();
-  std::vector<int64_t> bad((size_t)T, INT64_MAX);
-  parallel_parts(T, cnnz, 1 << 16, [&](int t) { return cnnz * t / T; }, [&](int64_t b, int64_t e, int t) {
-    for (int64_t q = b; q < e; ++q)
-      if (src.csr_col[q] < 0 || src.csr_col[q] >= L.n) {
-        bad[t] = q;
-        break;
-      }
-  });
-  const int64_t q = *std::min_element(bad.begin(), bad.end());
-  if (q != INT64_MAX) L.check_col(src.csr_col[q]);
+  const int64_t cnnz = src.rowptr[rows];
+  if (src.col) {
+    const int T = lowering_threads();
+    std::vector<int64_t> bad((size_t)T, INT64_MAX);
+    parallel_parts(T, cnnz, 1 << 16, [&](int t) { return cnnz * t / T; }, [&](int64_t b, int64_t e, int t) {
+      for (int64_t q = b; q < e; ++q)
+        if (src.col[q] < 0 || src.col[q] >= L.n) {
+          bad[t] = q;
+          break;
+        }
+    });
+    const int64_t q = *std::min_element(bad.begin(), bad.end());
+    if (q != INT64_MAX) L.check_col(src.col[q]);
+  } else if (cnnz > 0) {
+    // the first column outside [0, n), found where the columns are
+    void* d = nullptr;
+    if (hipMalloc(&d, 8) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(kLowerOnHost, "device lowering temporaries: hipMalloc failed");
+    }
+    unsigned long long first = ~0ull;
+    int32_t c = 0;
+    const bool ok = hipMemcpy(d, &first, 8, hipMemcpyHostToDevice) == hipSuccess &&
+                    trs::launch_check_columns(src.d_col, cnnz, L.n, static_cast<unsigned long long*>(d), nullptr) ==
+                        hipSuccess &&
+                    hipMemcpy(&first, d, 8, hipMemcpyDeviceToHost) == hipSuccess &&
+                    (first == ~0ull || hipMemcpy(&c, src.d_col + first, 4, hipMemcpyDeviceToHost) == hipSuccess);
+    (void)hipFree(d);
+    if (!ok) return fail(TRS_EDEVICE, "device lowering: column check failed");
+    if (first != ~0ull) L.check_col(c);
+  }
   if (!L.st.ok()) return L.st;
   csr_len.assign((size_t)m, 0);
-  for (int32_t r = 0; r < rows; ++r) csr_len[r] = src.csr_rowptr[r + 1] - src.csr_rowptr[r];
+  for (int32_t r = 0; r < rows; ++r) csr_len[r] = src.rowptr[r + 1] - src.rowptr[r];
   // a tile slot added twice (duplicate input entries) holds a sum the input CSR does not
   for (const auto& t : L.tiles)
     if (t.nnz != tile_present(t)) return fail(kLowerOnHost, "device lowering: a tile slot holds two entries");
@@ -1179,8 +1292,18 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
 // Residual CSR + tasks + MFMA windows -> device plan.  With src (the format that holds its input
 // CSR), L carries the tiles only and the residual -- the input CSR minus the kept tiles' entries --
 // is built on the device; the plan equals the host lowering's (same arrays, same statistics).
-Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const trs_format* src = nullptr) {
+// Tiles whose rows all lie at or past m hold no entries (the lowerings add none there: reference
+// kernels drop rows >= mOri).  They come from windows past the plan's rows, and from formats of
+// windows under 16 rows, whose t_window_row is the window id * 16 (block_online.cpp:494) and so
+// runs to twice the rows and more.
+void drop_tiles_past_m(Lowering& L) {
+  L.tiles.erase(std::remove_if(L.tiles.begin(), L.tiles.end(), [&](const Lowering::Tile& t) { return t.row0 >= L.m; }),
+                L.tiles.end());
+}
+
+Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const CsrSource* src = nullptr) {
   if (!L.st.ok()) return L.st;
+  drop_tiles_past_m(L);
   const int32_t m = L.m;
   // device lowering: row lengths of the input CSR (rows beyond its rows are empty)
   std::vector<int32_t> csr_len;
@@ -1301,9 +1424,12 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   // XCD column split for SpMM (each sub-row costs a partial slot of 4 K bytes written and read back)
   const int32_t split_min = opt.xcd_split < 0 ? 0 : opt.xcd_split > 0 ? opt.xcd_split : kSpmmSplitMin;
   const int32_t reuse = opt.xcd_split == 0 ? kSplitMinReuse : 0;
+  Status pst;
   const Placement PL =
-      src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, owned, true, split_min, reuse)
+      src ? place_entries(rowptr, src->col, src->rowptr, m, L.n, owned, true, split_min, reuse,
+                          src->col ? nullptr : src->d_col, &pst)
           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, owned, true, split_min, reuse);
+  if (!pst.ok()) return pst;
   std::vector<int32_t> col2;
   std::vector<uint16_t> val2;
   if (!src) move_entries(PL, rowptr, col.data(), val.data(), m, col2, &val2, nullptr);
@@ -1421,11 +1547,12 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
 // tiles with the output index of each stored slot.  Outputs follow the (row, column) order of all
 // entries, i.e. the input CSR order for canonical input; keep_order keeps a plain CSR as given.
 //
-// With src (the format that holds its input CSR), L carries the tiles only and the residual is
+// With src (the input CSR of the format), L carries the tiles only and the residual is
 // built on the device as for SpMM plans; the output index of an entry is then its input CSR index.
 Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order, trs_plan** out,
-                      const trs_format* src = nullptr) {
+                      const CsrSource* src = nullptr) {
   if (!L.st.ok()) return L.st;
+  drop_tiles_past_m(L);
   std::vector<int32_t> csr_len;
   if (src) {
     const Status is = input_rows(*src, L, csr_len);
@@ -1512,9 +1639,12 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   // the input rows')
   const int32_t split = with_pos ? 0 : split_min;
   const int32_t reuse = opt.xcd_split == 0 ? kSplitMinReuse : 0;
+  Status pst;
   const Placement PL =
-      src ? place_entries(rowptr, src->csr_col.data(), src->csr_rowptr.data(), m, L.n, {}, false, split, reuse)
+      src ? place_entries(rowptr, src->col, src->rowptr, m, L.n, {}, false, split, reuse,
+                          src->col ? nullptr : src->d_col, &pst)
           : place_entries(rowptr, col.data(), rowptr.data(), m, L.n, {}, false, split, reuse);
+  if (!pst.ok()) return pst;
   // the split rows' outputs merged from the split part's own buffer: merge_off[i] = entries of the
   // split rows before split row i; tasks of at most trs::kMergeTaskEntries output indices
   std::vector<int32_t> merge_off(PL.split_rows.size() + 1, 0);
@@ -1647,6 +1777,120 @@ void lower_format_tiles(Lowering& L, const trs_format& f, const trs_plan_options
                f.s_offsets.data(), (int64_t)f.s_offsets.size() - 1, f.window, o.mfma_sptc != 0, o.sptc_min_fill);
 }
 
+// The tiles of a device-resident builder output, as lower_format_tiles finds them in the host
+// one: the TC arrays (slots 0-4, 6) come to the host for lower_tc; the 2:4 group tiles that pass
+// the fill rule are chosen and gathered on the device, and only those come over.
+Status lower_dformat_tiles(Lowering& L, const trs_dformat& f, const trs_plan_options& o) {
+  auto fetch = [&](int s, auto& v) {
+    v.resize((size_t)f.slot[s].numel);
+    return v.empty() ||
+           hipMemcpy(v.data(), f.slot[s].ptr, v.size() * sizeof(v[0]), hipMemcpyDeviceToHost) == hipSuccess;
+  };
+  {
+    std::vector<int32_t> t_rowoff, t_blockoff, t_col, t_winrow;
+    std::vector<float> t_val;
+    std::vector<int64_t> t_bin;
+    if (!fetch(0, t_rowoff) || !fetch(1, t_blockoff) || !fetch(2, t_col) || !fetch(3, t_val) || !fetch(4, t_winrow) ||
+        !fetch(6, t_bin))
+      return fail(TRS_EDEVICE, "device format: TC array download failed");
+    lower_tc(L, t_rowoff.data(), (int64_t)t_winrow.size(), t_blockoff.data(), t_col.data(), t_val.data(), nullptr,
+             (int64_t)t_val.size(), t_winrow.data(), t_bin.data(), o.mfma_tc != 0);
+    if (!L.st.ok()) return L.st;
+  }
+  const int64_t ntiles = f.slot[23].numel;
+  if (!o.mfma_sptc || f.window != 16 || ntiles == 0) return Status{};
+  if (ntiles > INT32_MAX) return fail(TRS_ERANGE, "more than 2^31 group tiles");
+  const int32_t* tile_win = static_cast<const int32_t*>(f.slot[23].ptr);
+  const int32_t* tile_group = static_cast<const int32_t*>(f.slot[24].ptr);
+  const int32_t* s_off = static_cast<const int32_t*>(f.slot[22].ptr);
+  const int32_t* s_col = static_cast<const int32_t*>(f.slot[17].ptr);
+  const float* s_val = static_cast<const float*>(f.slot[19].ptr);
+  const int8_t* s_pos = static_cast<const int8_t*>(f.slot[20].ptr);
+  void* dpass = nullptr;
+  const size_t ids_off = ((size_t)ntiles + 3) & ~size_t(3);   // pass flags, then up to ntiles ids
+  if (hipMalloc(&dpass, ids_off + (size_t)ntiles * 4) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(kLowerOnHost, "device lowering temporaries: hipMalloc failed");
+  }
+  uint8_t* d_pass = static_cast<uint8_t*>(dpass);
+  int32_t* d_ids = reinterpret_cast<int32_t*>(d_pass + ids_off);
+  std::vector<uint8_t> pass((size_t)ntiles);
+  if (trs::launch_group_tile_fill(tile_win, tile_group, s_off, s_pos, (int32_t)ntiles, o.sptc_min_fill, d_pass,
+                                  nullptr) != hipSuccess ||
+      hipMemcpy(pass.data(), d_pass, pass.size(), hipMemcpyDeviceToHost) != hipSuccess) {
+    (void)hipFree(dpass);
+    return fail(TRS_EDEVICE, "device format: group tile fill failed");
+  }
+  std::vector<int32_t> ids;
+  for (int64_t t = 0; t < ntiles; ++t)
+    if (pass[t]) ids.push_back((int32_t)t);
+  std::vector<trs::GroupTile> gt(ids.size());
+  void* dgt = nullptr;
+  bool ok = true;
+  if (!ids.empty()) {
+    ok = hipMalloc(&dgt, gt.size() * sizeof(trs::GroupTile)) == hipSuccess;
+    if (!ok) {
+      (void)hipGetLastError();
+      (void)hipFree(dpass);
+      return fail(kLowerOnHost, "device lowering temporaries: hipMalloc failed");
+    }
+    ok = hipMemcpy(d_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         trs::launch_gather_group_tiles(d_ids, (int32_t)ids.size(), tile_win, tile_group, s_off, s_col, s_val, s_pos,
+                                        static_cast<trs::GroupTile*>(dgt), nullptr) == hipSuccess &&
+         hipMemcpy(gt.data(), dgt, gt.size() * sizeof(trs::GroupTile), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(dgt);
+  }
+  (void)hipFree(dpass);
+  if (!ok) return fail(TRS_EDEVICE, "device format: group tile gather failed");
+  // lower_groups_range's tile step, per gathered tile: a tile with a column outside [0, n) or a
+  // position outside 0..3 stops the lowering at the first such tile, in tile order
+  auto make = [&](const trs::GroupTile& g, Lowering::Tile& T, Lowering& E) {
+    Lowering::tile_init(T, g.row0);
+    for (int gi = 0; gi < g.ngroups; ++gi) {
+      for (int p = 0; p < 4; ++p) {
+        const int32_t c = g.cols[gi * 4 + p];
+        if (c >= 0 && !E.check_col(c)) return false;
+        T.cols[gi * 4 + p] = c;
+      }
+      for (int j = 0; j < 32; ++j) {
+        const int p = g.pos[gi][j];
+        if (p < 0) continue;
+        if (p > 3) {
+          E.st = fail(TRS_EINVAL, "s_pos entry outside 0..3");
+          return false;
+        }
+        if (g.cols[gi * 4 + p] < 0) continue;
+        if (g.row0 + j / 2 < E.m) E.tile_add(T, j / 2, gi * 4 + p, g.val[gi][j]);
+      }
+    }
+    return true;
+  };
+  const size_t t0 = L.tiles.size();
+  L.tiles.resize(t0 + gt.size());
+  std::vector<uint8_t> bad(gt.size(), 0);
+  parallel_tiles((int64_t)gt.size(), [&](int64_t b, int64_t e, int) {
+    Lowering E;
+    E.m = L.m;
+    E.n = L.n;
+    for (int64_t i = b; i < e; ++i) bad[i] = !make(gt[i], L.tiles[t0 + i], E);
+  });
+  for (size_t i = 0; i < gt.size(); ++i)
+    if (bad[i]) {
+      Lowering::Tile T;
+      make(gt[i], T, L);   // sets L.st as the serial lowering would
+      L.tiles.resize(t0 + i);
+      return L.st;
+    }
+  return Status{};
+}
+
+// The device lowering takes the residual from the input CSR, minus the entries of the kept tiles:
+// for window 16 only, where a TC part's t_window_row (the window id * 16, block_online.cpp:494) is
+// its window's first row.  Formats of other window sizes place TC entries at rows of their own.
+bool device_lowering_applies(const trs_format& f, const trs_plan_options& o) {
+  return !o.host_lowering && !f.csr_rowptr.empty() && f.window == 16;
+}
+
 int report(const Status& s) {
   if (!s.ok()) trs::set_error(s.msg);
   return s.code;
@@ -1707,14 +1951,15 @@ int trs_plan_create(const trs_format* f, int32_t m, int32_t n, const trs_plan_op
                                       "arrays cannot describe duplicate or unsorted entries"));
   trs_plan_options o;
   if (const Status rs = resolve(opt, o, "trs_plan_create"); !rs.ok()) return report(rs);
-  if (!o.host_lowering && !f->csr_rowptr.empty()) {
+  if (device_lowering_applies(*f, o)) {
     // device lowering: the tiles from the format, the residual from its input CSR
     Lowering D;
     D.m = m;
     D.n = n;
     D.tiles_only = true;
     lower_format_tiles(D, *f, o);
-    const Status ds = finalize(D, o, out, f);
+    const CsrSource cs = csr_of(*f);
+    const Status ds = finalize(D, o, out, &cs);
     if (ds.code != kLowerOnHost) return report(ds);
   }
   Lowering L;
@@ -1734,13 +1979,14 @@ int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_p
     return report(fail(TRS_ENOTCANON, "trs_plan_create_sddmm: input rows were not strictly increasing"));
   trs_plan_options o;
   if (const Status rs = resolve(opt, o, "trs_plan_create_sddmm"); !rs.ok()) return report(rs);
-  if (!o.host_lowering && !f->csr_rowptr.empty()) {
+  if (device_lowering_applies(*f, o)) {
     Lowering D;
     D.m = m;
     D.n = n;
     D.tiles_only = true;
     lower_format_tiles(D, *f, o);
-    const Status ds = finalize_sddmm(D, o, false, out, f);
+    const CsrSource cs = csr_of(*f);
+    const Status ds = finalize_sddmm(D, o, false, out, &cs);
     if (ds.code != kLowerOnHost) return report(ds);
   }
   Lowering L;
@@ -1748,6 +1994,56 @@ int trs_plan_create_sddmm(const trs_format* f, int32_t m, int32_t n, const trs_p
   L.n = n;
   lower_format(L, *f, o);
   return report(finalize_sddmm(L, o, false, out));
+}
+
+// Plans from a device-resident format: the tiles as lower_dformat_tiles finds them, the residual
+// from the format's device copy of the input CSR (only its row pointers come to the host).  Host
+// lowering (option host_lowering, or inputs the device lowering does not take) downloads the
+// format and lowers it as trs_plan_create does.
+static int plan_from_dformat(const trs_dformat* f, int32_t m, int32_t n, const trs_plan_options* opt, bool sddmm,
+                             trs_plan** out, const char* where) {
+  if (!f || !out) return report(fail(TRS_EINVAL, std::string(where) + ": NULL argument"));
+  *out = nullptr;
+  if (bad_dims(m, n)) return report(fail(TRS_EINVAL, std::string(where) + ": negative m or n"));
+  trs_plan_options o;
+  if (const Status rs = resolve(opt, o, where); !rs.ok()) return report(rs);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != f->device)
+    return report(fail(TRS_EINVAL, std::string(where) + ": the format lives on device " + std::to_string(f->device) +
+                                       ", not on the current device"));
+  if (!o.host_lowering && f->window == 16) {
+    std::vector<int32_t> rowptr((size_t)f->rows + 1);
+    if (hipMemcpy(rowptr.data(), f->csr_rowptr, rowptr.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+      return report(fail(TRS_EDEVICE, std::string(where) + ": row pointer download failed"));
+    CsrSource cs;
+    cs.rows = f->rows;
+    cs.rowptr = rowptr.data();
+    cs.d_col = f->csr_col;
+    cs.d_val = f->csr_val;
+    Lowering D;
+    D.m = m;
+    D.n = n;
+    D.tiles_only = true;
+    Status ds = lower_dformat_tiles(D, *f, o);
+    if (ds.ok()) ds = sddmm ? finalize_sddmm(D, o, false, out, &cs) : finalize(D, o, out, &cs);
+    if (ds.code != kLowerOnHost) return report(ds);
+  }
+  trs_format* hf = nullptr;
+  if (const int rc = trs_dformat_download(f, &hf); rc != TRS_OK) return rc;
+  trs_plan_options h = o;
+  h.host_lowering = 1;
+  const int rc = sddmm ? trs_plan_create_sddmm(hf, m, n, &h, out) : trs_plan_create(hf, m, n, &h, out);
+  trs_format_free(hf);
+  return rc;
+}
+
+int trs_plan_create_dformat(const trs_dformat* f, int32_t m, int32_t n, const trs_plan_options* opt, trs_plan** out) {
+  return plan_from_dformat(f, m, n, opt, false, out, "trs_plan_create_dformat");
+}
+
+int trs_plan_create_sddmm_dformat(const trs_dformat* f, int32_t m, int32_t n, const trs_plan_options* opt,
+                                  trs_plan** out) {
+  return plan_from_dformat(f, m, n, opt, true, out, "trs_plan_create_sddmm_dformat");
 }
 
 int trs_plan_create_parallel(const trs_parallel_arrays* a, const trs_plan_options* opt, trs_plan** out) {

@@ -89,6 +89,8 @@ PROTOTYPES = {
                                             ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_csr": (c_i32, [c_p, c_p, c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_create_sddmm": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
+    "trs_plan_create_dformat": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
+    "trs_plan_create_sddmm_dformat": (c_i32, [c_p, c_i32, c_i32, ctypes.POINTER(PlanOptions), c_pp]),
     "trs_plan_stats_get": (c_i32, [c_p, ctypes.POINTER(PlanStats), c_i64]),
     "trs_plan_free": (None, [c_p]),
     "trs_spmm_workspace_bytes": (c_i64, [c_p, c_i32]),

@@ -9,7 +9,7 @@ from __future__ import annotations
 import ctypes
 import hashlib
 import os
-from typing import Optional, Sequence
+from typing import Optional, Sequence, Union
 
 import numpy as np
 import torch
@@ -298,7 +298,7 @@ class Plan:
             self._h = ctypes.c_void_p(0)
 
     @classmethod
-    def from_format(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
+    def from_format(cls, fmt: Union[Format, "DeviceFormat"], m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
                     sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                     feature_lanes: Optional[int] = None, streaming: Optional[int] = None,
                     window_row_cap: Optional[int] = None, xcd_run: Optional[int] = None,
@@ -306,7 +306,8 @@ class Plan:
                     xcd_split: Optional[int] = None, host_lowering: bool = False,
                     sptc_sparse: bool = True, hot_rows: Optional[int] = None,
                     split_dispatch: Optional[int] = None) -> "Plan":
-        """Plan over the builder output (all shares + spill).  Tuning options: see trs_plan_options
+        """Plan over the builder output (all shares + spill); a :class:`DeviceFormat` is lowered
+        where it lives (trs_plan_create_dformat: the plan equals that of its downloaded format).  Tuning options: see trs_plan_options
         in include/trspmm.h (None keeps the library default).  host_lowering=True builds the
         residual on the host even when the format holds its input CSR (the plan is the same);
         sptc_sparse=False runs 2:4 tiles on the dense MFMA with zero fill instead of the sparse one."""
@@ -317,11 +318,12 @@ class Plan:
         o.host_lowering = int(bool(host_lowering))
         o.sptc_sparse = int(bool(sptc_sparse))
         h = ctypes.c_void_p()
-        nat.check(nat.lib().trs_plan_create(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), "trs_plan_create")
+        fn = "trs_plan_create_dformat" if isinstance(fmt, DeviceFormat) else "trs_plan_create"
+        nat.check(getattr(nat.lib(), fn)(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), fn)
         return cls(h.value)
 
     @classmethod
-    def for_sddmm(cls, fmt: Format, m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
+    def for_sddmm(cls, fmt: Union[Format, "DeviceFormat"], m: int, n: int, mfma_tc: bool = True, mfma_sptc: bool = True,
                   sptc_min_fill: float = 0.25, task_nnz: int = 0, piece_nnz: Optional[int] = None,
                   feature_lanes: Optional[int] = None, xcd_run: Optional[int] = None,
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
@@ -331,14 +333,15 @@ class Plan:
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
         residual outputs with non-temporal stores.  host_lowering=True builds the residual on the
-        host even when the format holds its input CSR (the plan is the same)."""
+        host even when the format holds its input CSR (the plan is the same).  A
+        :class:`DeviceFormat` is lowered where it lives (trs_plan_create_sddmm_dformat)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
                      streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows, split_dispatch=split_dispatch)
         o.host_lowering = int(bool(host_lowering))
         h = ctypes.c_void_p()
-        nat.check(nat.lib().trs_plan_create_sddmm(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)),
-                  "trs_plan_create_sddmm")
+        fn = "trs_plan_create_sddmm_dformat" if isinstance(fmt, DeviceFormat) else "trs_plan_create_sddmm"
+        nat.check(getattr(nat.lib(), fn)(fmt.handle, m, n, ctypes.byref(o), ctypes.byref(h)), fn)
         return cls(h.value)
 
     @classmethod
