@@ -254,7 +254,8 @@ def bench_sddmm(args, workload, g, K):
     t0 = time.time()
     plan, pre = build_and_plan(args, g, True, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
                                feature_lanes=args.feature_lanes, hot_rows=args.hot_rows,
-                               split_dispatch=int(args.split_dispatch), sddmm_unroll=args.sddmm_unroll)
+                               split_dispatch=int(args.split_dispatch), sddmm_unroll=args.sddmm_unroll,
+                               occupancy=args.occupancy)
     st = plan.stats()
     log(f"[bench] sddmm plan {st} ({time.time() - t0:.1f}s)")
     Xh = graphs.dense_operand(g.m, K, seed=4)
@@ -377,6 +378,8 @@ def main():
                          "default: the library's)")
     ap.add_argument("--sddmm-unroll", type=int, default=None,
                     help="plan option sddmm_unroll (SDDMM entries in flight per lane group: 4 or 8)")
+    ap.add_argument("--occupancy", type=int, default=None,
+                    help="plan option occupancy (residual task kernels held to N waves per SIMD; -1 uncapped)")
     ap.add_argument("--split-dispatch", action="store_true",
                     help="plan option split_dispatch: the XCD split part as its own launch (per-part profiles)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -414,7 +417,8 @@ def main():
     t0 = time.time()
     plan, built = build_and_plan(args, g, False, xcd_split=args.xcd_split, host_lowering=args.host_lowering,
                                  window_row_cap=args.window_row_cap, feature_lanes=args.feature_lanes,
-                                 hot_rows=args.hot_rows, split_dispatch=int(args.split_dispatch))
+                                 hot_rows=args.hot_rows, split_dispatch=int(args.split_dispatch),
+                                 occupancy=args.occupancy)
     pre.update(built)
     if "reorder_s" in pre:
         pre["reorder_s"] = round(pre["reorder_s"], 3)

@@ -28,8 +28,10 @@
 #include <stdint.h>
 
 /* 1: first release; 2: plan options xcd_split .. hot_rows, reorder minhash, wider plan stats;
- * 3: struct_size fields and the stats size argument. */
-#define TRSPMM_ABI_VERSION 3
+ * 3: struct_size fields and the stats size argument; 4: the GPU format builder
+ * (trs_build_online_device, trs_dformat_*) and plans from its output (trs_plan_create_dformat,
+ * trs_plan_create_sddmm_dformat); struct layouts as in 3. */
+#define TRSPMM_ABI_VERSION 4
 
 #ifdef __cplusplus
 extern "C" {
@@ -227,14 +229,14 @@ typedef struct trs_plan_options {
                              consecutive work items in a row; 1 = hardware round robin,
                              0 = automatic */
   int32_t sddmm_unroll;   /* SDDMM residual entries in flight per lane group: 4 or 8; 0 = automatic
-                             (8) */
+                             (4 for passes of exactly 128 features with 16-byte loads, else 8) */
   int32_t stage;          /* a residual task's column ids (and values) are copied into LDS once
                              before its gathers: 0 = automatic (16-lane groups, i.e. K = 65..128,
                              and tasks of <= 256 entries), -1 = never */
-  int32_t occupancy;      /* waves per SIMD the residual SpMM task kernel may hold (2..8; values
+  int32_t occupancy;      /* waves per SIMD the residual task kernels may hold (2..8; values
                              outside are clamped): fewer concurrent tasks keep fewer gathered rows
-                             in flight.  0 = automatic (2 for K <= 64, uncapped above), -1 =
-                             uncapped (as many as registers and LDS allow) */
+                             in flight.  0 = automatic (SpMM: 2 for K <= 64, uncapped above;
+                             SDDMM: uncapped), -1 = uncapped (as many as registers and LDS allow) */
   int32_t xcd_split;      /* XCD column split: the columns are divided among the 8 XCDs by a hash
                              and residual rows with at least this many entries are cut into one
                              sub-row per XCD, run by that XCD's workgroups (workgroup i runs on XCD

@@ -849,6 +849,12 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[U], int li) {
 // acc: add to the outputs instead of writing them (a later feature pass of the same entries).
 // HOT: P.col is the hot-renumbered copy and negative ids gather Y rows from the staged rows
 // P.hot_b.
+// Static LDS of k_sddmm_tasks<.., LPG, .., LS>: the row-pointer slices and, when staged, the
+// column id slices (the arrays it declares; checked there).
+constexpr size_t sddmm_static_lds(int lpg, bool ls) {
+  return (size_t)4 * (64 / lpg) * (kTaskRows + 1) * 4 + (ls ? (size_t)4 * (64 / lpg) * kStageSpan * 4 : 16);
+}
+
 template <int VEC, int LPG, int U, bool LS, bool SPF = false, bool NTO = false, bool HOT = false>
 __device__ __forceinline__ void sddmm_tasks_run(const DevicePlan& P, int block, int nblocks,
                                                 const uint16_t* __restrict__ X, int64_t ldx,
@@ -859,6 +865,8 @@ __device__ __forceinline__ void sddmm_tasks_run(const DevicePlan& P, int block, 
   constexpr int UB = U < LPG ? U : LPG;        // entries per reduce_scatter batch
   __shared__ int s_rp[4][GPW][kTaskRows + 1];
   __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
+  static_assert(sizeof(s_rp) + sizeof(s_col) == sddmm_static_lds(LPG, LS),
+                "sddmm_static_lds must describe this kernel's LDS (the occupancy cap depends on it)");
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int grp = lane / LPG;
@@ -1385,8 +1393,12 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     // 16-byte runs, as 4-lane groups write at K=16, lose: 0.418 -> 0.469)
     const bool ls = p.task_max <= kStageMax && p.stage >= 0 && (x.ntasks <= 0 || x.task_max <= kStageMax);
     const bool nto = (p.streaming & 2) != 0;
-#define TRS_SD_LAUNCH(...) \
-  hipLaunchKernelGGL((k_sddmm_tasks<__VA_ARGS__>), grid, dim3(256), 0, s, p, x, gm, Xp, ldx, Yp, ldy, Kp, out, xout, acc)
+    // occupancy: uncapped unless the plan asks (option occupancy: waves per SIMD, held by unused
+    // dynamic LDS)
+    const int waves = p.occupancy > 0 ? p.occupancy : 0;
+#define TRS_SD_LAUNCH(VV, LL, UU, LSV, ...)                                                               \
+  hipLaunchKernelGGL((k_sddmm_tasks<VV, LL, UU, LSV, ##__VA_ARGS__>), grid, dim3(256),                    \
+                     occupancy_pad(sddmm_static_lds(LL, LSV), waves), s, p, x, gm, Xp, ldx, Yp, ldy, Kp, out, xout, acc)
 #define TRS_SD_U(L, U)                                                                                     \
     constexpr bool nt_ok = (U < L ? U : L) >= 8;                                                           \
     if constexpr (L == 16) {                                                                               \
@@ -1408,9 +1420,13 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     }                                                                                                      \
     if (nt_ok && nto) TRS_SD_LAUNCH(VEC, L, U, false, (L <= 8), nt_ok);                                    \
     else TRS_SD_LAUNCH(VEC, L, U, false, (L <= 8));
+    // entries in flight per lane group: 4 where a 16-lane group's 16-byte loads cover 128 features,
+    // 8 elsewhere (same-box A/B on the R-MAT 2^20 pattern, 8 -> 4: K = 128 0.726 -> 0.705 ms, K = 256
+    // (two passes of 128) 1.544 -> 1.482; K = 96 0.689 -> 0.720, K = 32 0.380 -> 0.488)
+    const bool u4 = p.sddmm_unroll == 4 || (p.sddmm_unroll == 0 && VEC == 8 && lpg == 16 && Kp == 128);
 #define TRS_SD(L)                                                                                          \
   case L:                                                                                                  \
-    if (p.sddmm_unroll == 4) {                                                                             \
+    if (u4) {                                                                                              \
       TRS_SD_U(L, 4)                                                                                       \
     } else {                                                                                               \
       TRS_SD_U(L, 8)                                                                                       \

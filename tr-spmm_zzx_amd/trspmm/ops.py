@@ -329,7 +329,7 @@ class Plan:
                   sddmm_unroll: Optional[int] = None, stage: Optional[int] = None,
                   streaming: Optional[int] = None, xcd_split: Optional[int] = None,
                   host_lowering: bool = False, hot_rows: Optional[int] = None,
-                  split_dispatch: Optional[int] = None) -> "Plan":
+                  split_dispatch: Optional[int] = None, occupancy: Optional[int] = None) -> "Plan":
         """SDDMM plan on the hybrid tiling (dense tiles on MFMA, rest as CSR dot products);
         ``sddmm`` outputs follow the input CSR order.  ``streaming`` bit 1 (default on) writes the
         residual outputs with non-temporal stores.  host_lowering=True builds the residual on the
@@ -337,7 +337,8 @@ class Plan:
         :class:`DeviceFormat` is lowered where it lives (trs_plan_create_sddmm_dformat)."""
         o = _options(mfma_tc, mfma_sptc, sptc_min_fill, task_nnz, piece_nnz=piece_nnz,
                      feature_lanes=feature_lanes, xcd_run=xcd_run, sddmm_unroll=sddmm_unroll, stage=stage,
-                     streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows, split_dispatch=split_dispatch)
+                     streaming=streaming, xcd_split=xcd_split, hot_rows=hot_rows, split_dispatch=split_dispatch,
+                     occupancy=occupancy)
         o.host_lowering = int(bool(host_lowering))
         h = ctypes.c_void_p()
         fn = "trs_plan_create_sddmm_dformat" if isinstance(fmt, DeviceFormat) else "trs_plan_create_sddmm"
