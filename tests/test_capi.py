@@ -62,25 +62,25 @@ class _GuardedBuffer:
         return self.buf.raw[self.size:] == b"\xa5" * 256
 
 
-def _round1_plan_options() -> bytes:
-    """The 12-field trs_plan_options of the first header (mfma_tc .. occupancy), defaults."""
+def _v1_plan_options() -> bytes:
+    """The 12-field trs_plan_options of ABI version 1 (mfma_tc .. occupancy), defaults."""
     import struct
     return struct.pack("<iifiiiiiiiii", 1, 1, 0.25, 0, 0, 0, -1, 0, 0, 0, 0, 0)
 
 
-def _round2_plan_options() -> bytes:
-    """The 16-field trs_plan_options of the second header (no struct_size), defaults."""
+def _v2_plan_options() -> bytes:
+    """The 16-field trs_plan_options of ABI version 2 (no struct_size), defaults."""
     import struct
     return struct.pack("<iifiiiiiiiiiiiii", 1, 1, 0.25, 0, 0, 0, -1, 0, 0, 0, 0, 0, 0, 0, 1, 0)
 
 
-@pytest.mark.parametrize("layout", ["round1", "round2"])
+@pytest.mark.parametrize("layout", ["abi_v1", "abi_v2"])
 def test_older_plan_options_layouts_are_refused(layout):
     """A caller compiled against an earlier header passes a shorter options struct without
     struct_size: every plan constructor refuses it with TRS_EINVAL (its first field, mfma_tc = 1,
     is no valid size) before reading past that field.  No GPU is touched: the check comes first."""
     lib = nat.lib()
-    blob = _round1_plan_options() if layout == "round1" else _round2_plan_options()
+    blob = _v1_plan_options() if layout == "abi_v1" else _v2_plan_options()
     g = _GuardedBuffer(len(blob), blob)
     rowptr = np.array([0, 1], np.int32)
     col = np.array([0], np.int32)
@@ -115,7 +115,7 @@ def test_older_build_and_reorder_params_are_refused():
 
 @pytest.mark.parametrize("stats_bytes", [12 * 8, 16 * 8 - 8, 16 * 8 + 8])
 def test_plan_stats_of_another_size_are_refused(stats_bytes):
-    """trs_plan_stats_get checks the caller's stats size (12 fields in the first header) before
+    """trs_plan_stats_get checks the caller's stats size (12 fields in ABI version 1) before
     anything else, so the check is visible without a plan (GPU); with a real plan it is repeated in
     tests/test_gpu_operators.py."""
     lib = nat.lib()
