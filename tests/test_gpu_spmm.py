@@ -300,7 +300,7 @@ def test_pipelined_and_plain_streams(K, task_nnz):
 def test_staged_and_unstaged_streams_agree(K):
     """16-lane groups (K = 65..128) stage each task's column ids and values in LDS when every task
     holds <= 256 entries.  Tasks here start at every offset mod 8 and hold up to 256 entries; one
-    row of 280 entries is split in two pieces by the default plan (staged) and kept whole with
+    row of 280 entries is split in two pieces with piece_nnz = 256 (staged) and kept whole with
     piece_nnz = 300 (a 280-entry task: the plan falls back to the unstaged stream).  Both against
     the oracle; every other row is summed in the same order, so bitwise equal."""
     say("staged", K)
@@ -316,7 +316,7 @@ def test_staged_and_unstaged_streams_agree(K):
     Bh = dense_B(n, K, seed=5)
     R = osp.csr_spmm(rowptr, cols, val, Bh, m=m)
     opts = dict(mfma_tc=False, mfma_sptc=False, task_nnz=128, xcd_split=-1)
-    staged = trspmm.Plan.from_format(f, m, n, **opts)
+    staged = trspmm.Plan.from_format(f, m, n, piece_nnz=256, **opts)
     whole = trspmm.Plan.from_format(f, m, n, piece_nnz=300, **opts)
     assert staged.stats()["split_rows"] == 1 and whole.stats()["split_rows"] == 0
     C1 = run_plan(staged, Bh)
@@ -326,7 +326,7 @@ def test_staged_and_unstaged_streams_agree(K):
     keep = np.arange(m) != 1234
     assert np.array_equal(C1[keep], C2[keep])
     # the same plan with staging switched off (stage = -1): every row bitwise equal
-    C3 = run_plan(trspmm.Plan.from_format(f, m, n, stage=-1, **opts), Bh)
+    C3 = run_plan(trspmm.Plan.from_format(f, m, n, piece_nnz=256, stage=-1, **opts), Bh)
     assert np.array_equal(C1, C3)
 
 

@@ -685,6 +685,9 @@ struct Tasks {
   Status st;
 };
 
+// Residual tasks a plan aims at when the automatic task size leaves fewer (small matrices).
+constexpr int64_t kMinTasks = 16384;
+
 // Longest tasks first (a stable counting sort on the entry count, which never exceeds the piece
 // length): a workgroup's lane groups then carry tasks of similar length, so none idles while a
 // longer one finishes (R-MAT K = 32 / 64 / 128: -9% / -11% / -5%).
@@ -714,8 +717,14 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
     const double mean = nonempty ? (double)nent / (double)nonempty : 1.0;
     S = (int)std::min(128.0, std::max(32.0, 4.0 * mean));
   }
+  // Small matrices: fewer than kMinTasks tasks leave most lane groups of the chip idle while the
+  // rest walk long task streams one batch round trip after another, so automatic sizes shrink to
+  // reach kMinTasks (tasks of at least 16 entries, pieces of 64).  Measured on MI355X, R-MAT 2^14
+  // (426K entries) K = 64: 75 -> 42 us per call; R-MAT 2^20 (31.4M entries) is far above the bar.
+  const bool small = nent / S < kMinTasks;
+  if (opt.task_nnz <= 0 && small) S = (int)std::max<int64_t>(16, std::min<int64_t>(S, nent / kMinTasks));
   T.task_nnz = S;
-  const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : 256);
+  const int piece_max = std::max(S, opt.piece_nnz > 0 ? opt.piece_nnz : small ? 64 : 256);
   const int rows_cap = trs::kTaskRows;
   auto is_owned = [&](int32_t r) { return !owned.empty() && owned[r / 16]; };
   const int32_t J = P.J();

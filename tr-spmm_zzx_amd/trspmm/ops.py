@@ -278,8 +278,12 @@ def _stream_ptr(stream) -> int:
 def _on_current_device(name: str, t: torch.Tensor) -> None:
     """Plans are bound to the device they were created on, which the C ABI requires to be the
     current one (TRS_EDEVICE otherwise); operands on another GPU are refused here."""
-    if t.device.index != torch.cuda.current_device():
-        raise ValueError(f"{name} is on {t.device}, not on the current device cuda:{torch.cuda.current_device()}")
+    _on_device(name, t, torch.cuda.current_device())
+
+
+def _on_device(name: str, t: torch.Tensor, dev: int) -> None:
+    if t.device.index != dev:
+        raise ValueError(f"{name} is on {t.device}, not on the current device cuda:{dev}")
 
 
 class Plan:
@@ -287,6 +291,8 @@ class Plan:
 
     def __init__(self, handle: int):
         self._h = ctypes.c_void_p(handle)
+        self._dims = None    # (m, n, nnz): a plan is immutable, so read once
+        self._ws = {}        # ("spmm" | "sddmm", K) -> workspace bytes
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -379,40 +385,60 @@ class Plan:
         return {k: int(getattr(s, k)) for k, _ in nat.PlanStats._fields_}
 
     def workspace_bytes(self, K: int) -> int:
-        return int(nat.lib().trs_spmm_workspace_bytes(self._h, K))
+        key = ("spmm", K)
+        if key not in self._ws:
+            self._ws[key] = int(nat.lib().trs_spmm_workspace_bytes(self._h, K))
+        return self._ws[key]
+
+    def _shape(self):
+        if self._dims is None:
+            st = self.stats()
+            self._dims = (st["m"], st["n"], st["nnz"])
+        return self._dims
+
+    @staticmethod
+    def _temporaries(stream, make):
+        """Allocate the call's temporaries on the launch stream (entered only when something is
+        allocated: the context switch costs more than the call's checks)."""
+        with torch.cuda.stream(_launch_stream(stream)):
+            return make()
 
     def spmm(self, B: torch.Tensor, out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
              stream=None) -> torch.Tensor:
         """C = A B for B [n, K] fp16 on the GPU; returns float32 [m, K].  Temporaries (a defaulted
         ``out`` or workspace) are allocated on the launch stream, so the caching allocator does not
         hand them to other work while the kernels on ``stream`` still use them."""
-        st = self.stats()
-        if not (B.is_cuda and B.dtype == torch.float16 and B.dim() == 2 and B.shape[0] == st["n"]):
-            raise ValueError(f"B must be a CUDA fp16 tensor of shape [{st['n']}, K]")
-        _on_current_device("B", B)
+        m, n, _ = self._shape()
+        if not (B.is_cuda and B.dtype == torch.float16 and B.dim() == 2 and B.shape[0] == n):
+            raise ValueError(f"B must be a CUDA fp16 tensor of shape [{n}, K]")
+        dev = torch.cuda.current_device()
+        _on_device("B", B, dev)
         if B.stride(1) != 1:
             B = B.contiguous()
         K = B.shape[1]
         need = self.workspace_bytes(K)
-        with torch.cuda.stream(_launch_stream(stream)):
-            if out is None:
-                out = torch.empty((st["m"], K), dtype=torch.float32, device=B.device)
-            if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-                workspace = torch.empty(need, dtype=torch.uint8, device=B.device)
-        if not (out.is_cuda and out.dtype == torch.float32 and tuple(out.shape) == (st["m"], K) and out.stride(1) == 1):
+        new_ws = need and (workspace is None or workspace.numel() * workspace.element_size() < need)
+        if out is None or new_ws:
+            out, workspace = self._temporaries(stream, lambda: (
+                out if out is not None else torch.empty((m, K), dtype=torch.float32, device=B.device),
+                torch.empty(need, dtype=torch.uint8, device=B.device) if new_ws else workspace))
+        if not (out.is_cuda and out.dtype == torch.float32 and tuple(out.shape) == (m, K) and out.stride(1) == 1):
             raise ValueError("out must be a CUDA float32 tensor [m, K] with unit column stride")
-        _on_current_device("out", out)
+        _on_device("out", out, dev)
         if need:
             if not (workspace.is_cuda and workspace.is_contiguous()):
                 raise ValueError("workspace must be a contiguous CUDA tensor")
-            _on_current_device("workspace", workspace)
+            _on_device("workspace", workspace, dev)
         ws_ptr = workspace.data_ptr() if need else 0
         nat.check(nat.lib().trs_spmm_f16(self._h, B.data_ptr(), B.stride(0), K, out.data_ptr(), out.stride(0),
                                          ws_ptr, need, _stream_ptr(stream)), "trs_spmm_f16")
         return out
 
     def sddmm_workspace_bytes(self, K: int) -> int:
-        return int(nat.lib().trs_sddmm_workspace_bytes(self._h, K))
+        key = ("sddmm", K)
+        if key not in self._ws:
+            self._ws[key] = int(nat.lib().trs_sddmm_workspace_bytes(self._h, K))
+        return self._ws[key]
 
     def sddmm(self, X: torch.Tensor, Y: torch.Tensor, out: Optional[torch.Tensor] = None,
               workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
@@ -420,30 +446,31 @@ class Plan:
         ``out`` must be a contiguous float32 CUDA tensor of at least ``stats()['nnz']`` elements.
         Plans with staged hot rows take a workspace (``sddmm_workspace_bytes(K)``), allocated on the
         launch stream when not given."""
-        st = self.stats()
-        for name, t, rows in (("X", X, st["m"]), ("Y", Y, st["n"])):
+        m, n, nnz = self._shape()
+        dev = torch.cuda.current_device()
+        for name, t, rows in (("X", X, m), ("Y", Y, n)):
             if not (t.is_cuda and t.dtype == torch.float16 and t.dim() == 2 and t.shape[0] == rows):
                 raise ValueError(f"{name} must be a CUDA fp16 tensor with {rows} rows")
-            _on_current_device(name, t)
+            _on_device(name, t, dev)
         if X.shape[1] != Y.shape[1]:
             raise ValueError("X and Y need the same feature width")
         X = X if X.stride(1) == 1 else X.contiguous()
         Y = Y if Y.stride(1) == 1 else Y.contiguous()
         K = X.shape[1]
         need = self.sddmm_workspace_bytes(K)
-        with torch.cuda.stream(_launch_stream(stream)):
-            if out is None:
-                out = torch.empty(st["nnz"], dtype=torch.float32, device=X.device)
-            if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-                workspace = torch.empty(need, dtype=torch.uint8, device=X.device)
+        new_ws = need and (workspace is None or workspace.numel() * workspace.element_size() < need)
+        if out is None or new_ws:
+            out, workspace = self._temporaries(stream, lambda: (
+                out if out is not None else torch.empty(nnz, dtype=torch.float32, device=X.device),
+                torch.empty(need, dtype=torch.uint8, device=X.device) if new_ws else workspace))
         if not (isinstance(out, torch.Tensor) and out.is_cuda and out.dtype == torch.float32 and out.is_contiguous()
-                and out.numel() >= st["nnz"]):
-            raise ValueError(f"out must be a contiguous CUDA float32 tensor of at least {st['nnz']} elements")
-        _on_current_device("out", out)
+                and out.numel() >= nnz):
+            raise ValueError(f"out must be a contiguous CUDA float32 tensor of at least {nnz} elements")
+        _on_device("out", out, dev)
         if need:
             if not (workspace.is_cuda and workspace.is_contiguous()):
                 raise ValueError("workspace must be a contiguous CUDA tensor")
-            _on_current_device("workspace", workspace)
+            _on_device("workspace", workspace, dev)
         nat.check(nat.lib().trs_sddmm_f16_ws(self._h, X.data_ptr(), X.stride(0), Y.data_ptr(), Y.stride(0), K,
                                              out.data_ptr(), workspace.data_ptr() if need else 0, need,
                                              _stream_ptr(stream)), "trs_sddmm_f16_ws")
