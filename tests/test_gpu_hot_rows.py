@@ -328,3 +328,32 @@ def test_staged_rows_from_strided_operands(pad):
     sp = trspmm.Plan.for_sddmm(f, g.m, g.n, hot_rows=-1)
     X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=81)).cuda()
     assert torch.equal(sh.sddmm(X, B), sp.sddmm(X, B))
+
+
+def _brute_force_hot(col, n, want):
+    """The hot set the plan documents: among the columns gathered at least twice, the `want` first
+    in the order (count desc, column asc); returns (rows, their entries)."""
+    cnt = np.bincount(col, minlength=n)
+    cand = np.nonzero(cnt >= 2)[0]
+    order = cand[np.lexsort((cand, -cnt[cand]))][:want]
+    return len(order), int(cnt[order].sum())
+
+
+@pytest.mark.parametrize("name,gen,want", [
+    ("rmat16", lambda: graphs.rmat(scale=16, edge_factor=16, seed=21), 0),
+    ("rmat16_2048", lambda: graphs.rmat(scale=16, edge_factor=16, seed=21), 2048),
+    # many columns tied at each count: the cut falls inside a run of equal counts
+    ("ties", lambda: graphs.random_csr(30000, 20000, 0.0006, seed=9), 700),
+])
+def test_hot_selection_equals_brute_force(name, gen, want):
+    """The plan picks its hot rows through a histogram of the column counts; the rows and their
+    entries equal a plain sort's choice (no tiles, no split: every entry is a task entry)."""
+    g = gen()
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    s = trspmm.Plan.from_format(f, g.m, g.n, mfma_tc=False, mfma_sptc=False, xcd_split=-1,
+                                hot_rows=want).stats()
+    w = want if want > 0 else min(16384, g.n // 16)
+    nnz = int(g.rowptr[g.m])
+    rows, entries = _brute_force_hot(g.col[:nnz], g.n, w)
+    say("hot selection", name, s["hot_rows"], s["hot_entries"], rows, entries)
+    assert (s["hot_rows"], s["hot_entries"]) == (rows, entries)

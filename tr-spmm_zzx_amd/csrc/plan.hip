@@ -140,7 +140,8 @@ struct Lowering {
   std::vector<float> val;
   // MFMA tiles: row0, 16 columns, dense 16x16 values
   struct Tile { int32_t row0; int32_t cols[16]; float a[256]; uint64_t present[4]; int nnz; };
-  std::vector<Tile> tiles;
+  // (tiles are over 1 KB each and written whole: no zero-fill on resize)
+  trs::array<Tile> tiles;
   Status st;
   // Tiles only: entries outside tiles are not collected (the device lowering takes the residual
   // from the input CSR instead).
@@ -178,6 +179,8 @@ struct Lowering {
 };
 
 
+using TileVec = trs::array<Lowering::Tile>;
+
 float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // The private results of parallel lowering pieces, appended in piece order (sized once: a tile is
@@ -191,16 +194,26 @@ void append_parts(Lowering& L, std::vector<Lowering>& part, bool stop_at_error) 
   L.row.reserve(nr);
   L.col.reserve(nr);
   L.val.reserve(nr);
-  L.tiles.reserve(nt);
+  // the pieces' tiles land at their offsets, copied in parallel (a tile is over 1 KB)
+  std::vector<size_t> at;
+  size_t t0 = L.tiles.size();
   for (auto& q : part) {
     if (!q.st.ok() && L.st.ok()) L.st = q.st;
-    if (!q.st.ok() && stop_at_error) return;
+    if (!q.st.ok() && stop_at_error) break;
     L.row.insert(L.row.end(), q.row.begin(), q.row.end());
     L.col.insert(L.col.end(), q.col.begin(), q.col.end());
     L.val.insert(L.val.end(), q.val.begin(), q.val.end());
-    L.tiles.insert(L.tiles.end(), q.tiles.begin(), q.tiles.end());
-    std::vector<Lowering::Tile>().swap(q.tiles);
+    at.push_back(t0);
+    t0 += q.tiles.size();
   }
+  L.tiles.resize(t0);
+  parallel_parts((int)at.size(), (int64_t)at.size(), 2, [&](int t) { return (int64_t)t; },
+                 [&](int64_t b, int64_t e, int) {
+                   for (int64_t i = b; i < e; ++i) {
+                     std::copy(part[i].tiles.begin(), part[i].tiles.end(), L.tiles.begin() + at[i]);
+                     TileVec().swap(part[i].tiles);
+                   }
+                 });
 }
 
 // TC sub-blocks of parts [p_begin, p_end) -> MFMA tiles (pairs of sub-blocks of one part, 16
@@ -445,8 +458,8 @@ struct Blob {
   };
   std::vector<Piece> pieces;
   size_t total = 0;
-  template <class T>
-  size_t add(const std::vector<T>& v) {
+  template <class T, class A>
+  size_t add(const std::vector<T, A>& v) {
     return add_raw(v.data(), v.size() * sizeof(T));
   }
   // src = nullptr: a region the device fills (left as allocated)
@@ -970,13 +983,23 @@ Status upload(const Blob& blob, trs_plan*& P) {
 
 // Tiles by row0, equal row0 in their order: a stable sort of indices, then one gather (a tile is
 // over 1 KB, too large to move around in a sort).
-void sort_tiles(std::vector<Lowering::Tile>& tiles) {
+void sort_tiles(TileVec& tiles) {
   auto less = [&](const Lowering::Tile& a, const Lowering::Tile& b) { return a.row0 < b.row0; };
-  if (std::is_sorted(tiles.begin(), tiles.end(), less)) return;
+  const auto run = std::is_sorted_until(tiles.begin(), tiles.end(), less);
+  if (run == tiles.end()) return;
   std::vector<int32_t> order(tiles.size());
   std::iota(order.begin(), order.end(), 0);
-  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return tiles[a].row0 < tiles[b].row0; });
-  std::vector<Lowering::Tile> sorted(tiles.size());
+  auto by_row0 = [&](int32_t a, int32_t b) { return tiles[a].row0 < tiles[b].row0; };
+  const size_t k = (size_t)(run - tiles.begin());
+  if (std::is_sorted(run, tiles.end(), less)) {
+    // two sorted runs (TC tiles, then the 2:4 group tiles): a stable merge of their indices
+    std::vector<int32_t> merged(tiles.size());
+    std::merge(order.begin(), order.begin() + k, order.begin() + k, order.end(), merged.begin(), by_row0);
+    order.swap(merged);
+  } else {
+    std::stable_sort(order.begin(), order.end(), by_row0);
+  }
+  TileVec sorted(tiles.size());
   parallel_tiles((int64_t)tiles.size(), [&](int64_t b, int64_t e, int) {
     for (int64_t i = b; i < e; ++i) sorted[i] = tiles[order[i]];
   });
@@ -1006,7 +1029,7 @@ struct Quads {
 // columns) the present entries, at most 2, take the group's two slots in column order; a single
 // entry is paired with a zero at another position (position 1 if it sits at 0, else 0), an empty
 // group with zeros at 0 and 1, so every slot pair names two distinct positions in ascending order.
-void add_quad(Quads& Q, const std::vector<Lowering::Tile>& tiles, size_t b, size_t e) {
+void add_quad(Quads& Q, const TileVec& tiles, size_t b, size_t e) {
   const size_t q = (size_t)Q.count++;
   Q.cols.resize((q + 1) * 64, -1);
   Q.a.resize((q + 1) * 64 * 8, 0);
@@ -1077,7 +1100,7 @@ struct DeviceOut {
 // their flagged entries, split rows scattered into their XCD sub-rows.  Outputs follow the input
 // CSR order, so an entry's output index is its CSR index.  Temporaries live in one allocation
 // freed before returning.
-Status residual_on_device(const CsrSource& f, int32_t m, const std::vector<Lowering::Tile>& tiles,
+Status residual_on_device(const CsrSource& f, int32_t m, const TileVec& tiles,
                           int64_t expect_marked, const Placement& PL, const DeviceOut& o) {
   const int32_t rows = std::min(m, f.rows);
   const int64_t cnnz = f.rowptr[rows];
@@ -1208,7 +1231,7 @@ Status input_rows(const CsrSource& src, Lowering& L, std::vector<int32_t>& csr_l
 
 // Residual row pointers of the device lowering: the input rows minus the tiles' entries; a
 // negative length means the tiles hold entries the input CSR lacks.
-Status residual_rows(const std::vector<int32_t>& csr_len, const std::vector<Lowering::Tile>& tiles, int32_t m,
+Status residual_rows(const std::vector<int32_t>& csr_len, const TileVec& tiles, int32_t m,
                      std::vector<int32_t>& rowptr, int64_t* tile_entries) {
   std::vector<int32_t> len(csr_len);
   int64_t te = 0;
@@ -1256,17 +1279,38 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
     return done(fail(TRS_EDEVICE, "hot rows: column count failed"));
   // the task kernels' gathers: every entry but the window rows' residual entries
   const int64_t task_entries = total - P->stats.window_csr_nnz;
-  // a column gathered once gains nothing from a copy
-  std::vector<int32_t> hot;
+  // The `want` first columns in the order (count desc, column asc) among those gathered at least
+  // twice (a column gathered once gains nothing from a copy), found through a histogram of the
+  // counts: every column above the cut count t, then those at t in column order.  Counts from
+  // kCountCap on share the histogram's last bucket and are ordered by a sort of their own.
+  constexpr int32_t kCountCap = 1 << 16;
+  std::vector<int64_t> hc((size_t)kCountCap + 1, 0);
   for (int32_t c = 0; c < n; ++c)
-    if (cnt[c] >= 2) hot.push_back(c);
+    if (cnt[c] >= 2) hc[(size_t)std::min(cnt[c], kCountCap)]++;
+  int64_t taken = 0, hot_entries = 0;
+  int32_t t = kCountCap;   // the lowest count taken in full is above t
+  for (; t >= 2 && taken + hc[(size_t)t] <= want; --t) taken += hc[(size_t)t];
   auto before = [&](int32_t a, int32_t b) { return cnt[a] != cnt[b] ? cnt[a] > cnt[b] : a < b; };
-  if ((int64_t)hot.size() > want) {
+  std::vector<int32_t> hot;
+  hot.reserve((size_t)std::min<int64_t>(want, n));
+  if (t == kCountCap && hc[(size_t)kCountCap] > want) {
+    // more capped columns than wanted: take them all and cut by the exact order
+    for (int32_t c = 0; c < n; ++c)
+      if (cnt[c] >= kCountCap) hot.push_back(c);
     std::nth_element(hot.begin(), hot.begin() + want, hot.end(), before);
     hot.resize((size_t)want);
+  } else {
+    int64_t at_t = t >= 2 ? want - taken : 0;   // columns of count t still taken, lowest ids first
+    for (int32_t c = 0; c < n; ++c) {
+      const int32_t v = std::min(cnt[c], kCountCap);
+      if (v > t && v >= 2) hot.push_back(c);
+      else if (v == t && v >= 2 && at_t > 0) {
+        hot.push_back(c);
+        --at_t;
+      }
+    }
   }
   std::sort(hot.begin(), hot.end(), before);
-  int64_t hot_entries = 0;
   for (int32_t c : hot) hot_entries += cnt[c];
   if (hot.empty() || (opt.hot_rows == 0 && hot_entries * 10 < task_entries * kHotMinShare10)) return done(Status{});
   std::vector<int32_t> rank((size_t)n, -1);
@@ -1359,7 +1403,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
       any_demote |= demote[b] != 0;
     }
     if (any_demote) {
-      std::vector<Lowering::Tile> kept;
+      TileVec kept;
       for (const auto& t : L.tiles) {
         if (!demote[t.row0 / 16]) { kept.push_back(t); continue; }
         owned[t.row0 / 16] = 0;
@@ -1418,8 +1462,8 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
     mwin.push_back({L.tiles[i].row0, (int32_t)i, (int32_t)dense_end, 0});
     i = j;
   }
-  std::vector<int32_t> tile_cols(L.tiles.size() * 16);
-  std::vector<uint16_t> tile_a(L.tiles.size() * 256);
+  trs::array<int32_t> tile_cols(L.tiles.size() * 16);   // written whole below, in parallel
+  trs::array<uint16_t> tile_a(L.tiles.size() * 256);
   int64_t mfma_nnz = 0;
   for (const auto& t : L.tiles) mfma_nnz += t.nnz;
   parallel_tiles((int64_t)L.tiles.size(), [&](int64_t b, int64_t e, int) {
@@ -1703,7 +1747,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
     o.merge_off = &merge_off;
     o.tile_pos = with_pos ? reinterpret_cast<int32_t*>(base + o_tpos) : nullptr;
     o.compact = false;
-    const Status ds = residual_on_device(*src, m, with_pos ? L.tiles : std::vector<Lowering::Tile>{}, expect_marked, PL, o);
+    const Status ds = residual_on_device(*src, m, with_pos ? L.tiles : TileVec{}, expect_marked, PL, o);
     if (!ds.ok()) {
       delete P;
       return ds;
@@ -1780,6 +1824,11 @@ void lower_format(Lowering& L, const trs_format& f, const trs_plan_options& o) {
 
 // The tiles of a builder output only (L.tiles_only): the shares that can become MFMA tiles.
 void lower_format_tiles(Lowering& L, const trs_format& f, const trs_plan_options& o) {
+  // room for every tile (see lower_dformat_tiles)
+  int64_t room = f.window == 16 && o.mfma_sptc ? (int64_t)f.tile_win.size() : 0;
+  for (size_t p = 0; p < f.t_winrow.size() && o.mfma_tc; ++p)
+    if (f.t_winrow[p] >= 0 && f.t_winrow[p] % 16 == 0) room += (f.t_rowoff[p + 1] - f.t_rowoff[p] + 1) / 2;
+  L.tiles.reserve((size_t)room);
   lower_tc(L, f.t_rowoff.data(), (int64_t)f.t_winrow.size(), f.t_blockoff.data(), f.t_col.data(), f.t_val.data(),
            nullptr, (int64_t)f.t_val.size(), f.t_winrow.data(), f.t_bin.data(), o.mfma_tc != 0);
   lower_groups(L, f.s_col.data(), f.s_val.data(), f.s_pos.data(), (int64_t)f.s_win.size(), f.s_win.data(),
@@ -1802,6 +1851,12 @@ Status lower_dformat_tiles(Lowering& L, const trs_dformat& f, const trs_plan_opt
     if (!fetch(0, t_rowoff) || !fetch(1, t_blockoff) || !fetch(2, t_col) || !fetch(3, t_val) || !fetch(4, t_winrow) ||
         !fetch(6, t_bin))
       return fail(TRS_EDEVICE, "device format: TC array download failed");
+    // room for every tile this lowering can make (pairs of sub-blocks of 16-row parts, and the
+    // group tiles), so appending the group tiles does not move the TC tiles (over 1 KB each)
+    int64_t room = f.window == 16 && o.mfma_sptc ? f.slot[23].numel : 0;
+    for (size_t p = 0; p + 1 < t_rowoff.size() && o.mfma_tc; ++p)
+      if (t_winrow[p] >= 0 && t_winrow[p] % 16 == 0) room += (t_rowoff[p + 1] - t_rowoff[p] + 1) / 2;
+    L.tiles.reserve((size_t)room);
     lower_tc(L, t_rowoff.data(), (int64_t)t_winrow.size(), t_blockoff.data(), t_col.data(), t_val.data(), nullptr,
              (int64_t)t_val.size(), t_winrow.data(), t_bin.data(), o.mfma_tc != 0);
     if (!L.st.ok()) return L.st;
