@@ -213,9 +213,12 @@ typedef struct trs_plan_options {
   int32_t mfma_tc;        /* 1: TC sub-blocks run on MFMA tiles; 0: lowered to the CSR residual */
   int32_t mfma_sptc;      /* 1: 2:4 group tiles whose fill >= sptc_min_fill run on MFMA */
   float sptc_min_fill;    /* fill threshold (nnz / 256 slots of a 16x16 tile) for mfma_sptc */
-  int32_t task_nnz;       /* residual nnz per lane-group task packing short rows (0 = automatic) */
+  int32_t task_nnz;       /* residual nnz per lane-group task packing short rows (0 = automatic:
+                             about four mean rows, 32..128, and smaller -- down to 16 -- where
+                             that leaves fewer than 16,384 tasks) */
   int32_t piece_nnz;      /* longest residual run one lane group walks; longer rows are split
-                             into pieces summed by the fixup kernel (0 = automatic) */
+                             into pieces summed by the fixup kernel (0 = automatic: 256, or 64
+                             where the automatic task size leaves fewer than 16,384 tasks) */
   int32_t feature_lanes;  /* lanes per lane group (power of two <= 64; each lane holds 8 features):
                              fewer lanes = several feature passes with a smaller B working set
                              per pass (0 = automatic) */
