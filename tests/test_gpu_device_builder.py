@@ -171,3 +171,43 @@ def test_device_builder_full_size(name, gen, golden_env):
     say("  device build", round(df.elapsed, 4), "s")
     hf = host_build(g.rowptr, g.col, g.val, DEFAULT)
     assert_same_format(df, hf, name)
+
+
+def random_structured(seed):
+    """A seeded random matrix with dense rectangles (TC chunks and 2:4 groups of every fill) over
+    a uniform background, in a random shape, with random builder parameters."""
+    rng = np.random.default_rng(seed)
+    window = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 11, 13, 16, 16, 16]))
+    m, n = int(rng.integers(1, 3000)), int(rng.integers(1, 5000))
+    keys = [rng.integers(0, m * n, size=int(rng.integers(0, 4 * m + 1)), dtype=np.int64)]
+    for _ in range(int(rng.integers(0, 12))):
+        r0, c0 = int(rng.integers(0, m)), int(rng.integers(0, n))
+        h, w = int(rng.integers(1, 48)), int(rng.integers(1, 64))
+        rr, cc = np.meshgrid(np.arange(r0, min(m, r0 + h)), np.arange(c0, min(n, c0 + w)), indexing="ij")
+        keep = rng.random(rr.shape) < rng.uniform(0.3, 1.0)
+        keys.append(rr[keep].astype(np.int64) * n + cc[keep])
+    keys = np.unique(np.concatenate(keys))
+    m_pad = graphs.pad_rows(m, window)
+    rowptr, col = graphs.csr_from_keys(keys, m, n, m_pad)
+    val = rng.uniform(-1, 1, col.shape[0]).astype(np.float16).astype(np.float32)
+    p = dict(part_t=int(rng.integers(1, 40)), part_c=int(rng.integers(1, 40)), short_size=int(rng.integers(0, 6)),
+             density=int(rng.integers(1, window + 2)), window=window,
+             tc_min_util=float(rng.choice([0.0, 0.0, 0.3, 0.7])))
+    return graphs.Graph(f"rs{seed}", m, n, rowptr, col, val), p
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_device_builder_random_structured(seed, golden_env):
+    """Random shapes, windows of 1..16 rows and random builder parameters: all 32 slots equal the
+    host builder's; for 16-row windows the plan from the device format equals the plan from its
+    download (statistics and SpMM output bitwise)."""
+    golden_env({})
+    g, p = random_structured(seed)
+    say("case random", seed, "m", g.m, "n", g.n, "nnz", g.nnz, p)
+    df = device_build(g.rowptr, g.col, g.val, p)
+    f = assert_same_format(df, host_build(g.rowptr, g.col, g.val, p), f"seed {seed}")
+    if p["window"] == 16 and g.n > 0:
+        pd, ph = trspmm.Plan.from_format(df, g.m, g.n), trspmm.Plan.from_format(f, g.m, g.n)
+        assert pd.stats() == ph.stats()
+        B = torch.from_numpy(graphs.dense_operand(g.n, 32, seed=seed)).cuda()
+        assert torch.equal(pd.spmm(B), ph.spmm(B))
