@@ -232,3 +232,20 @@ def test_dformat_plan_full_size_rmat():
     hf = df.download()
     compare_spmm(df, hf, g.m, g.n, 128, {}, "rmat20 spmm")
     compare_sddmm(df, hf, g.m, g.n, 128, {}, "rmat20 sddmm")
+
+
+def test_dformat_plan_outlives_its_format():
+    """A plan keeps nothing of the device format it was made from: freed format, same outputs."""
+    g = graphs.sbm(communities=512, seed=8, val_seed=9)
+    df = trspmm.build_format_device(*dev_tensors(g))
+    keep = trspmm.Plan.from_format(df.download(), g.m, g.n)
+    plan = trspmm.Plan.from_format(df, g.m, g.n)
+    splan = trspmm.Plan.for_sddmm(df, g.m, g.n)
+    del df
+    torch.cuda.synchronize()
+    Bh = graphs.dense_operand(g.n, 64, seed=3)
+    assert np.array_equal(run_spmm(plan, Bh), run_spmm(keep, Bh))
+    Xh, Yh = graphs.dense_operand(g.m, 64, seed=4), graphs.dense_operand(g.n, 64, seed=5)
+    S = run_sddmm(splan, Xh, Yh)
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col[: int(g.rowptr[g.m])], Xh, Yh)
+    assert np.max(np.abs(S - R)) <= (1e-5 * np.sqrt(64) * 4 + 1e-6) * max(1.0, float(np.max(np.abs(R))))
