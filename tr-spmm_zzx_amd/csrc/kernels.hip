@@ -1254,9 +1254,14 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     const int gm = p.ntasks <= 0 ? 0 : gx > 0 ? (residual_grid(p, gpw) + kXcds - 1) / kXcds * kXcds : residual_grid(p, gpw);
     if (gm + gx == 0) return;
     dim3 grid(gm + gx, passes);
-    // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 2 for
-    // groups of >= 16 lanes (measured on R-MAT 2^20: K=128 1.12 ms vs 1.24 ms with 8, K=256
-    // 2.23 vs 2.51; K=32 0.54 ms with 8 vs 1.07 with 2)
+    // entries per batch: 8 for narrow groups (K <= 64: short gathers, many in flight pay), 4 for
+    // groups of >= 16 lanes (same-box A/B on R-MAT 2^20 with the staged stream and staged hot
+    // rows, 2 / 3 / 4 / 6 / 8 entries: K=128 0.687 / 0.631 / 0.612 / 0.611 / 0.616 ms, K=256
+    // 1.416 / 1.298 / 1.265 / 1.261 / 1.269, K=96 0.610 / - / 0.526 / - / 0.536; grid+hubs K=128
+    // 1.142 / - / 1.145 / - / 1.142; before the staged stream 2 had measured best: K=128 1.12 ms
+    // vs 1.24 with 8; K=32 0.54 ms with 8 vs 1.07 with 2); 16 for 4-lane groups of 16-byte loads
+    // (K = 32: R-MAT 0.311 -> 0.303 ms, grid+hubs 0.393 -> 0.383; 8-lane groups at K = 64 gain
+    // 0.6% on R-MAT and lose 2% on grid+hubs with 16, and keep 8)
     // pipelined stream for narrow groups with long tasks (same-box A/B: R-MAT K=32/64
     // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks, 4 lanes) +6%), and for 8-lane groups
     // whatever the task length (grid+hubs K=64 0.620 -> 0.582 ms, K=8 0.251 -> 0.238)
@@ -1291,7 +1296,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
-    constexpr int U = L >= 16 ? 2 : 8;                                                                    \
+    constexpr int U = L >= 16 ? 4 : (L == 4 && VEC == 8) ? 16 : 8;                                       \
     if constexpr (L <= 8) {                                                                               \
       if (pf) { TRS_TASKS_NT(L, U, true, false) } else { TRS_TASKS_NT(L, U, false, false) }               \
     } else if constexpr (L == 16) {                                                                       \
