@@ -1274,9 +1274,10 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     const bool ls = p.task_max <= kStageMax && p.stage >= 0 && (x.ntasks <= 0 || x.task_max <= kStageMax);
     // occupancy: lane groups of <= 8 lanes (K <= 64) run 8 entries per batch and are held to 2 waves
     // per SIMD (same-box A/B at 7/6/5/4/3/2 waves: grid+hubs K=32 0.426 ... 0.395 / 0.389 ms,
-    // R-MAT K=32 0.495 -> 0.420, K=64 0.579 -> 0.519, K=16 0.456 -> 0.400); wider groups run 2
-    // entries per batch and are not capped (R-MAT K=128 at 5 / 4 / 3 waves: 0.970 / 0.985 / 1.147
-    // ms; K=256 at 8 / 3 waves: 2.24 / 3.49)
+    // R-MAT K=32 0.495 -> 0.420, K=64 0.579 -> 0.519, K=16 0.456 -> 0.400); wider groups are not
+    // capped (R-MAT K=128 with 2 entries per batch at 5 / 4 / 3 waves: 0.970 / 0.985 / 1.147 ms,
+    // K=256 at 8 / 3 waves: 2.24 / 3.49; with 4 entries per batch, capped at 3 or 4 waves: slower
+    // than uncapped at K = 128 and 256)
     // (2-byte loads, used for K <= 8 and odd widths, stay uncapped: R-MAT K=8 0.293 ms uncapped,
     // 0.326 at 2 waves)
     // (4-byte loads in 8-lane groups, K = 10 and 14: 4 waves; R-MAT K=10 0.358 ms uncapped, 0.346
