@@ -546,7 +546,10 @@ __device__ __forceinline__ void spmm_tasks_run(const DevicePlan& P, int block, i
 // its XCD (block mod kXcds).  One launch instead of two lets the split part start while the main
 // part's last workgroups finish (same-box A/B on R-MAT 2^20: K = 128 0.706 -> 0.689 ms, K = 256
 // 1.464 -> 1.420; the two parts' workgroups interleaved instead: 0.695 / 1.432, split part first
-// 0.695 / 1.443).  Without a split part, Px is unused and gm is the grid.
+// 0.695 / 1.443; with 4 entries per batch, interleaved in chunks of kXcds workgroups: K = 128
+// 0.614 -> 0.642 ms, K = 256 1.266 -> 1.290, K = 32 0.298 -> 0.316 -- the split part's per-XCD
+// column classes keep their L2 hits only while the main part's gathers do not share the L2s).
+// Without a split part, Px is unused and gm is the grid.
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan Pm, DevicePlan Px, int gm,
                                                     const uint16_t* __restrict__ B, int64_t ldb, int K,
