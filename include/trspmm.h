@@ -266,7 +266,7 @@ typedef struct trs_plan_options {
                              call (workspace), and the task kernels read them there; the plan keeps
                              a second copy of its column ids with those columns renumbered.  Used
                              for K >= 128 (K % 8 == 0) on 16-byte aligned operands.  0 = automatic
-                             (16384 rows, at most n / 16, and only when they take >= 30% of the
+                             (32768 rows, at most n / 16, and only when they take >= 30% of the
                              gathers), > 0 = that many rows, -1 = off.  Never for plans with more
                              than 4 columns per entry (n > 4 nnz) */
   int32_t split_dispatch; /* 0: the residual task kernels run the main part and the XCD split part

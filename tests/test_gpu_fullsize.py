@@ -144,19 +144,19 @@ def test_fullsize_device_lowering_equals_host_lowering(name, K):
 
 
 def test_fullsize_staged_hot_rows_equal_unstaged():
-    """BASELINE config 2 (and 4 at K = 128): the plans stage 16,384 hot B (Y) rows by default; the
+    """BASELINE config 2 (and 4 at K = 128): the plans stage 32,768 hot B (Y) rows by default; the
     outputs are bitwise those of the same plans with staging off."""
     print("fullsize staged rows", flush=True)
     g, f = graph("rmat20")
     K = 128
     hot = trspmm.Plan.from_format(f, g.m, g.n)
     plain = trspmm.Plan.from_format(f, g.m, g.n, hot_rows=-1)
-    assert hot.stats()["hot_rows"] == 16384 and plain.stats()["hot_rows"] == 0
+    assert hot.stats()["hot_rows"] == 32768 and plain.stats()["hot_rows"] == 0
     B = torch.from_numpy(graphs.dense_operand(g.n, K, seed=2)).cuda()
     assert torch.equal(hot.spmm(B), plain.spmm(B))
     del hot, plain
     sh = trspmm.Plan.for_sddmm(f, g.m, g.n)
     sp = trspmm.Plan.for_sddmm(f, g.m, g.n, hot_rows=-1)
-    assert sh.stats()["hot_rows"] == 16384
+    assert sh.stats()["hot_rows"] == 32768
     X = torch.from_numpy(graphs.dense_operand(g.m, K, seed=4)).cuda()
     assert torch.equal(sh.sddmm(X, B), sp.sddmm(X, B))

@@ -352,7 +352,7 @@ def test_hot_selection_equals_brute_force(name, gen, want):
     f = trspmm.build_format(g.rowptr, g.col, g.val)
     s = trspmm.Plan.from_format(f, g.m, g.n, mfma_tc=False, mfma_sptc=False, xcd_split=-1,
                                 hot_rows=want).stats()
-    w = want if want > 0 else min(16384, g.n // 16)
+    w = want if want > 0 else min(32768, g.n // 16)
     nnz = int(g.rowptr[g.m])
     rows, entries = _brute_force_hot(g.col[:nnz], g.n, w)
     say("hot selection", name, s["hot_rows"], s["hot_entries"], rows, entries)

@@ -95,8 +95,11 @@ constexpr int64_t kWindowRowHardFactor = 4;
 // at most one in kHotColumnShare of all columns, and only when they take at least
 // kHotMinShare10 / 10 of the gathers.  R-MAT 2^20 (16,384 rows, 56.7% of the entries), K = 128:
 // 0.741 -> 0.699 ms per step plus ~0.007 ms for the copy; 4,096 rows 0.709, 65,536 rows 0.694
-// (+0.017 copy).  SBM 1M and the grid+hubs graph: 2.3% and 0.7% of the entries, not staged.
-constexpr int32_t kHotRows = 16384;
+// (+0.017 copy).  With 4 entries per batch in the task kernel, same box, twice each, 16,384 /
+// 32,768 / 65,536 rows: SpMM K = 128 0.615 / 0.609-0.612 / 0.612-0.613 ms, K = 256 1.265 / 1.267
+// / 1.271, SDDMM K = 128 0.707 / 0.697 / 0.699, K = 256 1.459 / 1.461 / 1.465.  SBM 1M and the
+// grid+hubs graph: 2.3% and 0.7% of the entries, not staged.
+constexpr int32_t kHotRows = 32768;
 constexpr int32_t kHotColumnShare = 16;
 constexpr int64_t kHotMinShare10 = 3;
 constexpr int64_t kHotMaxColumnsPerEntry = 4;
