@@ -1585,11 +1585,24 @@ __global__ __launch_bounds__(256) void k_place_entries(const PlaceEntries a) {
 }
 
 // Column histogram for the hot-row choice (global atomics: plan creation only).
+// Workgroup b counts into copy b % copies of the histogram (copies of n counts each), so that the
+// atomics on a hot column spread over that many addresses (R-MAT 2^20's hottest columns take tens
+// of thousands of entries each: 4.0 ms with one copy).
 __global__ __launch_bounds__(256) void k_count_columns(const int32_t* __restrict__ col, int64_t total, int32_t n,
-                                                       int32_t* __restrict__ counts) {
+                                                       int32_t* __restrict__ counts, int copies) {
+  int32_t* h = counts + (int64_t)(blockIdx.x % copies) * n;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int32_t c = col[e];
-    if (c >= 0 && c < n) atomicAdd(&counts[c], 1);
+    if (c >= 0 && c < n) atomicAdd(&h[c], 1);
+  }
+}
+
+// counts[c] = sum of the copies' counts of column c (copy 0 is counts itself).
+__global__ __launch_bounds__(256) void k_sum_copies(int32_t* __restrict__ counts, int32_t n, int copies) {
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < n; c += (int64_t)gridDim.x * 256) {
+    int32_t s = 0;
+    for (int k = 0; k < copies; ++k) s += counts[(int64_t)k * n + c];
+    counts[c] = s;
   }
 }
 
@@ -1625,12 +1638,16 @@ __global__ __launch_bounds__(256) void k_check_columns(const int32_t* __restrict
   }
 }
 
-// one wave per candidate row
+// One wave per chunk of a candidate row (long rows are cut into chunks, so that a hub row does not
+// hold one wave for its whole length).  Columns are flagged with relaxed byte stores of 1 (many
+// chunks flag the same hot columns; a store does not wait on the ones before it, as an atomic OR
+// to the same words did: 5.5 ms for R-MAT 2^20's 20M candidate entries).
 __global__ __launch_bounds__(256) void k_split_stats(const int32_t* __restrict__ col, const int32_t* __restrict__ start,
-                                                     const int32_t* __restrict__ len, int32_t rows,
-                                                     int32_t* __restrict__ cnt, uint32_t* __restrict__ seen) {
+                                                     const int32_t* __restrict__ len, const int32_t* __restrict__ row,
+                                                     int32_t chunks, int32_t* __restrict__ cnt,
+                                                     uint8_t* __restrict__ seen) {
   const int32_t i = (int32_t)(blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (i >= rows) return;
+  if (i >= chunks) return;
   const int l = threadIdx.x & 63;
   const int32_t* c = col + start[i];
   const int32_t n = len[i];
@@ -1640,21 +1657,22 @@ __global__ __launch_bounds__(256) void k_split_stats(const int32_t* __restrict__
     const int x = xcd_of_column(v);
 #pragma unroll
     for (int y = 0; y < kXcds; ++y) k[y] += x == y;
-    if (seen) atomicOr(&seen[(uint32_t)v >> 5], 1u << (v & 31));
+    if (seen) __hip_atomic_store(seen + v, (uint8_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #pragma unroll
   for (int y = 0; y < kXcds; ++y) {
     int32_t v = k[y];
     for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d);
-    if (l == 0) cnt[(int64_t)i * kXcds + y] = v;
+    if (l == 0 && v) atomicAdd(&cnt[(int64_t)row[i] * kXcds + y], v);
   }
 }
 
-__global__ __launch_bounds__(256) void k_popcount(const uint32_t* __restrict__ words, int64_t nwords,
-                                                  unsigned long long* __restrict__ out) {
+// *out += nonzero bytes of flags[0, n) (each 0 or 1), read as 32-bit words (n padded to 4 bytes).
+__global__ __launch_bounds__(256) void k_count_flags(const uint32_t* __restrict__ words, int64_t nwords,
+                                                     unsigned long long* __restrict__ out) {
   unsigned long long s = 0;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nwords; i += (int64_t)gridDim.x * 256)
-    s += __popc(words[i]);
+    s += __popc(words[i] & 0x01010101u);
   for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d);
   if ((threadIdx.x & 63) == 0 && s) atomicAdd(out, s);
 }
@@ -1756,9 +1774,12 @@ static unsigned stride_grid(int64_t total) {
   return (unsigned)(b < 8192 ? (b > 0 ? b : 1) : 8192);
 }
 
-hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream) {
-  if (total <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_count_columns, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, counts);
+hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, int copies,
+                                hipStream_t stream) {
+  if (total <= 0 || n <= 0) return hipSuccess;
+  if (copies < 1) copies = 1;
+  hipLaunchKernelGGL(k_count_columns, dim3(stride_grid(total)), dim3(256), 0, stream, col, total, n, counts, copies);
+  if (copies > 1) hipLaunchKernelGGL(k_sum_copies, dim3(stride_grid(n)), dim3(256), 0, stream, counts, n, copies);
   return hipGetLastError();
 }
 
@@ -1783,17 +1804,19 @@ hipError_t launch_check_columns(const int32_t* col, int64_t total, int32_t n, un
   return hipGetLastError();
 }
 
-hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, int32_t rows, int32_t* cnt,
-                              uint32_t* seen, hipStream_t stream) {
-  if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_split_stats, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, col, start, len, rows, cnt,
-                     seen);
+hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, const int32_t* row,
+                              int32_t chunks, int32_t* cnt, uint8_t* seen, hipStream_t stream) {
+  if (chunks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_split_stats, dim3((unsigned)((chunks + 3) / 4)), dim3(256), 0, stream, col, start, len, row,
+                     chunks, cnt, seen);
   return hipGetLastError();
 }
 
-hipError_t launch_popcount(const uint32_t* words, int64_t nwords, unsigned long long* out, hipStream_t stream) {
+hipError_t launch_count_flags(const uint8_t* flags, int64_t n, unsigned long long* out, hipStream_t stream) {
+  const int64_t nwords = (n + 3) / 4;
   if (nwords <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_popcount, dim3(stride_grid(nwords)), dim3(256), 0, stream, words, nwords, out);
+  hipLaunchKernelGGL(k_count_flags, dim3(stride_grid(nwords)), dim3(256), 0, stream,
+                     reinterpret_cast<const uint32_t*>(flags), nwords, out);
   return hipGetLastError();
 }
 

@@ -131,9 +131,11 @@ inline int64_t hot_buffer_bytes(const DevicePlan& p, int K) {
   if (p.nhot <= 0 || K < kHotMinK || K % 8 != 0) return 0;
   return (int64_t)p.nhot * K * 2;
 }
-// Column histogram of col[0, total) into counts[n] (zeroed by the caller; ids outside [0, n) are
-// skipped), and the renumbering hot_col[e] = rank[col[e]] >= 0 ? ~rank[col[e]] : col[e].
-hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, hipStream_t stream);
+// Column histogram of col[0, total) into counts[n] (ids outside [0, n) are skipped), counted in
+// `copies` histograms counts[k * n .. (k + 1) * n) (all zeroed by the caller) and summed into the
+// first; and the renumbering hot_col[e] = rank[col[e]] >= 0 ? ~rank[col[e]] : col[e].
+hipError_t launch_count_columns(const int32_t* col, int64_t total, int32_t n, int32_t* counts, int copies,
+                                hipStream_t stream);
 hipError_t launch_renumber_hot(const int32_t* col, int64_t total, int32_t n, const int32_t* rank, int32_t* hot_col,
                                hipStream_t stream);
 // counts[col[e]] -= 1 for the residual entries e of the nmwin MFMA windows' rows (rowptr [m + 1]):
@@ -187,13 +189,14 @@ hipError_t launch_place_entries(const PlaceEntries& a, hipStream_t stream);
 // *first_bad (the caller sets it to ~0ull) = the lowest index e with col[e] outside [0, n).
 hipError_t launch_check_columns(const int32_t* col, int64_t total, int32_t n, unsigned long long* first_bad,
                                 hipStream_t stream);
-// For split-row candidate i (entries col[start[i] .. start[i] + len[i])): cnt[i * kXcds + x] =
-// its entries of XCD class x (xcd_of_column); with seen (n bits, zeroed by the caller) also the
-// candidates' columns marked in it.
-hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, int32_t rows,
-                              int32_t* cnt, uint32_t* seen, hipStream_t stream);
-// *out += set bits of words[0, nwords) (*out zeroed by the caller).
-hipError_t launch_popcount(const uint32_t* words, int64_t nwords, unsigned long long* out, hipStream_t stream);
+// Chunk i of the split-row candidates, entries col[start[i] .. start[i] + len[i]) of candidate
+// row[i]: cnt[row[i] * kXcds + x] += its entries of XCD class x (xcd_of_column; cnt zeroed by the
+// caller); with seen (n bytes, zeroed by the caller, 4-byte padded) seen[c] = 1 for its columns.
+hipError_t launch_split_stats(const int32_t* col, const int32_t* start, const int32_t* len, const int32_t* row,
+                              int32_t chunks, int32_t* cnt, uint8_t* seen, hipStream_t stream);
+// *out += the nonzero bytes of flags[0, n) (values 0 or 1, n padded to 4 bytes; *out zeroed by
+// the caller).
+hipError_t launch_count_flags(const uint8_t* flags, int64_t n, unsigned long long* out, hipStream_t stream);
 // 2:4 group tiles of a window-16 format (tiles of four groups per window, block_online.cpp:796-841):
 // pass[t] = 1 when the stored values of tile t's groups (s_pos >= 0, 32 per group) are at least
 // min_fill * 256, the fill rule of the host lowering.

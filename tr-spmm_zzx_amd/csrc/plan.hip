@@ -103,6 +103,10 @@ constexpr int32_t kHotRows = 32768;
 constexpr int32_t kHotColumnShare = 16;
 constexpr int64_t kHotMinShare10 = 3;
 constexpr int64_t kHotMaxColumnsPerEntry = 4;
+// The column counts are taken in up to kCountCopies histograms (workgroup b into copy b mod
+// copies), at most kCountCopyBytes in all, and summed.
+constexpr int64_t kCountCopies = 8;
+constexpr int64_t kCountCopyBytes = 64ll << 20;
 
 // Host threads for plan lowering (std::thread: this object does not use an OpenMP runtime).
 int lowering_threads() {
@@ -811,14 +815,17 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
 
   // split part: per XCD, pieces of long sub-rows and runs of the others, longest first
   if (J > 0) {
-    std::vector<std::vector<int32_t>> piece_slots((size_t)J);
+    // sub-row j cut into pieces: their slots are pfirst[j] .. pfirst[j] + pn[j] (consecutive)
+    std::vector<int32_t> pfirst((size_t)J, 0), pn((size_t)J, 0);
     for (int y = 0; y < trs::kXcds; ++y) {
       T.xq[y] = (int32_t)T.xtasks.size();
       int32_t j = P.xfirst[y];
       while (j < P.xfirst[y + 1]) {
         const int32_t d = P.xrowptr[j + 1] - P.xrowptr[j];
         if (d > piece_max) {
-          cut_pieces(j, P.xrowptr[j], P.xrowptr[j + 1], T.xtasks, &piece_slots[j]);
+          pfirst[j] = T.slots;
+          cut_pieces(j, P.xrowptr[j], P.xrowptr[j + 1], T.xtasks, nullptr);
+          pn[j] = T.slots - pfirst[j];
           ++j;
           continue;
         }
@@ -830,21 +837,40 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
     }
     T.xq[trs::kXcds] = (int32_t)T.xtasks.size();
     if (with_fixup) {
-      // a split row's slots in XCD order: sub-row j's own slot, or its pieces' slots
-      std::vector<int32_t> first((size_t)m, -1);
-      std::vector<std::vector<int32_t>> rs;
-      for (int32_t jj = 0; jj < J; ++jj) {
-        const int32_t row = P.sub_row[jj];
-        if (first[row] < 0) {
-          first[row] = (int32_t)rs.size();
-          rs.emplace_back();
+      // a split row's slots in XCD order: sub-row j's own slot, or its pieces' slots.  Sub-rows are
+      // numbered XCD by XCD, split rows in order within each (place_entries), and split row i has
+      // a sub-row of XCD y exactly where P.cursor[i * kXcds + y] >= 0; the split rows are in row
+      // order, and so are their fixups
+      const size_t ns = P.split_rows.size();
+      std::vector<int32_t> nsl(ns + 1, 0);
+      int32_t j = 0;
+      for (int y = 0; y < trs::kXcds; ++y)
+        for (size_t i = 0; i < ns; ++i)
+          if (P.cursor[i * trs::kXcds + y] >= 0) {
+            nsl[i] += pn[(size_t)j] > 0 ? pn[(size_t)j] : 1;
+            ++j;
+          }
+      std::vector<int32_t> sbeg(ns + 1, 0);
+      for (size_t i = 0; i < ns; ++i) sbeg[i + 1] = sbeg[i] + nsl[i];
+      std::vector<int32_t> flat((size_t)sbeg[ns]), fill(sbeg.begin(), sbeg.end() - 1);
+      j = 0;
+      for (int y = 0; y < trs::kXcds; ++y)
+        for (size_t i = 0; i < ns; ++i) {
+          if (P.cursor[i * trs::kXcds + y] < 0) continue;
+          if (pn[(size_t)j] > 0)
+            for (int32_t k = 0; k < pn[(size_t)j]; ++k) flat[(size_t)fill[i]++] = pfirst[(size_t)j] + k;
+          else
+            flat[(size_t)fill[i]++] = j;
+          ++j;
         }
-        auto& v = rs[first[row]];
-        if (piece_slots[jj].empty()) v.push_back(jj);
-        else v.insert(v.end(), piece_slots[jj].begin(), piece_slots[jj].end());
+      T.slot_list.reserve(T.slot_list.size() + flat.size());
+      for (size_t i = 0; i < ns; ++i) {
+        const int32_t cntv = nsl[i];
+        (cntv > trs::kWideFixupSlots ? T.wfix : T.fix)
+            .push_back({P.split_rows[i], (int32_t)T.slot_list.size(), cntv, 0});
+        T.slot_list.insert(T.slot_list.end(), flat.begin() + sbeg[i], flat.begin() + sbeg[i + 1]);
+        ++T.split_rows;
       }
-      for (int32_t q = 0; q < m; ++q)
-        if (first[q] >= 0) add_fixup(q, rs[first[q]]);
     }
   }
   for (const trs::Task& t : T.tasks) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
@@ -918,20 +944,30 @@ Status split_stats_device(const int32_t* d_col, const int32_t* col_rowptr, const
                           const std::vector<int32_t>& split_rows, int32_t n, bool need_distinct, int64_t& total,
                           int64_t& distinct, std::vector<int32_t>& cnt) {
   const size_t ns = split_rows.size();
-  std::vector<int32_t> start(ns), len(ns);
+  // chunks of at most kChunk entries, one wave each
+  constexpr int32_t kChunk = 2048;
+  std::vector<int32_t> start, len, row;
+  start.reserve(ns);
+  len.reserve(ns);
+  row.reserve(ns);
   total = 0;
   for (size_t i = 0; i < ns; ++i) {
     const int32_t r = split_rows[i];
-    start[i] = col_rowptr[r];
-    len[i] = rowptr[r + 1] - rowptr[r];
-    total += len[i];
+    const int32_t b = col_rowptr[r], d = rowptr[r + 1] - rowptr[r];
+    for (int32_t q = 0; q < d; q += kChunk) {
+      start.push_back(b + q);
+      len.push_back(std::min(kChunk, d - q));
+      row.push_back((int32_t)i);
+    }
+    total += d;
   }
-  const size_t words = need_distinct ? ((size_t)n + 31) / 32 : 0;
+  const size_t flag_bytes = need_distinct ? ((size_t)n + 3) / 4 * 4 : 0;
   Blob tmp;
   const size_t o_start = tmp.add(start);
   const size_t o_len = tmp.add(len);
+  const size_t o_row = tmp.add(row);
   const size_t o_cnt = tmp.add_raw(nullptr, ns * trs::kXcds * 4);
-  const size_t o_pop = tmp.add_raw(nullptr, 8 + words * 4);   // the count, then the bitmap
+  const size_t o_pop = tmp.add_raw(nullptr, 8 + flag_bytes);   // the count, then the column flags
   void* dmem = nullptr;
   if (hipMalloc(&dmem, tmp.size()) != hipSuccess) {
     (void)hipGetLastError();
@@ -943,13 +979,15 @@ Status split_stats_device(const int32_t* d_col, const int32_t* col_rowptr, const
     return st;
   };
   unsigned long long* d_pop = reinterpret_cast<unsigned long long*>(base + o_pop);
-  uint32_t* d_seen = need_distinct ? reinterpret_cast<uint32_t*>(base + o_pop + 8) : nullptr;
+  uint8_t* d_seen = need_distinct ? base + o_pop + 8 : nullptr;
   int32_t* d_cnt = reinterpret_cast<int32_t*>(base + o_cnt);
-  if (!copy_pieces(tmp, dmem) || hipMemset(base + o_pop, 0, 8 + words * 4) != hipSuccess ||
+  if (!copy_pieces(tmp, dmem) || hipMemset(d_cnt, 0, ns * trs::kXcds * 4) != hipSuccess ||
+      hipMemset(base + o_pop, 0, 8 + flag_bytes) != hipSuccess ||
       trs::launch_split_stats(d_col, reinterpret_cast<const int32_t*>(base + o_start),
-                              reinterpret_cast<const int32_t*>(base + o_len), (int32_t)ns, d_cnt, d_seen,
+                              reinterpret_cast<const int32_t*>(base + o_len),
+                              reinterpret_cast<const int32_t*>(base + o_row), (int32_t)start.size(), d_cnt, d_seen,
                               nullptr) != hipSuccess ||
-      (need_distinct && trs::launch_popcount(d_seen, (int64_t)words, d_pop, nullptr) != hipSuccess))
+      (need_distinct && trs::launch_count_flags(d_seen, (int64_t)flag_bytes, d_pop, nullptr) != hipSuccess))
     return done(fail(TRS_EDEVICE, "device lowering: split statistics launch failed"));
   cnt.resize(ns * trs::kXcds);
   unsigned long long pop = 0;
@@ -1265,8 +1303,10 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   // the choice costs O(n) memory (a count per column, here and on the host): not for matrices with
   // far more columns than entries, whose columns are mostly unused anyway
   if (want <= 0 || (int64_t)n > kHotMaxColumnsPerEntry * total) return Status{};
+  // histogram copies against atomic contention on hot columns, within kCountCopyBytes
+  const int copies = (int)std::max<int64_t>(1, std::min<int64_t>(kCountCopies, kCountCopyBytes / ((int64_t)n * 4)));
   int32_t* counts = nullptr;
-  if (hipMalloc(&counts, (size_t)n * 4) != hipSuccess) {
+  if (hipMalloc(&counts, (size_t)n * 4 * copies) != hipSuccess) {
     (void)hipGetLastError();
     return fail(TRS_ENOMEM, "hot rows: hipMalloc of the column counts failed");
   }
@@ -1275,8 +1315,8 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
     return st;
   };
   std::vector<int32_t> cnt((size_t)n);
-  if (hipMemset(counts, 0, (size_t)n * 4) != hipSuccess ||
-      trs::launch_count_columns(d.col, total, n, counts, nullptr) != hipSuccess ||
+  if (hipMemset(counts, 0, (size_t)n * 4 * copies) != hipSuccess ||
+      trs::launch_count_columns(d.col, total, n, counts, copies, nullptr) != hipSuccess ||
       trs::launch_uncount_windows(d.mwin, d.nmwin, d.m, d.rowptr, d.col, n, counts, nullptr) != hipSuccess ||
       hipMemcpy(cnt.data(), counts, (size_t)n * 4, hipMemcpyDeviceToHost) != hipSuccess)
     return done(fail(TRS_EDEVICE, "hot rows: column count failed"));
@@ -1284,36 +1324,54 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   const int64_t task_entries = total - P->stats.window_csr_nnz;
   // The `want` first columns in the order (count desc, column asc) among those gathered at least
   // twice (a column gathered once gains nothing from a copy), found through a histogram of the
-  // counts: every column above the cut count t, then those at t in column order.  Counts from
-  // kCountCap on share the histogram's last bucket and are ordered by a sort of their own.
+  // counts: every column above the cut count t, then those at t in column order, each placed in
+  // its count's bucket in one pass over the columns (ascending, so each bucket is in column
+  // order).  Counts from kCountCap on share the histogram's last bucket and are ordered by a sort
+  // of their own.
   constexpr int32_t kCountCap = 1 << 16;
-  std::vector<int64_t> hc((size_t)kCountCap + 1, 0);
-  for (int32_t c = 0; c < n; ++c)
-    if (cnt[c] >= 2) hc[(size_t)std::min(cnt[c], kCountCap)]++;
+  std::vector<int32_t> hc((size_t)kCountCap + 1, 0);
+  for (int32_t c = 0; c < n; ++c) {
+    const int32_t v = cnt[c];
+    if (v >= 2) hc[(size_t)(v < kCountCap ? v : kCountCap)]++;
+  }
   int64_t taken = 0, hot_entries = 0;
   int32_t t = kCountCap;   // the lowest count taken in full is above t
   for (; t >= 2 && taken + hc[(size_t)t] <= want; --t) taken += hc[(size_t)t];
   auto before = [&](int32_t a, int32_t b) { return cnt[a] != cnt[b] ? cnt[a] > cnt[b] : a < b; };
   std::vector<int32_t> hot;
-  hot.reserve((size_t)std::min<int64_t>(want, n));
   if (t == kCountCap && hc[(size_t)kCountCap] > want) {
     // more capped columns than wanted: take them all and cut by the exact order
     for (int32_t c = 0; c < n; ++c)
       if (cnt[c] >= kCountCap) hot.push_back(c);
     std::nth_element(hot.begin(), hot.begin() + want, hot.end(), before);
     hot.resize((size_t)want);
+    std::sort(hot.begin(), hot.end(), before);
   } else {
-    int64_t at_t = t >= 2 ? want - taken : 0;   // columns of count t still taken, lowest ids first
+    const int32_t lo = std::max(t, 2);               // lowest count taken
+    int64_t at_t = t >= 2 ? want - taken : 0;        // columns of count t still taken, lowest ids first
+    const int64_t ncap = t < kCountCap ? hc[(size_t)kCountCap] : 0;
+    std::vector<int64_t> off((size_t)kCountCap, 0);  // next slot of each count below the cap
+    int64_t pos = ncap;
+    for (int32_t v = kCountCap - 1; v >= lo; --v) {
+      off[(size_t)v] = pos;
+      pos += v == t ? at_t : hc[(size_t)v];
+    }
+    hot.resize((size_t)pos);
+    std::vector<int32_t> capped;
+    capped.reserve((size_t)ncap);
     for (int32_t c = 0; c < n; ++c) {
-      const int32_t v = std::min(cnt[c], kCountCap);
-      if (v > t && v >= 2) hot.push_back(c);
-      else if (v == t && v >= 2 && at_t > 0) {
-        hot.push_back(c);
+      const int32_t v = cnt[c];
+      if (v < lo) continue;
+      if (v >= kCountCap) capped.push_back(c);
+      else if (v > t) hot[(size_t)off[(size_t)v]++] = c;
+      else if (at_t > 0) {   // v == t
+        hot[(size_t)off[(size_t)v]++] = c;
         --at_t;
       }
     }
+    std::sort(capped.begin(), capped.end(), before);
+    std::copy(capped.begin(), capped.end(), hot.begin());
   }
-  std::sort(hot.begin(), hot.end(), before);
   for (int32_t c : hot) hot_entries += cnt[c];
   if (hot.empty() || (opt.hot_rows == 0 && hot_entries * 10 < task_entries * kHotMinShare10)) return done(Status{});
   std::vector<int32_t> rank((size_t)n, -1);
