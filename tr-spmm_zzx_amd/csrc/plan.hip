@@ -707,6 +707,8 @@ struct Tasks {
 
 // Residual tasks a plan aims at when the automatic task size leaves fewer (small matrices).
 constexpr int64_t kMinTasks = 16384;
+// Rows per chunk of the main part's task packing (a multiple of 16: MFMA windows stay whole).
+constexpr int64_t kPackRows = 1 << 16;
 
 // Longest tasks first (a stable counting sort on the entry count, which never exceeds the piece
 // length): a workgroup's lane groups then carry tasks of similar length, so none idles while a
@@ -784,30 +786,47 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
     return r1;
   };
 
-  // main part (skip_split: without the split rows), longest tasks first
+  // main part (skip_split: without the split rows), longest tasks first.  Runs of rows are packed
+  // in chunks of kPackRows rows, in parallel (a run never crosses a chunk boundary, so the tasks do
+  // not depend on the thread count); rows longer than piece_max are collected and cut afterwards,
+  // in row order, which numbers their slots.
   const std::vector<int32_t>& rp = P.main_rowptr;
   auto build_main = [&](bool skip_split, std::vector<trs::Task>& outv) {
-    std::vector<trs::Task> pieces, packed;
+    const int64_t nchunks = ((int64_t)m + kPackRows - 1) / kPackRows;
+    std::vector<std::vector<trs::Task>> packed((size_t)nchunks);
+    std::vector<std::vector<int32_t>> longer((size_t)nchunks);
+    const int T = (int)std::min<int64_t>(lowering_threads(), nchunks);
+    parallel_parts(T, nchunks, 2, [&](int t) { return nchunks * t / T; }, [&](int64_t cb, int64_t ce, int) {
+      for (int64_t ch = cb; ch < ce; ++ch) {
+        const int32_t end = (int32_t)std::min<int64_t>(m, (ch + 1) * kPackRows);
+        int32_t r = (int32_t)(ch * kPackRows);
+        while (r < end) {
+          if (is_owned(r)) { r = std::min(end, (r / 16 + 1) * 16); continue; }
+          if (skip_split && P.split[r]) { ++r; continue; }
+          if (rp[r + 1] - rp[r] > piece_max) {
+            longer[(size_t)ch].push_back(r);
+            ++r;
+            continue;
+          }
+          const int32_t r1 = pack(rp, r, end, [&](int32_t q) { return is_owned(q) || (skip_split && P.split[q] != 0); });
+          packed[(size_t)ch].push_back({r, r1, rp[r], rp[r1]});
+          r = r1;
+        }
+      }
+    });
+    std::vector<trs::Task> pieces;
     std::vector<int32_t> sl;
-    int32_t r = 0;
-    while (r < m) {
-      if (is_owned(r)) { r = std::min(m, (r / 16 + 1) * 16); continue; }
-      if (skip_split && P.split[r]) { ++r; continue; }
-      const int32_t deg = rp[r + 1] - rp[r];
-      if (deg > piece_max) {
+    for (const auto& rows : longer)
+      for (int32_t r : rows) {
         sl.clear();
         cut_pieces(r, rp[r], rp[r + 1], pieces, &sl);
         add_fixup(r, sl);
-        ++r;
-        continue;
       }
-      const int32_t r1 = pack(rp, r, m, [&](int32_t q) { return is_owned(q) || (skip_split && P.split[q] != 0); });
-      packed.push_back({r, r1, rp[r], rp[r1]});
-      r = r1;
-    }
-    outv.reserve(pieces.size() + packed.size());
+    size_t np = pieces.size();
+    for (const auto& v : packed) np += v.size();
+    outv.reserve(np);
     outv.insert(outv.end(), pieces.begin(), pieces.end());
-    outv.insert(outv.end(), packed.begin(), packed.end());
+    for (const auto& v : packed) outv.insert(outv.end(), v.begin(), v.end());
     sort_longest_first(outv.begin(), outv.end());
   };
   build_main(true, T.tasks);
@@ -1330,10 +1349,16 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
   // of their own.
   constexpr int32_t kCountCap = 1 << 16;
   std::vector<int32_t> hc((size_t)kCountCap + 1, 0);
+  int64_t capped_entries = 0;
   for (int32_t c = 0; c < n; ++c) {
     const int32_t v = cnt[c];
+    if (v >= kCountCap) capped_entries += v;
     if (v >= 2) hc[(size_t)(v < kCountCap ? v : kCountCap)]++;
   }
+  // the automatic choice stages nothing when the chosen columns take too few of the gathers
+  auto too_few = [&](int64_t entries) {
+    return opt.hot_rows == 0 && entries * 10 < task_entries * kHotMinShare10;
+  };
   int64_t taken = 0, hot_entries = 0;
   int32_t t = kCountCap;   // the lowest count taken in full is above t
   for (; t >= 2 && taken + hc[(size_t)t] <= want; --t) taken += hc[(size_t)t];
@@ -1350,6 +1375,10 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
     const int32_t lo = std::max(t, 2);               // lowest count taken
     int64_t at_t = t >= 2 ? want - taken : 0;        // columns of count t still taken, lowest ids first
     const int64_t ncap = t < kCountCap ? hc[(size_t)kCountCap] : 0;
+    // their entries, from the histogram, before any column is placed
+    int64_t chosen = capped_entries + (t >= 2 ? at_t * t : 0);
+    for (int32_t v = std::max(t + 1, 2); v < kCountCap; ++v) chosen += (int64_t)v * hc[(size_t)v];
+    if (taken + (t >= 2 ? at_t : 0) == 0 || too_few(chosen)) return done(Status{});
     std::vector<int64_t> off((size_t)kCountCap, 0);  // next slot of each count below the cap
     int64_t pos = ncap;
     for (int32_t v = kCountCap - 1; v >= lo; --v) {
@@ -1373,7 +1402,7 @@ Status stage_hot_rows(trs_plan* P, int64_t total, const trs_plan_options& opt) {
     std::copy(capped.begin(), capped.end(), hot.begin());
   }
   for (int32_t c : hot) hot_entries += cnt[c];
-  if (hot.empty() || (opt.hot_rows == 0 && hot_entries * 10 < task_entries * kHotMinShare10)) return done(Status{});
+  if (hot.empty() || too_few(hot_entries)) return done(Status{});
   std::vector<int32_t> rank((size_t)n, -1);
   for (size_t i = 0; i < hot.size(); ++i) rank[hot[i]] = (int32_t)i;
   // renumbered ids with the 256-byte tail every entry array has (staged streams read whole
