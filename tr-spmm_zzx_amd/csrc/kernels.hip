@@ -439,9 +439,24 @@ __device__ __forceinline__ void stage_cols(const int32_t* __restrict__ col, int 
 }
 
 // Static LDS of k_spmm_tasks<.., LPG, .., LS>: the row-pointer slices and, when staged, the column
-// id and value slices (the arrays it declares; checked there).
+// id and value slices (TasksLds; checked there).
 constexpr size_t tasks_static_lds(int lpg, bool ls) {
   return (size_t)4 * (64 / lpg) * (kTaskRows + 1) * 4 + (ls ? (size_t)4 * (64 / lpg) * kStageSpan * 6 : 32);
+}
+
+// The task body's LDS, one block per (LPG, LS): the main and split parts of one launch run the body
+// with different batch sizes, and arrays declared in the body would be allocated once per batch
+// size (twice the LDS, half the occupancy).
+template <int LPG, bool LS>
+struct TasksLds {
+  int rp[4][64 / LPG][kTaskRows + 1];
+  alignas(16) int32_t col[LS ? 4 * (64 / LPG) * kStageSpan : 4];
+  alignas(16) uint16_t val[LS ? 4 * (64 / LPG) * kStageSpan : 8];
+};
+template <int LPG, bool LS>
+__device__ __forceinline__ TasksLds<LPG, LS>& tasks_lds() {
+  __shared__ TasksLds<LPG, LS> s;
+  return s;
 }
 
 // PF: pipelined stream (see Batch); the first batch's column ids and values are then loaded
@@ -457,12 +472,13 @@ __device__ __forceinline__ void spmm_tasks_run(const DevicePlan& P, int block, i
   constexpr bool NTS = (NT & kNtStores) != 0;
   // row pointers of each lane group's task, preloaded once so a row flush never waits on a
   // dependent global load (tasks carry at most kTaskRows rows)
-  __shared__ int s_rp[4][GPW][kTaskRows + 1];
-  __shared__ __align__(16) int32_t s_col[LS ? 4 * GPW * kStageSpan : 4];
-  __shared__ __align__(16) uint16_t s_val[LS ? 4 * GPW * kStageSpan : 8];
+  TasksLds<LPG, LS>& lds = tasks_lds<LPG, LS>();
+  auto& s_rp = lds.rp;
+  int32_t* s_col = lds.col;
+  uint16_t* s_val = lds.val;
   static_assert(!(LS && PF), "a staged stream is not pipelined");
   static_assert(!HOT || LS, "staged hot rows are read by the staged-stream kernel");
-  static_assert(sizeof(s_rp) + sizeof(s_col) + sizeof(s_val) == tasks_static_lds(LPG, LS),
+  static_assert(sizeof(TasksLds<LPG, LS>) == tasks_static_lds(LPG, LS),
                 "tasks_static_lds must describe this kernel's LDS (the occupancy cap depends on it)");
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -550,13 +566,21 @@ __device__ __forceinline__ void spmm_tasks_run(const DevicePlan& P, int block, i
 // 0.614 -> 0.642 ms, K = 256 1.266 -> 1.290, K = 32 0.298 -> 0.316 -- the split part's per-XCD
 // column classes keep their L2 hits only while the main part's gathers do not share the L2s).
 // Without a split part, Px is unused and gm is the grid.
+// The split part takes split_batch(...) entries per batch: 8 for 16-byte loads in groups of >= 16
+// lanes, where the main part takes 3 (its gathers miss the L2 about half the time and keep the
+// memory busy, while the split part's mostly hit it and wait on latency).  Same-box A/B on R-MAT
+// 2^20, main / split entries per batch, K = 128 and 256: 4 / 4 0.610 / 1.267 ms, 3 / 8 0.597 /
+// 1.244, 4 / 8 0.600 / 1.246, 2 / 8 0.597 / 1.253, 3 / 6 0.597 / 1.246, 3 / 12 0.609 / 1.265,
+// 3 / 16 0.644 / 1.354, 6 / 4 0.619 / 1.281; grid+hubs K = 128 1.144 / 1.151 (3 / 8) / 1.127 (3 / 12).
+constexpr int split_batch(int vec, int lpg, int u) { return vec == 8 && lpg >= 16 ? 8 : u; }
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan Pm, DevicePlan Px, int gm,
                                                     const uint16_t* __restrict__ B, int64_t ldb, int K,
                                                     float* __restrict__ C, int64_t ldc, float* __restrict__ partial) {
+  constexpr int XU = split_batch(VEC, LPG, U);
   const int b = (int)blockIdx.x;
   if (b < gm) spmm_tasks_run<VEC, LPG, U, NT, PF, LS, HOT>(Pm, b, gm, B, ldb, K, C, ldc, partial);
-  else spmm_tasks_run<VEC, LPG, U, NT, PF, LS, HOT>(Px, b - gm, (int)gridDim.x - gm, B, ldb, K, partial, K, partial);
+  else spmm_tasks_run<VEC, LPG, XU, NT, PF, LS, HOT>(Px, b - gm, (int)gridDim.x - gm, B, ldb, K, partial, K, partial);
 }
 
 // C[row] = sum of a split row's partial slots, in slot order (deterministic), 4 slots in flight.
@@ -1262,7 +1286,8 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // rows, 2 / 3 / 4 / 6 / 8 entries: K=128 0.687 / 0.631 / 0.612 / 0.611 / 0.616 ms, K=256
     // 1.416 / 1.298 / 1.265 / 1.261 / 1.269, K=96 0.610 / - / 0.526 / - / 0.536; grid+hubs K=128
     // 1.142 / - / 1.145 / - / 1.142; before the staged stream 2 had measured best: K=128 1.12 ms
-    // vs 1.24 with 8; K=32 0.54 ms with 8 vs 1.07 with 2); 16 for 4-lane groups of 16-byte loads
+    // vs 1.24 with 8; K=32 0.54 ms with 8 vs 1.07 with 2) -- 3 in the main part where the split
+    // part takes 8, with 16-byte loads (split_batch); 16 for 4-lane groups of 16-byte loads
     // (K = 32: R-MAT 0.311 -> 0.303 ms, grid+hubs 0.393 -> 0.383; 8-lane groups at K = 64 gain
     // 0.6% on R-MAT and lose 2% on grid+hubs with 16, and keep 8)
     // pipelined stream for narrow groups with long tasks (same-box A/B: R-MAT K=32/64
@@ -1300,7 +1325,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
-    constexpr int U = L >= 16 ? 4 : (L == 4 && VEC == 8) ? 16 : 8;                                       \
+    constexpr int U = L >= 16 ? (VEC == 8 ? 3 : 4) : (L == 4 && VEC == 8) ? 16 : 8;                     \
     if constexpr (L <= 8) {                                                                               \
       if (pf) { TRS_TASKS_NT(L, U, true, false) } else { TRS_TASKS_NT(L, U, false, false) }               \
     } else if constexpr (L == 16) {                                                                       \
