@@ -566,13 +566,20 @@ __device__ __forceinline__ void spmm_tasks_run(const DevicePlan& P, int block, i
 // 0.614 -> 0.642 ms, K = 256 1.266 -> 1.290, K = 32 0.298 -> 0.316 -- the split part's per-XCD
 // column classes keep their L2 hits only while the main part's gathers do not share the L2s).
 // Without a split part, Px is unused and gm is the grid.
-// The split part takes split_batch(...) entries per batch: 8 for 16-byte loads in groups of >= 16
+// The split part takes split_batch(...) entries per batch: with 16-byte loads, 8 in groups of >= 16
 // lanes, where the main part takes 3 (its gathers miss the L2 about half the time and keep the
-// memory busy, while the split part's mostly hit it and wait on latency).  Same-box A/B on R-MAT
-// 2^20, main / split entries per batch, K = 128 and 256: 4 / 4 0.610 / 1.267 ms, 3 / 8 0.597 /
-// 1.244, 4 / 8 0.600 / 1.246, 2 / 8 0.597 / 1.253, 3 / 6 0.597 / 1.246, 3 / 12 0.609 / 1.265,
-// 3 / 16 0.644 / 1.354, 6 / 4 0.619 / 1.281; grid+hubs K = 128 1.144 / 1.151 (3 / 8) / 1.127 (3 / 12).
-constexpr int split_batch(int vec, int lpg, int u) { return vec == 8 && lpg >= 16 ? 8 : u; }
+// memory busy, while the split part's mostly hit it and wait on latency), and 16 in groups of 8
+// and 4 lanes, where the main part takes 8 and 32.  Same-box A/B, main / split entries per batch:
+// R-MAT 2^20 K = 128 and 256: 4 / 4 0.610 / 1.267 ms, 3 / 8 0.597 / 1.244, 4 / 8 0.600 / 1.246,
+// 2 / 8 0.597 / 1.253, 3 / 6 0.597 / 1.246, 3 / 12 0.609 / 1.265, 3 / 16 0.644 / 1.354, 6 / 4
+// 0.619 / 1.281 (grid+hubs K = 128 1.144 / 1.151 (3 / 8) / 1.127 (3 / 12)); K = 64, R-MAT and
+// grid+hubs: 8 / 8 0.450 / 0.588, 8 / 16 0.441 / 0.589, 4 / 8 0.454 / 0.639, 16 / 8 0.450 /
+// 0.600, 12 / 16 0.447 / 0.593, 8 / 32 0.72 / 0.75; K = 32: 16 / 16 0.301 / 0.381, 32 / 16
+// 0.300 / 0.367, 32 / 32 0.312 / 0.366, 16 / 32 0.309 / 0.381, 8 / 16 0.302 / 0.389, 48 / 16
+// 0.435 / 0.450.
+constexpr int split_batch(int vec, int lpg, int u) {
+  return vec != 8 ? u : lpg >= 16 ? 8 : lpg == 8 || lpg == 4 ? 16 : u;
+}
 template <int VEC, int LPG, int U, int NT, bool PF, bool LS, bool HOT = false>
 __global__ __launch_bounds__(256) void k_spmm_tasks(DevicePlan Pm, DevicePlan Px, int gm,
                                                     const uint16_t* __restrict__ B, int64_t ldb, int K,
@@ -1286,10 +1293,11 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     // rows, 2 / 3 / 4 / 6 / 8 entries: K=128 0.687 / 0.631 / 0.612 / 0.611 / 0.616 ms, K=256
     // 1.416 / 1.298 / 1.265 / 1.261 / 1.269, K=96 0.610 / - / 0.526 / - / 0.536; grid+hubs K=128
     // 1.142 / - / 1.145 / - / 1.142; before the staged stream 2 had measured best: K=128 1.12 ms
-    // vs 1.24 with 8; K=32 0.54 ms with 8 vs 1.07 with 2) -- 3 in the main part where the split
-    // part takes 8, with 16-byte loads (split_batch); 16 for 4-lane groups of 16-byte loads
+    // vs 1.24 with 8; K=32 0.54 ms with 8 vs 1.07 with 2); 16 for 4-lane groups of 16-byte loads
     // (K = 32: R-MAT 0.311 -> 0.303 ms, grid+hubs 0.393 -> 0.383; 8-lane groups at K = 64 gain
-    // 0.6% on R-MAT and lose 2% on grid+hubs with 16, and keep 8)
+    // 0.6% on R-MAT and lose 2% on grid+hubs with 16, and keep 8).  With 16-byte loads the two
+    // parts then took batches of their own (split_batch): the main part 3 at >= 16 lanes, 8 at 8
+    // lanes and 32 at 4 lanes, the split part 8, 16 and 16
     // pipelined stream for narrow groups with long tasks (same-box A/B: R-MAT K=32/64
     // -9%/-12%; K=128 +8%, grid+hubs K=32 (32-entry tasks, 4 lanes) +6%), and for 8-lane groups
     // whatever the task length (grid+hubs K=64 0.620 -> 0.582 ms, K=8 0.251 -> 0.238)
@@ -1325,7 +1333,7 @@ hipError_t launch_spmm_vec(const DevicePlan& p, const uint16_t* B, int64_t ldb, 
     }
 #define TRS_TASKS(L)                                                                                      \
   case L: {                                                                                               \
-    constexpr int U = L >= 16 ? (VEC == 8 ? 3 : 4) : (L == 4 && VEC == 8) ? 16 : 8;                     \
+    constexpr int U = L >= 16 ? (VEC == 8 ? 3 : 4) : (L == 4 && VEC == 8) ? 32 : 8;                     \
     if constexpr (L <= 8) {                                                                               \
       if (pf) { TRS_TASKS_NT(L, U, true, false) } else { TRS_TASKS_NT(L, U, false, false) }               \
     } else if constexpr (L == 16) {                                                                       \
