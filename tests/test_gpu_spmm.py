@@ -391,11 +391,13 @@ def test_nonfinite_B_reaches_only_rows_that_use_it(K):
         assert not bad[:, 1:K - 1].any(), "non-finite values leaked into other features"
 
 
-@pytest.mark.parametrize("K", [32, 128])
+@pytest.mark.parametrize("K", [16, 32, 64, 96, 128])
 def test_xcd_column_split_matches_oracle_and_unsplit_rows(K):
     """Rows of >= xcd_split residual entries cut by 8 column ranges (one queue per XCD): against
     the oracle, deterministic from call to call, and every row left whole bitwise equal to the
-    plan without the split (same entries, same order)."""
+    plan without the split (same entries, same order).  The widths cover each lane-group width of
+    16-byte loads, whose split part takes batches of another size than the main part (8 lanes at
+    K = 64, 4 at K = 32, 16 at K = 96 and 128), and 8-byte loads (K = 16)."""
     say("xcd split", K)
     g = graphs.rmat(scale=14, edge_factor=16, seed=12)
     f = trspmm.build_format(g.rowptr, g.col, g.val)
