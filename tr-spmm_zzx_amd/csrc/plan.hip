@@ -233,7 +233,9 @@ void lower_tc_range(Lowering& L, const int32_t* t_rowoff, int64_t p_begin, int64
     const int32_t row0 = t_winrow[p];
     const bool mfma = to_mfma && row0 % 16 == 0 && row0 >= 0;
     for (int32_t s = s0; s < s1 && L.st.ok(); s += (mfma ? 2 : 1)) {
-      Lowering::Tile T;
+      // MFMA tiles are built in place (a tile is over 1 KB)
+      Lowering::Tile scratch;
+      Lowering::Tile& T = mfma ? L.tiles.emplace_back() : scratch;
       if (mfma) Lowering::tile_init(T, row0);
       const int nsub = mfma ? std::min(2, s1 - s) : 1;
       for (int h = 0; h < nsub; ++h) {
@@ -243,11 +245,15 @@ void lower_tc_range(Lowering& L, const int32_t* t_rowoff, int64_t p_begin, int64
         const int pop = __builtin_popcountll(lo) + __builtin_popcountll(hi);
         if (vi < 0 || vi + pop > nvals) {
           L.st = fail(TRS_EINVAL, "t_blockNew_offset / t_binary describe values beyond t_value");
+          if (mfma) L.tiles.pop_back();
           return;
         }
         for (int k = 0; k < 8 && mfma; ++k) {
           const int32_t c = t_col[(int64_t)sb * 8 + k];
-          if (c >= 0 && !L.check_col(c)) return;
+          if (c >= 0 && !L.check_col(c)) {
+            L.tiles.pop_back();
+            return;
+          }
           T.cols[h * 8 + k] = c;
         }
         for (int half = 0; half < 2; ++half) {
@@ -268,7 +274,6 @@ void lower_tc_range(Lowering& L, const int32_t* t_rowoff, int64_t p_begin, int64
           }
         }
       }
-      if (mfma) L.tiles.push_back(T);
     }
   }
 }
@@ -1559,7 +1564,7 @@ Status finalize(Lowering& L, const trs_plan_options& opt, trs_plan** out, const 
   parallel_tiles((int64_t)L.tiles.size(), [&](int64_t b, int64_t e, int) {
     for (int64_t t = b; t < e; ++t) {
       for (int k = 0; k < 16; ++k) tile_cols[t * 16 + k] = L.tiles[t].cols[k];
-      for (int i = 0; i < 256; ++i) tile_a[t * 256 + i] = trs::half_bits(L.tiles[t].a[i]);
+      trs::half_bits_n(L.tiles[t].a, &tile_a[t * 256], 256);   // F16C, the same bits as half_bits
     }
   });
 
