@@ -1392,7 +1392,7 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
   const bool hot_on = VEC == 8 && hot != nullptr && hot_buffer_bytes(p, K) > 0;
   const DevicePlan hp = hot_on ? hot_view(p, Y, ldy, K, hot, s) : p;
   // the split part writes its own buffer (then merged) where the workspace holds one
-  const bool merge_on = p.x_ntasks > 0 && xbuf != nullptr && merge_buffer_bytes(p, K) > 0;
+  bool merge_on = p.x_ntasks > 0 && xbuf != nullptr && merge_buffer_bytes(p, K) > 0;
   // feature passes of at most 128 features for 16-byte loads, each over all entries, the later
   // ones adding to the outputs: 256-byte slices of Y rows keep twice as many rows in an XCD's L2
   // as whole 512-byte rows, for one extra read and write of each output per pass (R-MAT 2^20
@@ -1481,7 +1481,15 @@ hipError_t launch_sddmm_vec(const DevicePlan& p, const uint16_t* X, int64_t ldx,
     };
     DevicePlan none = pp;
     none.ntasks = 0;
-    if (merge_on) {
+    if (lpg <= 8 && p.nnarrow_tasks > 0) {
+      // lane groups of <= 8 lanes: the unsplit layout of every row in pieces of S entries, every
+      // output written in place (no split part, nothing to merge)
+      DevicePlan v = pp;
+      v.tasks = p.narrow_tasks;
+      v.ntasks = p.nnarrow_tasks;
+      run_tasks(v, out, none, out);
+      merge_on = false;
+    } else if (merge_on) {
       // the split part into its own buffer, merged below
       DevicePlan v = split_view(pp);
       v.res_pos = nullptr;

@@ -91,6 +91,8 @@ struct DevicePlan {
   // kSddmmSplitMinK
   const Task* full_tasks = nullptr;
   int32_t nfull_tasks = 0;
+  const Task* narrow_tasks = nullptr;  // SDDMM: the unsplit layout in pieces of S entries, for lane
+  int32_t nnarrow_tasks = 0;           // groups of <= 8 lanes (none where no row is longer than S)
   int32_t xq[kXcds + 1] = {};
   // set in the view the launcher builds for the split part (see split_view): tasks come from the
   // per-XCD queues, workgroup i taking queue i mod kXcds; rows are sub-rows

@@ -701,6 +701,8 @@ struct Tasks {
   std::vector<trs::Task> xtasks;     // split part: queue x = xtasks [xq[x], xq[x + 1])
   int32_t xq[trs::kXcds + 1] = {};
   std::vector<trs::Task> full;       // SDDMM with a split part: the unsplit layout of every row
+  std::vector<trs::Task> narrow;     // SDDMM: the unsplit layout with pieces of S entries (lane
+                                     // groups of <= 8 lanes), where some row is longer than S
   std::vector<trs::Fixup> fix, wfix; // SpMM: {row, first index into slot_list, slots}
   std::vector<int32_t> slot_list;
   int32_t slots = 0;
@@ -791,9 +793,10 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
   if (with_fixup) T.slots = J;   // sub-row j sums into slot j; piece slots follow
 
   // equal pieces of at most piece_max entries of [b, e) of (sub-)row r
-  auto cut_pieces = [&](int32_t r, int32_t b, int32_t e, std::vector<trs::Task>& outv, std::vector<int32_t>* slots_of) {
+  auto cut_pieces = [&](int32_t r, int32_t b, int32_t e, std::vector<trs::Task>& outv, std::vector<int32_t>* slots_of,
+                        int32_t pmax) {
     const int32_t d = e - b;
-    const int np = (d + piece_max - 1) / piece_max;
+    const int np = (d + pmax - 1) / pmax;
     for (int q = 0; q < np; ++q) {
       const int32_t pb = b + (int32_t)((int64_t)d * q / np), pe = b + (int32_t)((int64_t)d * (q + 1) / np);
       outv.push_back({r, with_fixup ? ~T.slots : -1, pb, pe});
@@ -829,7 +832,7 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
   // not depend on the thread count); rows longer than piece_max are collected and cut afterwards,
   // in row order, which numbers their slots.
   const std::vector<int32_t>& rp = P.main_rowptr;
-  auto build_main = [&](bool skip_split, std::vector<trs::Task>& outv) {
+  auto build_main = [&](bool skip_split, std::vector<trs::Task>& outv, int32_t pmax) {
     const int64_t nchunks = ((int64_t)m + kPackRows - 1) / kPackRows;
     std::vector<std::vector<trs::Task>> packed((size_t)nchunks);
     std::vector<std::vector<int32_t>> longer((size_t)nchunks);
@@ -841,7 +844,7 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
         while (r < end) {
           if (is_owned(r)) { r = std::min(end, (r / 16 + 1) * 16); continue; }
           if (skip_split && P.split[r]) { ++r; continue; }
-          if (rp[r + 1] - rp[r] > piece_max) {
+          if (rp[r + 1] - rp[r] > pmax) {
             longer[(size_t)ch].push_back(r);
             ++r;
             continue;
@@ -857,7 +860,7 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
     for (const auto& rows : longer)
       for (int32_t r : rows) {
         sl.clear();
-        cut_pieces(r, rp[r], rp[r + 1], pieces, &sl);
+        cut_pieces(r, rp[r], rp[r + 1], pieces, &sl, pmax);
         add_fixup(r, sl);
       }
     size_t np = pieces.size();
@@ -867,8 +870,18 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
     for (const auto& v : packed) outv.insert(outv.end(), v.begin(), v.end());
     sort_longest_first(outv.begin(), outv.end());
   };
-  build_main(true, T.tasks);
-  if (!with_fixup && J > 0) build_main(false, T.full);   // SDDMM: no slots, no fixups to repeat
+  build_main(true, T.tasks, piece_max);
+  if (!with_fixup && J > 0) build_main(false, T.full, piece_max);   // SDDMM: no slots, no fixups to repeat
+  // SDDMM lane groups of <= 8 lanes walk the unsplit layout in pieces of S entries: with 8 lanes
+  // to a group a wave holds 8 tasks, and the long rows' pieces should not hold them for 256
+  // entries (same-box A/B on R-MAT 2^20, pieces of 128 against 256: K = 16 0.302 -> 0.288 ms, K =
+  // 32 0.359 -> 0.337; 16-lane groups lose with them, K = 64 0.443 -> 0.454, K = 96 0.651 ->
+  // 0.668, and keep the 256-entry pieces)
+  if (!with_fixup && opt.piece_nnz <= 0 && piece_max > S) {
+    bool longer = false;
+    for (int32_t r = 0; r < m && !longer; ++r) longer = !is_owned(r) && rp[r + 1] - rp[r] > S;
+    if (longer) build_main(false, T.narrow, S);
+  }
 
   // split part: per XCD, pieces of long sub-rows and runs of the others, longest first
   if (J > 0) {
@@ -881,7 +894,7 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
         const int32_t d = P.xrowptr[j + 1] - P.xrowptr[j];
         if (d > piece_max) {
           pfirst[j] = T.slots;
-          cut_pieces(j, P.xrowptr[j], P.xrowptr[j + 1], T.xtasks, nullptr);
+          cut_pieces(j, P.xrowptr[j], P.xrowptr[j + 1], T.xtasks, nullptr, piece_max);
           pn[j] = T.slots - pfirst[j];
           ++j;
           continue;
@@ -933,7 +946,8 @@ Tasks build_tasks(const Placement& P, const std::vector<int32_t>& rowptr, int32_
   for (const trs::Task& t : T.tasks) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
   for (const trs::Task& t : T.full) T.task_max = std::max(T.task_max, t.nz_end - t.nz_begin);
   for (const trs::Task& t : T.xtasks) T.xtask_max = std::max(T.xtask_max, t.nz_end - t.nz_begin);
-  if (T.tasks.size() + T.xtasks.size() + T.full.size() > (size_t)INT32_MAX / 64) T.st = fail(TRS_ERANGE, "too many tasks");
+  if (T.tasks.size() + T.xtasks.size() + T.full.size() + T.narrow.size() > (size_t)INT32_MAX / 64)
+    T.st = fail(TRS_ERANGE, "too many tasks");
   return T;
 }
 
@@ -1854,6 +1868,7 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   const size_t o_merge = blob.add(merge);
   const size_t o_srow = blob.add(PL.sub_row);
   const size_t o_full = blob.add(T.full);
+  const size_t o_narrow = blob.add(T.narrow);
   const size_t o_rpos = src ? blob.add_raw(nullptr, with_pos ? (size_t)nent * 4 : 0) : blob.add(res_pos);
   const size_t o_trow = blob.add(tile_row0);
   const size_t o_tcol = blob.add(tile_cols);
@@ -1900,6 +1915,8 @@ Status finalize_sddmm(Lowering& L, const trs_plan_options& opt, bool keep_order,
   d.x_entries = (int64_t)n_xpos;
   d.full_tasks = reinterpret_cast<const trs::Task*>(base + o_full);
   d.nfull_tasks = (int32_t)T.full.size();
+  d.narrow_tasks = reinterpret_cast<const trs::Task*>(base + o_narrow);
+  d.nnarrow_tasks = (int32_t)T.narrow.size();
   std::copy(T.xq, T.xq + trs::kXcds + 1, d.xq);
   d.x_task_max = T.xtask_max;
   d.res_pos = with_pos ? reinterpret_cast<const int32_t*>(base + o_rpos) : nullptr;
