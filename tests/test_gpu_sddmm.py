@@ -50,15 +50,18 @@ def test_sddmm_strided_operands(K, pad):
     assert np.max(np.abs(out.cpu().numpy() - R)) <= tol
 
 
-def test_sddmm_long_rows_and_empty_rows():
+@pytest.mark.parametrize("K", [8, 16, 32, 64])
+def test_sddmm_long_rows_and_empty_rows(K):
+    """A 30,000-entry row among empty and 4-entry ones: cut into pieces of 256 entries for 16-lane
+    groups (K = 64) and of S entries for narrower groups (K <= 32, the narrow task list)."""
     rng = np.random.default_rng(1)
     m, n = 48, 50000
     degs = np.array([30000 if r == 5 else (0 if r % 3 == 0 else 4) for r in range(m)])
     cols = np.concatenate([np.sort(rng.choice(n, size=d, replace=False)) for d in degs]).astype(np.int32)
     rowptr = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
     plan = trspmm.Plan.from_csr(rowptr, cols, np.ones(len(cols), np.float16), m, n)
-    Xh = graphs.dense_operand(m, 64, seed=1)
-    Yh = graphs.dense_operand(n, 64, seed=2)
+    Xh = graphs.dense_operand(m, K, seed=1)
+    Yh = graphs.dense_operand(n, K, seed=2)
     out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda())
     torch.cuda.synchronize()
     R = osp.csr_sddmm(rowptr, cols, Xh, Yh)
@@ -244,6 +247,28 @@ def test_sddmm_nonfinite_Y_reaches_only_entries_that_use_it():
     Yh[hub, 5] = np.float16(np.nan)
     out = plan.sddmm(torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()).cpu().numpy()
     assert np.array_equal(~np.isfinite(out), g.col[: g.nnz] == hub)
+
+
+@pytest.mark.parametrize("K", [8, 16, 32])
+def test_sddmm_narrow_task_list_equals_pieces_of_S(K):
+    """Lane groups of <= 8 lanes (K <= 32) walk the plan's narrow task list, the unsplit layout in
+    pieces of S entries: bitwise the outputs of a plan whose every piece is S entries long."""
+    print("sddmm narrow list", K, flush=True)
+    # large enough that S = 32 is not shrunk further (small matrices take pieces of 64 anyway)
+    g = graphs.rmat(scale=15, edge_factor=16, seed=8)
+    Xh = graphs.dense_operand(g.m, K, seed=3)
+    Yh = graphs.dense_operand(g.n, K, seed=4)
+    X, Y = torch.from_numpy(Xh).cuda(), torch.from_numpy(Yh).cuda()
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    narrow = trspmm.Plan.for_sddmm(f, g.m, g.n, task_nnz=32)
+    pieces = trspmm.Plan.for_sddmm(f, g.m, g.n, task_nnz=32, piece_nnz=32)
+    assert int(g.rowptr[g.m]) // 32 >= 16384
+    assert np.max(np.diff(g.rowptr[: g.m + 1])) > 256
+    a, b = narrow.sddmm(X, Y), pieces.sddmm(X, Y)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    R = osp.csr_sddmm(g.rowptr[: g.m + 1], g.col, Xh, Yh)
+    assert np.max(np.abs(a.cpu().numpy() - R)) <= (1e-5 * np.sqrt(K) * 4 + 1e-6) * max(1.0, np.max(np.abs(R)))
 
 
 def test_sddmm_xcd_column_split_is_bitwise_equal():
