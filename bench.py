@@ -46,6 +46,10 @@ def make_workload(cfg: int):
         return "grid2048_hubs_k32", graphs.grid_hubs(), 32, 7
     if cfg == 1:
         return "er4096_k64", graphs.erdos_renyi_gcn(), 64, 1
+    if cfg == 6:
+        # not a BASELINE configuration: config 3's windows with every intra-community edge and no
+        # other, so that every entry sits in a dense 16x16 tile on MFMA (the MFMA path on its own)
+        return "blockdiag1m_k256", graphs.sbm(p_in=1.0, inter_per_node=0), 256, 3
     raise SystemExit(f"unknown config {cfg}")
 
 
@@ -334,7 +338,8 @@ def load_traffic(kernel: str, workload: str):
 def roofline(bytes_k: int, impl: int, ms: float, kernel: str, names, kms, workload: str) -> dict:
     """Roofline object of the dominant kernel: `achieved` = its compulsory bytes per launch over
     its HIP-event duration, `impl_bytes` = what its data layout reads or writes on top (not counted
-    as achieved), `traffic` = measured HBM bytes per launch from the stored counter run named in
+    as achieved; negative where the layout reads less than the compulsory CSR bytes, as dense tiles
+    with 2 bytes per slot and one column id per 16 slots do), `traffic` = measured HBM bytes per launch from the stored counter run named in
     `traffic_source` (null where none is recorded)."""
     achieved = bytes_k / (ms * 1e-3) / 1e9
     traffic, source = load_traffic(kernel, workload)
@@ -352,7 +357,9 @@ def main():
     # clocks need tens of milliseconds of work to ramp up (SDDMM K=64: 0.592 ms per step after 5
     # warm-up steps, 0.499 after 200; R-MAT SpMM K=128 unchanged at 0.969)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2,
+                    help="BASELINE configuration 1-5 (2: the headline); 6: dense 16x16 blocks only (not a "
+                         "BASELINE configuration: the MFMA path on its own)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--k", type=int, default=0, help="override the configuration's feature width")
     ap.add_argument("--scramble", type=int, default=None, metavar="SEED",
