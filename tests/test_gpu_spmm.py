@@ -431,6 +431,22 @@ def test_feature_passes_with_split_rows(K):
     assert np.array_equal(C, run_plan(plan, Bh))
 
 
+@pytest.mark.parametrize("K", [64, 256])
+def test_dense_blocks_run_on_mfma_only(K):
+    """bench.py's configuration 6 at a smaller size: every intra-community edge of 16-node
+    communities aligned with the windows and no other edge, so every entry sits in a dense 16x16
+    tile on MFMA and the window kernel runs no residual row; against the oracle."""
+    say("dense blocks", K)
+    g = graphs.sbm(communities=4096, p_in=1.0, inter_per_node=0, seed=5, val_seed=6)
+    f = trspmm.build_format(g.rowptr, g.col, g.val)
+    plan = trspmm.Plan.from_format(f, g.m, g.n)
+    st = plan.stats()
+    nnz = int(g.rowptr[g.m])
+    assert nnz == 4096 * 16 * 15 and st["mfma_nnz"] == nnz and st["csr_nnz"] == 0 and st["mfma_tiles"] == 4096
+    Bh = dense_B(g.n, K, seed=7)
+    check(run_plan(plan, Bh), osp.csr_spmm(g.rowptr, g.col, g.val, Bh, m=g.m), f"dense blocks K={K}")
+
+
 def test_plan_stats_size_is_checked_with_a_real_plan():
     """trs_plan_stats_get on a device plan: a stats struct of another header's size (12 fields in
     the first one) gets TRS_EINVAL and nothing is written past it; the right size succeeds."""
